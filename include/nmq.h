@@ -1,0 +1,123 @@
+/*
+ * nmq.h -- C ABI of the MI355X (gfx950) GGUF quantized mat-vec library (libnmq.so).
+ *
+ * Plain pointers and sizes only.  Every device pointer is a HIP device address (a torch tensor's
+ * data_ptr() on ROCm).  `stream` is a hipStream_t passed as void* (torch.cuda.current_stream()
+ * .cuda_stream); NULL means the null stream.  No entry point allocates, frees or synchronises:
+ * launches are asynchronous on `stream` and may be captured in a HIP graph.
+ *
+ * Return value: 0 on success; a negative NMQ_ERR_* for a rejected argument (nothing launched); a
+ * positive hipError_t if the launch itself failed.  nmq_strerror() names either kind.
+ *
+ * Format ids are the GGML type ids (reference ggufengine/gguf.py:64-78).
+ */
+#ifndef NMQ_H
+#define NMQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NMQ_Q8_0 8     /* 32 values, 34 bytes: fp16 d, int8 qs[32]                             */
+#define NMQ_Q4_K 12    /* 256 values, 144 bytes: fp16 d, dmin, scales[12], qs[128]              */
+#define NMQ_Q6_K 14    /* 256 values, 210 bytes: ql[128], qh[64], int8 sc[16], fp16 d           */
+#define NMQ_IQ2_XXS 16 /* 256 values, 66 bytes: fp16 d, 8 x {u32 grid idx, u32 signs+scale}     */
+#define NMQ_TQ2_0 35   /* 256 values, 66 bytes: qs[64] (2-bit codes), fp16 d                    */
+
+#define NMQ_OK 0
+#define NMQ_ERR_FORMAT (-1) /* unknown or unsupported format id                                  */
+#define NMQ_ERR_SHAPE (-2)  /* n_in not a multiple of the block size, sizes <= 0 or too large      */
+#define NMQ_ERR_ARG (-3)    /* NULL pointer where one is required, bad count                       */
+#define NMQ_ERR_DEVICE (-4) /* no usable device / not a gfx950 device                             */
+
+/* Tokens handled by one launch of the mat-vec kernels; nmq_mv loops over larger counts. */
+#define NMQ_MAX_COLS 8
+
+/* ABI version of this header (bumped on incompatible changes). */
+int nmq_abi_version(void);
+
+/* Text for a return code of any entry point (static storage). */
+const char* nmq_strerror(int code);
+
+/* Values and bytes per block of a format; returns NMQ_OK or NMQ_ERR_FORMAT.
+ * Replaces the table lookups GGML_TYPES[...] (gguf.py:64-78), mmvq.FORMATE (mmvq.py:25) and
+ * cudakern.FORMATE (cudakern.py:42-49) for the five formats of this library. */
+int nmq_format_info(int fmt, int* block_values, int* block_bytes);
+
+/* Name of the current device's architecture (e.g. "gfx950") into buf; NMQ_OK or NMQ_ERR_DEVICE.
+ * Replaces the availability probe behind mmvq.verfuegbar / cudakern.verfuegbar
+ * (mmvq.py:792-810, cudakern.py:717-739): the kernels exist only for gfx950. */
+int nmq_device_arch(char* buf, int len);
+
+/*
+ * Two-stage int8 activation ("Eingang").  Replaces the `quant_q8` launch of mmvq.Eingang
+ * (mmvq.py:62-83, 825-843).  x: n values (fp32 if x_is_f32, else bf16), n % 32 == 0; several token
+ * rows may be passed back to back.  Per 32 values g:
+ *   xd[g] = max|x| / 127, xq = rint(x / xd), xq2 = clamp(rint((x - xq*xd) / (xd/254)), +-127),
+ *   xs[g] = sum of the 32 values.
+ */
+int nmq_quant_q8(const void* x, int x_is_f32, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
+                 void* stream);
+
+/*
+ * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of NMQ_MAX_COLS tokens).
+ * w: n_out rows of n_in values in GGUF block format, rows back to back.  Token c's two-stage input
+ * lies at xq + c*n_in, xq2 + c*n_in, xd + c*n_in/32, xs + c*n_in/32 (the layout of an Eingang of
+ * ncols rows).  y: fp32, token-major (ncols x n_out).
+ * Replaces the mvq_<fmt>_<nc> launches of mmvq.mv (mmvq.py:341-489, 852-865) and the mv/mm
+ * kernels of cudakern for one matrix (cudakern.py:482-555, 756-790).
+ * n_in % block_values == 0 (Q8_0: 32, others 256), 1 <= n_out, n_in <= 1<<20.
+ */
+int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
+           float* y, int n_out, int n_in, int ncols, void* stream);
+
+/*
+ * Expert-id-gathered mat-vec (MoE): for j < n_ids,
+ *   y[j][r] = W_{ids[j]}[r,:] . x_(j / x_group)
+ * Weights of expert e start at w + e*per_expert (per_expert >= 0, bytes), or, with per_expert < 0,
+ * at the address ((const int64_t*)w)[e] (a device table of expert addresses: VRAM slots or mapped
+ * pinned host memory).  ids: int64 on the device (read by the kernel, so a captured graph follows
+ * new ids without a host sync).  x_group = n_ids: one input shared by all experts (gate/up of one
+ * token); x_group = 1: every expert has its own input row (down); x_group = k: rows of k slots per
+ * token.  y: fp32 (n_ids x n_out).
+ * Replaces cudakern.mv with ids / adressen (cudakern.py:482-505, 756-774) as called by
+ * PackedExperts.matvec / matvec_je (models/common.py:462-475).
+ */
+int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_t per_expert,
+                   const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int x_group,
+                   float* y, int n_out, int n_in, void* stream);
+
+/*
+ * Diagnostic: the int32 sums the mat-vec kernels form, per 16 weights, for one token:
+ *   s1[r][g] = sum_{j<16} w_int(r, 16g+j) * xq[16g+j],  s2 likewise with xq2,
+ * where w_int is the format's integer weight (Q4_K nibble, Q6_K q-32, Q8_0 qs, TQ2_0 code-1,
+ * IQ2_XXS +-grid byte).  s1, s2: int32 (n_out x n_in/16).  Uses the same device decoders as
+ * nmq_mv; exists so the integer part can be checked bit-exactly.  No counterpart in the reference
+ * (its kernels keep these sums in registers, mmvq.py:385-396).
+ */
+int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2,
+                   int n_out, int n_in, void* stream);
+
+/*
+ * Unpack n_blocks blocks to bf16 values (uint16 bit patterns), the exact fp32 dequantisation of
+ * quant.py rounded to bf16.  Replaces mmvq.entpacken / aus_<fmt> (mmvq.py:496-534, 923-931) and
+ * the unpack step of the PackedLinear fallback (models/common.py:414-428).
+ */
+int nmq_dequant_bf16(int fmt, const void* w, uint16_t* out, int64_t n_blocks, void* stream);
+
+/* ---- host-side encoders (CPU, no device involved) -----------------------------------------------
+ * Write n values (n % block_values == 0) of fp32 weights into GGUF blocks at out
+ * (n / block_values * block_bytes bytes).  Return the number of bytes written, or a negative
+ * NMQ_ERR_*.  The reference ships no quantiser for Q4_K, Q6_K or IQ2_XXS; these are this library's
+ * own (the mat-vec is checked against the dequantisation of the same bytes, so the encoder only
+ * decides how realistic the weights are).  threads <= 0: all cores.
+ */
+int64_t nmq_encode(int fmt, const float* w, int64_t n, uint8_t* out, int threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NMQ_H */

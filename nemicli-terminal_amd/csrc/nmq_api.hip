@@ -1,0 +1,366 @@
+// C ABI of libnmq (include/nmq.h): argument checks, launch selection, and the small kernels that
+// are not mat-vecs (two-stage activation, integer-sum diagnostic, unpack to bf16).
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "nmq_mv_impl.hpp"
+
+namespace nmq {
+
+// ---- device properties (per device, cached) ---------------------------------------------------
+
+static std::mutex g_info_mu;
+static DeviceInfo g_info[64];
+static bool g_info_ok[64];
+
+DeviceInfo device_info() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceInfo{256, 64 * 1024};
+    std::lock_guard<std::mutex> lk(g_info_mu);
+    if (!g_info_ok[dev]) {
+        int cus = 256, lds = 64 * 1024;
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+        // static LDS of the kernels (IQ2 tables) comes on top of the dynamic part
+        lds = (lds > 64 * 1024 ? 64 * 1024 : lds) - 4096;
+        g_info[dev] = DeviceInfo{cus, lds};
+        g_info_ok[dev] = true;
+    }
+    return g_info[dev];
+}
+
+// ---- two-stage int8 activation (reference mmvq.py:59-83) ----------------------------------------
+// One lane per value, 32 lanes (half a wave) per group.  max|x| and the sum use the xor butterfly
+// over offsets 16, 8, 4, 2, 1 (never crossing the 32-lane half), in the order of mmvq.py:42-46.
+// d = max / 127 and the quotients are IEEE divisions (the library is built without fast-math);
+// the residual x - q*d is one fused multiply-add (the CPU oracle does the same).
+__global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ x, int f32, int8_t* __restrict__ xq,
+                                                        int8_t* __restrict__ xq2, float* __restrict__ xd,
+                                                        float* __restrict__ xs, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((i & ~(int64_t)31) >= n) return;  // whole 32-lane groups only (n % 32 == 0)
+    const float v = f32 ? ((const float*)x)[i] : __uint_as_float((u32)((const u16*)x)[i] << 16);
+    float a = fabsf(v);
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+    const float d = a / 127.0f;
+    int q = 0, q2 = 0;
+    if (d > 0.0f) {
+        q = (int)rintf(v / d);
+        const float r = fmaf(-(float)q, d, v);
+        q2 = (int)rintf(r / (d * FEIN));
+        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+    }
+    float s = v;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    xq[i] = (int8_t)q;
+    xq2[i] = (int8_t)q2;
+    if ((threadIdx.x & 31) == 0) {
+        xd[i >> 5] = d;
+        xs[i >> 5] = s;
+    }
+}
+
+// ---- diagnostic: per-16 integer sums, through the same unit decoders as mv_kernel ---------------
+template <int F>
+__global__ __launch_bounds__(256) void block_sums_kernel(const u8* __restrict__ w, const int8_t* __restrict__ xq,
+                                                          const int8_t* __restrict__ xq2, int32_t* __restrict__ s1,
+                                                          int32_t* __restrict__ s2, int n_out, int n_in) {
+    using FM = Fmt<F>;
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    fill_tables<F>(tab);
+    __syncthreads();
+    const int units = (n_in + 63) / 64, nblk = n_in / FM::BV;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)n_out * units) return;
+    const int row = (int)(idx / units), u = (int)(idx % units);
+    typename FM::Raw raw;
+    WUnit wu;
+    FM::load(w + (int64_t)row * nblk * FM::BB, u, nblk, raw);
+    FM::decode(raw, u, tab, wu);
+    XSlice x;
+    int g[4];
+    const int G = n_in / 16;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        int pos;
+        if (FM::STRIDED) {
+            const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+            pos = 256 * b + 128 * h + 32 * k + 16 * j;
+        } else {
+            pos = 64 * u + 16 * k;
+        }
+        g[k] = pos / 16;
+        const bool ok = pos < n_in;
+        const u32x4 a = ok ? *(const u32x4*)(xq + pos) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 b = ok ? *(const u32x4*)(xq2 + pos) : u32x4{0u, 0u, 0u, 0u};
+        x.q[4 * k] = a.x; x.q[4 * k + 1] = a.y; x.q[4 * k + 2] = a.z; x.q[4 * k + 3] = a.w;
+        x.q2[4 * k] = b.x; x.q2[4 * k + 1] = b.y; x.q2[4 * k + 2] = b.z; x.q2[4 * k + 3] = b.w;
+    }
+    int a1[4], a2[4];
+    unit_sums(wu.w, x, a1, a2);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (g[k] < G) {
+            s1[(int64_t)row * G + g[k]] = a1[k];
+            s2[(int64_t)row * G + g[k]] = a2[k];
+        }
+}
+
+// ---- unpack to bf16 (exact quant.py fp32 value, then round to nearest even) --------------------
+__device__ __forceinline__ u16 f2bf(float f) {
+    const u32 u = __float_as_uint(f);
+    return (u16)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+template <int F>
+__global__ __launch_bounds__(256) void dequant_bf16_kernel(const u8* __restrict__ w, u16* __restrict__ out,
+                                                            int64_t n_blocks) {
+#pragma clang fp contract(off)
+    using FM = Fmt<F>;
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    fill_tables<F>(tab);
+    __syncthreads();
+    // a "row" of one block; Q8_0 units span two blocks, so Q8_0 rows are two blocks (last may be one)
+    constexpr int BPU = FM::BV == 32 ? 2 : 1;  // blocks per row handled here
+    constexpr int UPR = FM::BV == 32 ? 1 : 4;  // units per row
+    const int64_t rows = (n_blocks + BPU - 1) / BPU;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * UPR) return;
+    const int64_t row = idx / UPR;
+    const int u = (int)(idx % UPR);
+    const int nblk = (int)((n_blocks - row * BPU) < BPU ? (n_blocks - row * BPU) : BPU);
+    typename FM::Raw raw;
+    WUnit wu;
+    FM::load(w + row * BPU * FM::BB, u, nblk, raw);
+    FM::decode(raw, u, tab, wu);
+    u16* o = out + row * BPU * FM::BV;
+    const int nvals = nblk * FM::BV;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        int pos;
+        if (FM::STRIDED) {
+            const int h = (u >> 1) & 1, j = u & 1;
+            pos = 128 * h + 32 * r + 16 * j;
+        } else {
+            pos = 64 * u + 16 * r;
+        }
+        if (pos >= nvals) continue;
+        const float sc = wu.ws[r];
+        const float mn = FM::HAS_MIN ? wu.wm[r >> 1] : 0.f;
+        u32 pk[8];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32 v = wu.w[4 * r + k];
+            float f[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float q = (float)(int8_t)(v >> (8 * e));
+                f[e] = FM::HAS_MIN ? (sc * q - mn) : sc * q;
+            }
+            pk[2 * k] = (u32)f2bf(f[0]) | ((u32)f2bf(f[1]) << 16);
+            pk[2 * k + 1] = (u32)f2bf(f[2]) | ((u32)f2bf(f[3]) << 16);
+        }
+        u32x4* dst = (u32x4*)(o + pos);
+        dst[0] = u32x4{pk[0], pk[1], pk[2], pk[3]};
+        dst[1] = u32x4{pk[4], pk[5], pk[6], pk[7]};
+    }
+}
+
+// ---- per-format launch tables -----------------------------------------------------------------
+template <int F>
+int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream);
+extern template int launch_mv<NMQ_Q8_0>(MvParams, int, int, hipStream_t);
+extern template int launch_mv<NMQ_Q4_K>(MvParams, int, int, hipStream_t);
+extern template int launch_mv<NMQ_Q6_K>(MvParams, int, int, hipStream_t);
+extern template int launch_mv<NMQ_IQ2_XXS>(MvParams, int, int, hipStream_t);
+extern template int launch_mv<NMQ_TQ2_0>(MvParams, int, int, hipStream_t);
+
+static int launch_any(int fmt, const MvParams& p, int nc, int n_mats, hipStream_t s) {
+    switch (fmt) {
+        case NMQ_Q8_0: return launch_mv<NMQ_Q8_0>(p, nc, n_mats, s);
+        case NMQ_Q4_K: return launch_mv<NMQ_Q4_K>(p, nc, n_mats, s);
+        case NMQ_Q6_K: return launch_mv<NMQ_Q6_K>(p, nc, n_mats, s);
+        case NMQ_IQ2_XXS: return launch_mv<NMQ_IQ2_XXS>(p, nc, n_mats, s);
+        case NMQ_TQ2_0: return launch_mv<NMQ_TQ2_0>(p, nc, n_mats, s);
+        default: return NMQ_ERR_FORMAT;
+    }
+}
+
+template <template <int> class K, typename... A>
+static int launch_fmt_kernel(int fmt, dim3 grid, hipStream_t s, A... a) {
+    switch (fmt) {
+        case NMQ_Q8_0: hipLaunchKernelGGL(K<NMQ_Q8_0>::fn, grid, dim3(256), 0, s, a...); break;
+        case NMQ_Q4_K: hipLaunchKernelGGL(K<NMQ_Q4_K>::fn, grid, dim3(256), 0, s, a...); break;
+        case NMQ_Q6_K: hipLaunchKernelGGL(K<NMQ_Q6_K>::fn, grid, dim3(256), 0, s, a...); break;
+        case NMQ_IQ2_XXS: hipLaunchKernelGGL(K<NMQ_IQ2_XXS>::fn, grid, dim3(256), 0, s, a...); break;
+        case NMQ_TQ2_0: hipLaunchKernelGGL(K<NMQ_TQ2_0>::fn, grid, dim3(256), 0, s, a...); break;
+        default: return NMQ_ERR_FORMAT;
+    }
+    return (int)hipGetLastError();
+}
+template <int F>
+struct SumsK {
+    static constexpr auto fn = block_sums_kernel<F>;
+};
+template <int F>
+struct DeqK {
+    static constexpr auto fn = dequant_bf16_kernel<F>;
+};
+
+}  // namespace nmq
+
+using namespace nmq;
+
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+extern "C" {
+
+int nmq_abi_version(void) { return 1; }
+
+const char* nmq_strerror(int code) {
+    switch (code) {
+        case NMQ_OK: return "ok";
+        case NMQ_ERR_FORMAT: return "nmq: unsupported block format";
+        case NMQ_ERR_SHAPE: return "nmq: bad shape (n_in must be a multiple of the block size; sizes in range)";
+        case NMQ_ERR_ARG: return "nmq: bad argument (NULL or misaligned pointer, bad count)";
+        case NMQ_ERR_DEVICE: return "nmq: no usable gfx950 device";
+        default: return code > 0 ? hipGetErrorString((hipError_t)code) : "nmq: unknown error";
+    }
+}
+
+int nmq_format_info(int fmt, int* block_values, int* block_bytes) {
+    int bv, bb;
+    switch (fmt) {
+        case NMQ_Q8_0: bv = 32; bb = 34; break;
+        case NMQ_Q4_K: bv = 256; bb = 144; break;
+        case NMQ_Q6_K: bv = 256; bb = 210; break;
+        case NMQ_IQ2_XXS: bv = 256; bb = 66; break;
+        case NMQ_TQ2_0: bv = 256; bb = 66; break;
+        default: return NMQ_ERR_FORMAT;
+    }
+    if (block_values) *block_values = bv;
+    if (block_bytes) *block_bytes = bb;
+    return NMQ_OK;
+}
+
+int nmq_device_arch(char* buf, int len) {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (!buf || len <= 0) return NMQ_ERR_ARG;
+    buf[0] = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) return NMQ_ERR_DEVICE;
+    snprintf(buf, (size_t)len, "%s", prop.gcnArchName);
+    return strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? NMQ_OK : NMQ_ERR_DEVICE;
+}
+
+int nmq_quant_q8(const void* x, int x_is_f32, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
+                 void* stream) {
+    if (!x || !xq || !xq2 || !xd || !xs) return NMQ_ERR_ARG;
+    if (n <= 0 || n % 32) return NMQ_ERR_SHAPE;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    hipLaunchKernelGGL(quant_q8_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, x_is_f32, xq,
+                       xq2, xd, xs, n);
+    return (int)hipGetLastError();
+}
+
+static int check_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
+                    const float* y, int n_out, int n_in) {
+    int bv, bb;
+    if (nmq_format_info(fmt, &bv, &bb)) return NMQ_ERR_FORMAT;
+    if (!w || !xq || !xq2 || !xd || !xs || !y) return NMQ_ERR_ARG;
+    if (!aligned(xq, 16) || !aligned(xq2, 16) || !aligned(xd, 4) || !aligned(xs, 4) || !aligned(y, 4))
+        return NMQ_ERR_ARG;
+    if (n_out < 1 || n_in < bv || n_in % bv || n_in > (1 << 20)) return NMQ_ERR_SHAPE;
+    // Q4_K reads its 16-byte block header and quant groups with aligned 16-byte loads
+    if (fmt == NMQ_Q4_K && !aligned(w, 16)) return NMQ_ERR_ARG;
+    if (!aligned(w, 2)) return NMQ_ERR_ARG;
+    return NMQ_OK;
+}
+
+int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, float* y,
+           int n_out, int n_in, int ncols, void* stream) {
+    int e = check_mv(fmt, w, xq, xq2, xd, xs, y, n_out, n_in);
+    if (e) return e;
+    if (ncols < 1) return NMQ_ERR_ARG;
+    for (int c0 = 0; c0 < ncols; c0 += NMQ_MAX_COLS) {
+        const int nc = ncols - c0 < NMQ_MAX_COLS ? ncols - c0 : NMQ_MAX_COLS;
+        MvParams p{};
+        p.w = (const u8*)w;
+        p.ids = nullptr;
+        p.per_expert = 0;
+        p.xq = xq + (int64_t)c0 * n_in;
+        p.xq2 = xq2 + (int64_t)c0 * n_in;
+        p.xd = xd + (int64_t)c0 * (n_in / 32);
+        p.xs = xs + (int64_t)c0 * (n_in / 32);
+        p.y = y + (int64_t)c0 * n_out;
+        p.n_out = n_out;
+        p.n_in = n_in;
+        p.x_group = 1;
+        e = launch_any(fmt, p, nc, 1, (hipStream_t)stream);
+        if (e) return e;
+    }
+    return NMQ_OK;
+}
+
+int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_t per_expert, const int8_t* xq,
+                   const int8_t* xq2, const float* xd, const float* xs, int x_group, float* y, int n_out, int n_in,
+                   void* stream) {
+    int e = check_mv(fmt, w, xq, xq2, xd, xs, y, n_out, n_in);
+    if (e) return e;
+    if (!ids || n_ids < 1 || n_ids > 65535 || x_group < 1) return NMQ_ERR_ARG;
+    if (per_expert >= 0) {
+        int bv, bb;
+        nmq_format_info(fmt, &bv, &bb);
+        if (per_expert < (int64_t)n_out * (n_in / bv) * bb) return NMQ_ERR_SHAPE;
+        if (fmt == NMQ_Q4_K && per_expert % 16) return NMQ_ERR_ARG;
+        if (per_expert % 2) return NMQ_ERR_ARG;
+    } else if (!aligned(w, 8)) {
+        return NMQ_ERR_ARG;
+    }
+    MvParams p{};
+    p.w = (const u8*)w;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xq = xq;
+    p.xq2 = xq2;
+    p.xd = xd;
+    p.xs = xs;
+    p.y = y;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    p.x_group = x_group;
+    return launch_any(fmt, p, 1, n_ids, (hipStream_t)stream);
+}
+
+int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2, int n_out,
+                   int n_in, void* stream) {
+    int bv, bb;
+    if (nmq_format_info(fmt, &bv, &bb)) return NMQ_ERR_FORMAT;
+    if (!w || !xq || !xq2 || !s1 || !s2 || !aligned(xq, 16) || !aligned(xq2, 16) || !aligned(w, 16))
+        return NMQ_ERR_ARG;
+    if (n_out < 1 || n_in < bv || n_in % bv || n_in > (1 << 20)) return NMQ_ERR_SHAPE;
+    const int64_t threads = (int64_t)n_out * ((n_in + 63) / 64);
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    return launch_fmt_kernel<SumsK>(fmt, dim3((unsigned)blocks), (hipStream_t)stream, (const u8*)w, xq, xq2, s1, s2,
+                                    n_out, n_in);
+}
+
+int nmq_dequant_bf16(int fmt, const void* w, uint16_t* out, int64_t n_blocks, void* stream) {
+    int bv, bb;
+    if (nmq_format_info(fmt, &bv, &bb)) return NMQ_ERR_FORMAT;
+    if (!w || !out || !aligned(out, 16) || !aligned(w, fmt == NMQ_Q4_K ? 16 : 2)) return NMQ_ERR_ARG;
+    if (n_blocks < 1) return NMQ_ERR_SHAPE;
+    const int64_t threads = bv == 32 ? (n_blocks + 1) / 2 : n_blocks * 4;
+    const int64_t blocks = (threads + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    return launch_fmt_kernel<DeqK>(fmt, dim3((unsigned)blocks), (hipStream_t)stream, (const u8*)w, (u16*)out,
+                                   n_blocks);
+}
+
+}  // extern "C"

@@ -1,0 +1,316 @@
+// Device-side building blocks of the gfx950 GGUF mat-vec kernels: scalar helpers, the two-stage
+// int8 input slice a lane works on, and one "unit" decoder per block format.
+//
+// A unit is the piece of one weight row a lane handles at a time: 64 values, decoded to sixteen
+// dwords of four int8 weights each (w[0..15]) plus fp32 factors per 16 values.  The sixteen dwords
+// are ordered like the lane's slice of the input, so w[k] pairs with xq dword k.  Two slice shapes:
+//   contiguous (Q4_K, Q8_0, IQ2_XXS): the unit covers values 64u .. 64u+63 of the row; runs 0,1
+//     (values 0..31) share one weight factor and xd, runs 2,3 the next.
+//   strided (Q6_K, TQ2_0): unit u = 4b + 2h + j of block b covers the four 16-value runs at
+//     256b + 128h + 32k + 16j (k = 0..3), one weight factor and one xd per run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/nmq.h"
+
+namespace nmq {
+
+typedef uint8_t u8;
+typedef uint16_t u16;
+typedef uint32_t u32;
+typedef uint64_t u64;
+
+// Loads of weight bytes.  Q6_K (210 B), Q8_0 (34 B), TQ2_0 and IQ2_XXS (66 B) blocks are only
+// 2-byte aligned; gfx950 serves dword-multiple global loads at any alignment, and these types tell
+// the compiler so (it emits global_load_dwordx4 / dwordx2 / dword for them).
+typedef u32 u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef u32 u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef u32 u32_a2 __attribute__((aligned(2)));
+typedef u32 u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float FEIN = 1.0f / 254.0f;  // scale of the second input stage relative to xd
+
+__device__ __forceinline__ float h2f(u32 bits16) {
+    return (float)__builtin_bit_cast(_Float16, (u16)(bits16 & 0xffffu));
+}
+
+__device__ __forceinline__ int dot4(u32 a, u32 b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ u32 bfe(u32 v, u32 off, u32 len) { return __builtin_amdgcn_ubfe(v, off, len); }
+
+__device__ __forceinline__ u32x4 ld4(const u8* p) { return *(const u32x4_a2*)p; }
+__device__ __forceinline__ u32x2 ld2(const u8* p) { return *(const u32x2_a2*)p; }
+__device__ __forceinline__ u32 ld1(const u8* p) { return *(const u32_a2*)p; }
+__device__ __forceinline__ u32 ld16(const u8* p) { return *(const u16*)p; }
+
+// q - 32 per byte for bytes 0..63 (Q6_K): ((q | 0x80) - 0x20) ^ 0x80 never borrows across bytes.
+__device__ __forceinline__ u32 sub32x4(u32 v) { return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
+// code - 1 per byte for codes 0..3 (TQ2_0): (c + 0x7f) ^ 0x80 never carries across bytes.
+__device__ __forceinline__ u32 sub1x4(u32 v) { return (v + 0x7f7f7f7fu) ^ 0x80808080u; }
+
+// The two-stage input of one unit for one token (read from LDS).
+struct XSlice {
+    u32 q[16];   // xq bytes in unit order
+    u32 q2[16];  // xq2 bytes
+    float d[4];  // xd: contiguous shape uses d[0], d[1]; strided shape d[0..3]
+    float s[2];  // xs (contiguous shape only; Q4_K min term)
+};
+
+// Weight factors of one decoded unit.
+struct WUnit {
+    u32 w[16];
+    float ws[4];  // per run (contiguous shape: ws[0] for runs 0,1 and ws[2] for runs 2,3)
+    float wm[2];  // Q4_K: dmin*m of the two sub-blocks; 0 otherwise
+};
+
+// Integer sums of one unit against one token's slice, run by run (exposed for the diagnostic).
+__device__ __forceinline__ void unit_sums(const u32 (&w)[16], const XSlice& x, int (&s1)[4], int (&s2)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        int a = 0, b = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            a = dot4(w[4 * r + k], x.q[4 * r + k], a);
+            b = dot4(w[4 * r + k], x.q2[4 * r + k], b);
+        }
+        s1[r] = a;
+        s2[r] = b;
+    }
+}
+
+template <bool STRIDED, bool HAS_MIN>
+__device__ __forceinline__ float unit_dot(const WUnit& u, const XSlice& x) {
+    int s1[4], s2[4];
+    unit_sums(u.w, x, s1, s2);
+    if (STRIDED) {
+        float acc = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc += u.ws[r] * x.d[r] * ((float)s1[r] + FEIN * (float)s2[r]);
+        return acc;
+    } else {
+        const float f0 = (float)(s1[0] + s1[1]) + FEIN * (float)(s2[0] + s2[1]);
+        const float f1 = (float)(s1[2] + s1[3]) + FEIN * (float)(s2[2] + s2[3]);
+        float acc = u.ws[0] * x.d[0] * f0 + u.ws[2] * x.d[1] * f1;
+        if (HAS_MIN) acc -= u.wm[0] * x.s[0] + u.wm[1] * x.s[1];
+        return acc;
+    }
+}
+
+// ---- per-format unit decoders -------------------------------------------------------------------
+// Fmt<F>::Raw holds the loaded bytes of one unit; load() never touches memory outside the row
+// (row_units = units in the row; a Q8_0 row may end with half a unit).  decode() turns the bytes
+// into a WUnit.  `tab` points at the LDS tables (IQ2_XXS only).
+
+template <int F>
+struct Fmt;
+
+// Q4_K, 144-byte blocks (reference quant.py:111-120, mmvq.py:333-419): unit u = group i = u % 4
+// of block u / 4: qs bytes 32i .. 32i+31 hold sub-block 2i (low nibbles) and 2i+1 (high nibbles).
+template <>
+struct Fmt<NMQ_Q4_K> {
+    static constexpr int BV = 256, BB = 144;
+    static constexpr bool STRIDED = false, HAS_MIN = true;
+    struct Raw {
+        u32x4 a, b, h;
+    };
+    __device__ static void load(const u8* row, int u, int /*row_units*/, Raw& r) {
+        const u8* blk = row + (u >> 2) * BB;
+        const int i = u & 3;
+        r.h = *(const u32x4*)blk;  // d, dmin, scales[12]: 16-byte aligned when the row is
+        r.a = *(const u32x4*)(blk + 16 + 32 * i);
+        r.b = *(const u32x4*)(blk + 32 + 32 * i);
+    }
+    __device__ static void decode(const Raw& r, int u, const u64* /*tab*/, WUnit& o) {
+        const u32 q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            o.w[k] = q[k] & 0x0f0f0f0fu;
+            o.w[8 + k] = (q[k] >> 4) & 0x0f0f0f0fu;
+        }
+        // get_scale_min_k4 for sub-blocks j = 2i and 2i+1 (t = j % 4, both in the same half)
+        const int i = u & 3;
+        const bool hi = i >= 2;
+        const u32 t0 = (u32)(2 * i) & 3u;
+        float sc[2], mn[2];
+#pragma unroll
+        for (int z = 0; z < 2; ++z) {
+            const u32 sh = 8u * (t0 + z);
+            const u32 A = bfe(r.h.y, sh, 8), B = bfe(r.h.z, sh, 8), C = bfe(r.h.w, sh, 8);
+            const u32 s = hi ? ((C & 15u) | ((A >> 6) << 4)) : (A & 63u);
+            const u32 m = hi ? ((C >> 4) | ((B >> 6) << 4)) : (B & 63u);
+            sc[z] = (float)s;
+            mn[z] = (float)m;
+        }
+        const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+        o.ws[0] = o.ws[1] = d * sc[0];
+        o.ws[2] = o.ws[3] = d * sc[1];
+        o.wm[0] = dmin * mn[0];
+        o.wm[1] = dmin * mn[1];
+    }
+};
+
+// Q6_K, 210-byte blocks (quant.py:140-159, mmvq.py:421-482): unit u = 4b + 2h + j takes
+// l = 16j .. 16j+15 of half h: ql[64h + l], ql[64h + 32 + l], qh[32h + l]; runs k = 0..3 are the
+// values 128h + 32k + l with the int8 scales sc[8h + 2k + j].
+template <>
+struct Fmt<NMQ_Q6_K> {
+    static constexpr int BV = 256, BB = 210;
+    static constexpr bool STRIDED = true, HAS_MIN = false;
+    struct Raw {
+        u32x4 la, lb, qh;
+        u32x2 sc;
+        u32 d;
+    };
+    __device__ static void load(const u8* row, int u, int /*row_units*/, Raw& r) {
+        const u8* blk = row + (u >> 2) * BB;
+        const int h = (u >> 1) & 1, j = u & 1;
+        r.la = ld4(blk + 64 * h + 16 * j);
+        r.lb = ld4(blk + 64 * h + 32 + 16 * j);
+        r.qh = ld4(blk + 128 + 32 * h + 16 * j);
+        r.sc = ld2(blk + 192 + 8 * h);
+        r.d = ld16(blk + 208);
+    }
+    __device__ static void decode(const Raw& r, int u, const u64* /*tab*/, WUnit& o) {
+        const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+        const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+        const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o.w[0 + k] = sub32x4((la[k] & 0x0f0f0f0fu) | ((qh[k] & 0x03030303u) << 4));
+            o.w[4 + k] = sub32x4((lb[k] & 0x0f0f0f0fu) | (((qh[k] >> 2) & 0x03030303u) << 4));
+            o.w[8 + k] = sub32x4(((la[k] >> 4) & 0x0f0f0f0fu) | (((qh[k] >> 4) & 0x03030303u) << 4));
+            o.w[12 + k] = sub32x4(((lb[k] >> 4) & 0x0f0f0f0fu) | (((qh[k] >> 6) & 0x03030303u) << 4));
+        }
+        const int j = u & 1;
+        const float d = h2f(r.d);
+        // scale bytes sc[8h + 2k + j]: k = 0,1 in the low dword, k = 2,3 in the high one
+        const u32 sh = 8u * j;
+        o.ws[0] = d * (float)(int8_t)bfe(r.sc.x, sh, 8);
+        o.ws[1] = d * (float)(int8_t)bfe(r.sc.x, sh + 16, 8);
+        o.ws[2] = d * (float)(int8_t)bfe(r.sc.y, sh, 8);
+        o.ws[3] = d * (float)(int8_t)bfe(r.sc.y, sh + 16, 8);
+        o.wm[0] = o.wm[1] = 0.f;
+    }
+};
+
+// Q8_0, 34-byte blocks (quant.py:46-50, cudakern.py:307-313): unit u = blocks 2u and 2u+1 (68
+// bytes).  The second block is absent when the row has an odd number of blocks and u is the last.
+template <>
+struct Fmt<NMQ_Q8_0> {
+    static constexpr int BV = 32, BB = 34;
+    static constexpr bool STRIDED = false, HAS_MIN = false;
+    struct Raw {
+        u32 v[17];
+    };
+    __device__ static void load(const u8* row, int u, int nblk, Raw& r) {
+        const u8* p = row + 68 * u;
+        const u32x4 a = ld4(p), b = ld4(p + 16);
+        r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
+        r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
+        if (2 * u + 1 < nblk) {
+            r.v[8] = ld1(p + 32);  // qs[30], qs[31] of block 0 and d of block 1
+            const u32x4 c = ld4(p + 36), e = ld4(p + 52);
+            r.v[9] = c.x; r.v[10] = c.y; r.v[11] = c.z; r.v[12] = c.w;
+            r.v[13] = e.x; r.v[14] = e.y; r.v[15] = e.z; r.v[16] = e.w;
+        } else {
+            r.v[8] = ld16(p + 32);  // only qs[30], qs[31]: block 1 is past the row end
+#pragma unroll
+            for (int k = 9; k < 17; ++k) r.v[k] = 0u;
+        }
+    }
+    __device__ static void decode(const Raw& r, int /*u*/, const u64* /*tab*/, WUnit& o) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o.w[k] = __builtin_amdgcn_alignbyte(r.v[k + 1], r.v[k], 2);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o.w[8 + k] = r.v[9 + k];
+        o.ws[0] = o.ws[1] = h2f(r.v[0]);
+        o.ws[2] = o.ws[3] = h2f(r.v[8] >> 16);
+        o.wm[0] = o.wm[1] = 0.f;
+    }
+};
+
+// TQ2_0, 66-byte blocks (quant.py:417-421, cudakern.py:432-439): unit u = 4b + 2n + j takes qs
+// bytes 32n + 16j .. +15; run l holds the 2-bit codes at shift 2l (values 128n + 32l + 16j + m).
+template <>
+struct Fmt<NMQ_TQ2_0> {
+    static constexpr int BV = 256, BB = 66;
+    static constexpr bool STRIDED = true, HAS_MIN = false;
+    struct Raw {
+        u32x4 q;
+        u32 d;
+    };
+    __device__ static void load(const u8* row, int u, int /*row_units*/, Raw& r) {
+        const u8* blk = row + (u >> 2) * BB;
+        r.q = ld4(blk + 16 * (u & 3));
+        r.d = ld16(blk + 64);
+    }
+    __device__ static void decode(const Raw& r, int /*u*/, const u64* /*tab*/, WUnit& o) {
+        const u32 q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+#pragma unroll
+        for (int l = 0; l < 4; ++l)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o.w[4 * l + k] = sub1x4((q[k] >> (2 * l)) & 0x03030303u);
+        const float d = h2f(r.d);
+        o.ws[0] = o.ws[1] = o.ws[2] = o.ws[3] = d;
+        o.wm[0] = o.wm[1] = 0.f;
+    }
+};
+
+// IQ2_XXS, 66-byte blocks (quant.py:235-245, cudakern.py:187-195): unit u = sub-blocks 2i, 2i+1
+// (i = u % 4) of block u / 4; each sub-block is {u32 aux0: 4 grid indices, u32 aux1: 4 x 7 sign
+// bits + 4-bit scale ls}.  tab[0..255] = grid (LDS), tab[256..383] = byte masks of the 128 sign
+// patterns with the parity bit as bit 7.
+template <>
+struct Fmt<NMQ_IQ2_XXS> {
+    static constexpr int BV = 256, BB = 66;
+    static constexpr bool STRIDED = false, HAS_MIN = false;
+    struct Raw {
+        u32x4 q;
+        u32 d;
+    };
+    __device__ static void load(const u8* row, int u, int /*row_units*/, Raw& r) {
+        const u8* blk = row + (u >> 2) * BB;
+        r.q = ld4(blk + 2 + 16 * (u & 3));
+        r.d = ld16(blk);
+    }
+    __device__ static void decode(const Raw& r, int /*u*/, const u64* tab, WUnit& o) {
+        const float d = h2f(r.d);
+        const u32 aux0[2] = {r.q.x, r.q.z}, aux1[2] = {r.q.y, r.q.w};
+#pragma unroll
+        for (int z = 0; z < 2; ++z) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const u64 g = tab[bfe(aux0[z], 8 * l, 8)];
+                const u64 m = tab[256 + bfe(aux1[z], 7 * l, 7)];
+                const u32 glo = (u32)g, ghi = (u32)(g >> 32), mlo = (u32)m, mhi = (u32)(m >> 32);
+                o.w[8 * z + 2 * l] = (glo ^ mlo) + (mlo & 0x01010101u);
+                o.w[8 * z + 2 * l + 1] = (ghi ^ mhi) + (mhi & 0x01010101u);
+            }
+            const float db = d * (0.125f + 0.25f * (float)(aux1[z] >> 28));
+            o.ws[2 * z] = o.ws[2 * z + 1] = db;
+        }
+        o.wm[0] = o.wm[1] = 0.f;
+    }
+};
+
+// IQ2_XXS tables for LDS: the grid and the 128 sign masks (bit j of the 8-bit sign pattern ->
+// byte j = 0xff).  Filled by the first threads of a workgroup.
+__device__ const u64 IQ2XXS_GRID[256] = {
+#include "iq2xxs_grid.inc"
+};
+
+__device__ __forceinline__ u64 iq2_sign_mask(u32 s7) {
+    const u32 s = s7 | ((u32)(__builtin_popcount(s7) & 1) << 7);
+    u64 m = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        if ((s >> j) & 1u) m |= (u64)0xff << (8 * j);
+    return m;
+}
+
+}  // namespace nmq

@@ -1,0 +1,6 @@
+// Mat-vec kernels of format IQ2_XXS: every (tokens, team width) variant of mv_kernel.
+#include "nmq_mv_impl.hpp"
+
+namespace nmq {
+template int launch_mv<NMQ_IQ2_XXS>(MvParams, int, int, hipStream_t);
+}  // namespace nmq

@@ -1,0 +1,100 @@
+"""ctypes binding of libnmq.so (C ABI in include/nmq.h).
+
+torch is imported first so that libnmq.so binds to the HIP runtime torch already loaded (same
+soname), and torch's streams and allocations are valid in the library.  Nothing here falls back
+to another implementation: a missing library or a non-gfx950 device makes `available()` False and
+every launch wrapper raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime first)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.abspath(os.path.join(HERE, "..", "libnmq.so"))
+
+NMQ_OK, NMQ_ERR_FORMAT, NMQ_ERR_SHAPE, NMQ_ERR_ARG, NMQ_ERR_DEVICE = 0, -1, -2, -3, -4
+MAX_COLS = 8
+
+_lock = threading.Lock()
+_lib = None
+_load_error = None
+_device_ok: dict = {}
+
+
+class NativeError(RuntimeError):
+    """A launch failed on the device (the reference raises RuntimeError on cuLaunchKernel errors,
+    mmvq.py:817-818, cudakern.py:751-753)."""
+
+
+def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
+    p, i, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+    L.nmq_abi_version.restype = i
+    L.nmq_strerror.argtypes, L.nmq_strerror.restype = [i], ctypes.c_char_p
+    L.nmq_format_info.argtypes, L.nmq_format_info.restype = [i, p, p], i
+    L.nmq_device_arch.argtypes, L.nmq_device_arch.restype = [ctypes.c_char_p, i], i
+    L.nmq_quant_q8.argtypes, L.nmq_quant_q8.restype = [p, i, p, p, p, p, i64, p], i
+    L.nmq_mv.argtypes, L.nmq_mv.restype = [i, p, p, p, p, p, p, i, i, i, p], i
+    L.nmq_mv_experts.argtypes = [i, p, p, i, i64, p, p, p, p, i, p, i, i, p]
+    L.nmq_mv_experts.restype = i
+    L.nmq_block_sums.argtypes, L.nmq_block_sums.restype = [i, p, p, p, p, p, i, i, p], i
+    L.nmq_dequant_bf16.argtypes, L.nmq_dequant_bf16.restype = [i, p, p, i64, p], i
+    L.nmq_encode.argtypes, L.nmq_encode.restype = [i, p, i64, p, i], i64
+    return L
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it is missing (build it with __graft_entry__.build())."""
+    global _lib, _load_error
+    if _lib is None:
+        with _lock:
+            if _lib is None and _load_error is None:
+                try:
+                    _lib = _bind(ctypes.CDLL(LIB_PATH))
+                except OSError as exc:
+                    _load_error = exc
+    if _lib is None:
+        raise NativeError(f"libnmq.so not loadable ({LIB_PATH}): {_load_error}")
+    return _lib
+
+
+def strerror(code: int) -> str:
+    return lib().nmq_strerror(code).decode()
+
+
+def check(code: int) -> None:
+    if code == NMQ_OK:
+        return
+    if code in (NMQ_ERR_SHAPE, NMQ_ERR_ARG, NMQ_ERR_FORMAT):
+        raise ValueError(strerror(code))
+    raise NativeError(strerror(code))
+
+
+def available(device=None) -> bool:
+    """True when libnmq.so loads and `device` is a gfx950 GPU (the only target of the kernels)."""
+    try:
+        L = lib()
+    except NativeError:
+        return False
+    dev = torch.device(device) if device is not None else torch.device("cuda")
+    if dev.type != "cuda" or not torch.cuda.is_available():
+        return False
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx not in _device_ok:
+        with _lock:
+            if idx not in _device_ok:
+                buf = ctypes.create_string_buffer(64)
+                with torch.cuda.device(idx):
+                    _device_ok[idx] = L.nmq_device_arch(buf, 64) == NMQ_OK
+    return _device_ok[idx]
+
+
+def stream_ptr(device=None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t) -> int:
+    return 0 if t is None else t.data_ptr()

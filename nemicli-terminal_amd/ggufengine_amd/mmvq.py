@@ -1,0 +1,161 @@
+"""
+Drop-in for the reference's ggufengine/mmvq.py (int8 mat-vec on Q4_K / Q6_K blocks), on gfx950.
+
+Same names, arguments and return shapes as the reference module (mmvq.py:25-37, 808-938):
+`FORMATE`, `SPALTEN`, `MMVQ_BIS`, `MMQ_BIS`, `ZEILEN_JE_WARP`, `verfuegbar`, `Eingang`, `mv`,
+`eingang_teilen`, `mm`, `entpacken`, `schritt_moeglich`.  The arithmetic is the reference's: the
+input is quantised per 32 values in two int8 stages (about 15 bits, fp32 scale and sum), every
+weight byte is read once and multiplied with v_dot4_i32_i8, and the per-sub-block scales are applied
+in fp32.  Launches go through libnmq.so (include/nmq.h) on torch's current stream, so they can be
+captured in a HIP graph.  No torch or CPU fallback: `verfuegbar` is False without the library or a
+gfx950 device, and calls raise.
+
+Differences from the reference (documented, same results within the parity tolerance):
+  - up to SPALTEN = 8 tokens per launch (the reference compiles 1..9);
+  - `mm` (the reference's tensor-core MMQ tiles for 17..112 tokens) runs the same int8 mat-vec
+    kernels in groups of SPALTEN tokens;
+  - the fused one-token steps (norm_q8, akt_q8, rope_kv, attention1) are not provided here;
+    `schritt_moeglich` returns False, and callers then take their unfused path
+    (models/baukasten.py:205).
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+import threading
+from typing import Optional
+
+import torch
+
+from . import _native
+from .gguf_types import TYPE_ID
+
+FORMATE = {"Q4_K": (256, 144), "Q6_K": (256, 210)}
+WARPS = 4                     # waves per workgroup (at most; fewer for short matrices)
+SPALTEN = _native.MAX_COLS    # tokens (input rows) per launch, weights read once for all of them
+# weight rows per team of lanes by token count (the kernels are compiled for these)
+ZEILEN_JE_WARP = {"Q4_K": lambda nc: 1 if nc == 1 else 2, "Q6_K": lambda nc: 1 if nc == 1 else 2}
+MMVQ_BIS = {"Q4_K": 16, "Q6_K": 16}
+MMQ_BIS = {"Q4_K": 112, "Q6_K": 112}
+
+
+def verfuegbar(device, fmt: str, n_in: int) -> bool:
+    """Kernel for this format and row length on this device (reference mmvq.py:808-810)."""
+    return fmt in FORMATE and n_in % 256 == 0 and n_in > 0 and _native.available(device)
+
+
+def _starten(name: str, fn, *args) -> None:
+    """Every launch of this module goes through here (name of the kernel family, C function,
+    arguments); a nonzero return raises like the reference's _starten (mmvq.py:813-818)."""
+    _native.check(fn(*args))
+
+
+def _z(t: Optional[torch.Tensor]) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+class Eingang:
+    """The two-stage int8 input of a vector (or of M token rows back to back): xq, xq2 int8 (n),
+    xd = scale and xs = sum per 32 values (float32, n/32).  Built once per input, shared by every
+    matrix that reads it.  Without x only the buffers (reference mmvq.py:821-849)."""
+
+    def __init__(self, x: Optional[torch.Tensor] = None, n: int = 0, device=None):
+        if x is not None:
+            x = x.reshape(-1)
+            if x.dtype != torch.float32:
+                x = x.to(torch.bfloat16)
+            x = x.contiguous()
+            n, device = x.numel(), x.device
+        if n % 32:
+            raise ValueError(f"Eingang: {n} values are not a multiple of 32")
+        self.n = n
+        self.xq = torch.empty(n, dtype=torch.int8, device=device)
+        self.xq2 = torch.empty(n, dtype=torch.int8, device=device)          # rest, scale xd / 254
+        self.xd = torch.empty(n // 32, dtype=torch.float32, device=device)
+        self.xs = torch.empty(n // 32, dtype=torch.float32, device=device)
+        if x is not None:
+            L = _native.lib()
+            _starten("quant_q8", L.nmq_quant_q8, x.data_ptr(), int(x.dtype == torch.float32),
+                     *[t.data_ptr() for t in (self.xq, self.xq2, self.xd, self.xs)], n,
+                     _native.stream_ptr(x.device))
+
+    def zeiger(self, ab: int = 0) -> list:
+        """Pointers to xq, xq2, xd, xs from value `ab` on (the start of a token row)."""
+        if not ab:
+            return [_z(self.xq), _z(self.xq2), _z(self.xd), _z(self.xs)]
+        return [_z(self.xq[ab:]), _z(self.xq2[ab:]), _z(self.xd[ab // 32:]), _z(self.xs[ab // 32:])]
+
+
+_TEILEN = threading.local()
+
+
+@contextlib.contextmanager
+def eingang_teilen():
+    """Matrices with the same input (q/k/v, gate/up): inside, the int8 input of a tensor is built
+    once (keyed by data pointer, shape and dtype, as the reference keys its MMQ input,
+    mmvq.py:868-899) and reused by `mv` and `mm`."""
+    alt = getattr(_TEILEN, "werte", None)
+    _TEILEN.werte = {}
+    try:
+        yield
+    finally:
+        _TEILEN.werte = alt
+
+
+def _eingang(x: torch.Tensor) -> Eingang:
+    geteilt = getattr(_TEILEN, "werte", None)
+    if geteilt is None:
+        return Eingang(x)
+    key = (x.data_ptr(), tuple(x.shape), x.dtype)
+    e = geteilt.get(key)
+    if e is None:
+        e = geteilt[key] = Eingang(x)
+    return e
+
+
+def _mv(fmt: str, raw: torch.Tensor, e: Eingang, n_out: int, n_in: int) -> torch.Tensor:
+    if e.n % n_in:
+        raise ValueError(f"mv: input of {e.n} values is not a multiple of n_in={n_in}")
+    M = e.n // n_in
+    y = torch.empty(M, n_out, dtype=torch.float32, device=raw.device)
+    L = _native.lib()
+    _starten("mv", L.nmq_mv, TYPE_ID[fmt], raw.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+             e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, M, _native.stream_ptr(raw.device))
+    return y
+
+
+def mv(fmt: str, raw: torch.Tensor, x, n_out: int, n_in: int) -> torch.Tensor:
+    """raw: (n_out, n_in) in block format on the GPU; x: (M, n_in) or (n_in,) bf16/float32, or an
+    Eingang of M rows -> (M, n_out) float32, or (n_out,) for a vector (reference mmvq.py:852-865)."""
+    if fmt not in FORMATE:
+        raise ValueError(f"mmvq.mv: format {fmt} (this module serves {tuple(FORMATE)})")
+    e = x if isinstance(x, Eingang) else _eingang(x)
+    y = _mv(fmt, raw, e, n_out, n_in)
+    vektor = y.shape[0] == 1 if isinstance(x, Eingang) else x.dim() == 1
+    return y[0] if vektor else y
+
+
+def mm(fmt: str, raw: torch.Tensor, x: torch.Tensor, n_out: int, n_in: int) -> torch.Tensor:
+    """Several tokens: x (M, n_in) -> (M, n_out) float32 (reference mmvq.py:902-920).  Runs the int8
+    mat-vec kernels in groups of SPALTEN tokens."""
+    if fmt not in FORMATE:
+        raise ValueError(f"mmvq.mm: format {fmt}")
+    x2 = x.reshape(-1, n_in)
+    return _mv(fmt, raw, _eingang(x2), n_out, n_in)
+
+
+def entpacken(fmt: str, raw: torch.Tensor, n_out: int, n_in: int) -> torch.Tensor:
+    """raw: (n_out, n_in) in block format -> (n_out, n_in) bf16 (reference mmvq.py:923-931): the
+    exact fp32 value of quant.py rounded to nearest-even bf16."""
+    bs, _ = FORMATE[fmt]
+    out = torch.empty(n_out, n_in, dtype=torch.bfloat16, device=raw.device)
+    L = _native.lib()
+    _starten("entpacken", L.nmq_dequant_bf16, TYPE_ID[fmt], raw.data_ptr(), out.data_ptr(), n_out * n_in // bs,
+             _native.stream_ptr(raw.device))
+    return out
+
+
+def schritt_moeglich(device, H: int, Hkv: int, D: int) -> bool:
+    """The fused one-token step kernels are not part of this library: always False, so callers run
+    their general layer path (reference mmvq.py:1009-1014, models/baukasten.py:205)."""
+    return False

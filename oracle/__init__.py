@@ -1,0 +1,157 @@
+"""CPU oracle for the GGUF quantized mat-vec path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this package, and only
+as the checker (or as the timed CPU baseline).  The product path (nemicli-terminal_amd/) never
+imports it and fails loudly when its own HIP library is missing.
+
+numpy wrappers over liboracle.so (built from nmq_oracle.c and nmq_cpu_baseline.c by the Makefile
+beside this file).  Each wrapped C function cites the reference lines it restates.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+Q8_0, Q4_K, Q6_K, IQ2_XXS, TQ2_0 = 8, 12, 14, 16, 35
+FORMATS = {"Q8_0": (Q8_0, 32, 34), "Q4_K": (Q4_K, 256, 144), "Q6_K": (Q6_K, 256, 210),
+           "IQ2_XXS": (IQ2_XXS, 256, 66), "TQ2_0": (TQ2_0, 256, 66)}
+
+_lib = None
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        p, i, i64, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+        L.or_half_to_float.argtypes, L.or_half_to_float.restype = [ctypes.c_uint16], f
+        L.or_round_bf16.argtypes, L.or_round_bf16.restype = [f], f
+        L.or_dequant.argtypes, L.or_dequant.restype = [i, p, i64, p], i
+        L.or_quant_q8.argtypes, L.or_quant_q8.restype = [p, i64, p, p, p, p], None
+        L.or_block_sums.argtypes, L.or_block_sums.restype = [i, p, i, i, p, p, p, p], i
+        L.or_mv_int.argtypes, L.or_mv_int.restype = [i, p, i, i, p, p, p, p, i, p], i
+        L.or_mv_deq.argtypes, L.or_mv_deq.restype = [i, p, i, i, p, i, p], i
+        L.or_gemv_f32.argtypes, L.or_gemv_f32.restype = [p, i, i, p, p, i], None
+        L.or_deq_gemv_f32.argtypes, L.or_deq_gemv_f32.restype = [i, p, i, i, p, p, i], i
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data
+
+
+def fmt_id(fmt) -> int:
+    return FORMATS[fmt][0] if isinstance(fmt, str) else int(fmt)
+
+
+def fmt_info(fmt):
+    for name, (t, bv, bb) in FORMATS.items():
+        if t == fmt_id(fmt):
+            return name, bv, bb
+    raise KeyError(fmt)
+
+
+def half_to_float(bits: np.ndarray) -> np.ndarray:
+    f = lib().or_half_to_float
+    return np.array([f(int(b)) for b in np.asarray(bits, dtype=np.uint16).ravel()], dtype=np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    """RNE rounding of fp32 to bf16 (returned as fp32): torch's .to(torch.bfloat16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    r = np.where(nan, u.astype(np.uint32), r)
+    return r.view(np.float32).reshape(np.shape(x))
+
+
+def dequant(fmt, raw: np.ndarray) -> np.ndarray:
+    """quant.py:484-503 `dequantize` -> flat fp32."""
+    _, bv, bb = fmt_info(fmt)
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    assert raw.size % bb == 0
+    nb = raw.size // bb
+    out = np.empty(nb * bv, dtype=np.float32)
+    assert lib().or_dequant(fmt_id(fmt), _ptr(raw), nb, _ptr(out)) == 0
+    return out
+
+
+def quant_q8(x: np.ndarray):
+    """mmvq.py:62-83 quant_q8 on fp32 values (flattened) -> (xq, xq2, xd, xs)."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    n = x.size
+    assert n % 32 == 0
+    xq = np.empty(n, np.int8)
+    xq2 = np.empty(n, np.int8)
+    xd = np.empty(n // 32, np.float32)
+    xs = np.empty(n // 32, np.float32)
+    lib().or_quant_q8(_ptr(x), n, _ptr(xq), _ptr(xq2), _ptr(xd), _ptr(xs))
+    return xq, xq2, xd, xs
+
+
+def block_sums(fmt, raw: np.ndarray, n_out: int, n_in: int, xq: np.ndarray, xq2: np.ndarray):
+    """int32 sums per 16 weights: (s1, s2), each (n_out, n_in/16)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    xq = np.ascontiguousarray(xq, dtype=np.int8).ravel()
+    xq2 = np.ascontiguousarray(xq2, dtype=np.int8).ravel()
+    s1 = np.empty((n_out, n_in // 16), np.int32)
+    s2 = np.empty((n_out, n_in // 16), np.int32)
+    assert lib().or_block_sums(fmt_id(fmt), _ptr(raw), n_out, n_in, _ptr(xq), _ptr(xq2), _ptr(s1), _ptr(s2)) == 0
+    return s1, s2
+
+
+def mv_int(fmt, raw, n_out, n_in, xq, xq2, xd, xs, ncols=1) -> np.ndarray:
+    """Integer-decomposition mat-vec, fp64 combine -> (ncols, n_out) float64."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    a = [np.ascontiguousarray(v) for v in (xq, xq2, xd, xs)]
+    y = np.empty((ncols, n_out), np.float64)
+    assert lib().or_mv_int(fmt_id(fmt), _ptr(raw), n_out, n_in, *[_ptr(v) for v in a], ncols, _ptr(y)) == 0
+    return y
+
+
+def mv_deq(fmt, raw, n_out, n_in, x) -> np.ndarray:
+    """Dequantise + matmul, fp64 accumulation: x (ncols, n_in) fp32 -> (ncols, n_out) float64."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+    y = np.empty((x.shape[0], n_out), np.float64)
+    assert lib().or_mv_deq(fmt_id(fmt), _ptr(raw), n_out, n_in, _ptr(x), x.shape[0], _ptr(y)) == 0
+    return y
+
+
+def gemv_f32(w: np.ndarray, x: np.ndarray, threads: int) -> np.ndarray:
+    """CPU baseline GEMV (F.linear of the Linear path, models/common.py:526-527)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.empty(w.shape[0], np.float32)
+    lib().or_gemv_f32(_ptr(w), w.shape[0], w.shape[1], _ptr(x), _ptr(y), threads)
+    return y
+
+
+def deq_gemv_f32(fmt, raw, n_out, n_in, x, threads: int) -> np.ndarray:
+    """CPU baseline of the PackedLinear fallback: dequantise per call + GEMV (common.py:414-428)."""
+    raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    y = np.empty(n_out, np.float32)
+    assert lib().or_deq_gemv_f32(fmt_id(fmt), _ptr(raw), n_out, n_in, _ptr(x), _ptr(y), threads) == 0
+    return y
+
+
+def rel_err_rows(y: np.ndarray, ref: np.ndarray) -> np.ndarray:
+    """Per output row-vector: max_i |y - ref| / max_i |ref| (test_gguf_iq.py:215 convention)."""
+    y = np.asarray(y, np.float64).reshape(-1, np.shape(ref)[-1])
+    ref = np.asarray(ref, np.float64).reshape(y.shape)
+    return np.abs(y - ref).max(axis=1) / np.maximum(np.abs(ref).max(axis=1), 1e-30)

@@ -1,0 +1,80 @@
+"""libnmq.so on the CPU: it loads, exports every entry point include/nmq.h declares, and rejects bad
+arguments before anything reaches a device (no compute call is made here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "nmq.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nmq_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    from ggufengine_amd import _native
+    return _native.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    names = declared_functions()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(L, n), n
+
+
+def test_format_table(L):
+    bv, bb = ctypes.c_int(), ctypes.c_int()
+    from ggufengine_amd.gguf_types import GGML_TYPES
+    for t, (name, v, b) in GGML_TYPES.items():
+        assert L.nmq_format_info(t, ctypes.byref(bv), ctypes.byref(bb)) == 0, name
+        assert (bv.value, bb.value) == (v, b), name
+    assert L.nmq_format_info(2, None, None) == -1          # Q4_0: not served
+    assert L.nmq_abi_version() == 1
+
+
+def test_rejects_bad_arguments_without_launching(L):
+    from ggufengine_amd import _native
+    buf = ctypes.create_string_buffer(4096)
+    a16 = (ctypes.addressof(buf) + 15) // 16 * 16
+    # NULL weight pointer, bad n_in, bad format, bad token count: all rejected before a launch
+    assert L.nmq_mv(12, None, a16, a16, a16, a16, a16, 4, 256, 1, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv(12, a16, a16, a16, a16, a16, a16, 4, 300, 1, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mv(13, a16, a16, a16, a16, a16, a16, 4, 256, 1, None) == _native.NMQ_ERR_FORMAT
+    assert L.nmq_mv(12, a16, a16, a16, a16, a16, a16, 4, 256, 0, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv(12, a16 + 2, a16, a16, a16, a16, a16, 4, 256, 1, None) == _native.NMQ_ERR_ARG  # Q4_K needs 16 B
+    assert L.nmq_mv(14, a16, a16 + 1, a16, a16, a16, a16, 4, 256, 1, None) == _native.NMQ_ERR_ARG  # xq alignment
+    assert L.nmq_quant_q8(a16, 1, a16, a16, a16, a16, 33, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mv_experts(12, a16, None, 2, 0, a16, a16, a16, a16, 1, a16, 4, 256, None) == _native.NMQ_ERR_ARG
+    # per-expert stride smaller than one matrix
+    assert L.nmq_mv_experts(12, a16, a16, 2, 144, a16, a16, a16, a16, 1, a16, 4, 256, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_dequant_bf16(12, a16, a16, 0, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_encode(12, None, 256, a16, 1) == _native.NMQ_ERR_ARG
+    assert b"block format" in L.nmq_strerror(-1)
+
+
+def test_python_api_without_gpu():
+    import torch
+    from ggufengine_amd import cudakern, mmvq, qlinear
+    from ggufengine_amd.gguf_types import GGUFError
+    if torch.cuda.is_available():
+        pytest.skip("CPU-only behaviour")
+    assert not mmvq.verfuegbar("cpu", "Q4_K", 4096)
+    assert not cudakern.verfuegbar("cpu", "IQ2_XXS", 4096)
+    assert not qlinear.kernel_available(torch.device("cpu"))
+    assert cudakern.mm_bis("cpu") == 1
+    with pytest.raises(ValueError):
+        cudakern.mm("Q8_0", torch.zeros(34, dtype=torch.uint8), torch.zeros(2, 32), 1, 32)
+    with pytest.raises(GGUFError):
+        qlinear.build_quant_linear(torch.zeros(100, dtype=torch.uint8), 12, 2, 256)
+    with pytest.raises(ValueError):
+        mmvq.Eingang(n=33, device="cpu")
+    assert qlinear.quantizable(12, 4096, 4096) and not qlinear.quantizable(16, 4096, 4096)
+    assert not mmvq.schritt_moeglich("cpu", 32, 8, 128)

@@ -1,0 +1,254 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each oracle function is checked by something other than a re-typing of its own formula:
+golden vectors built from the reference's tests and from the reference's kernel indexing
+(tests/golden/gen_golden.py), closed forms, invariants, exhaustive comparisons against numpy/torch,
+and brute force on small inputs.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN, random_blocks
+
+
+@pytest.fixture(scope="module")
+def gold():
+    with np.load(os.path.join(GOLDEN, "formats.npz"), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+# ---- scalar conversions ------------------------------------------------------------------------------
+
+def test_half_to_float_exhaustive(oracle):
+    bits = np.arange(65536, dtype=np.uint16)
+    got = oracle.half_to_float(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref)
+    assert np.array_equal(got[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isinf(got), np.isinf(ref))
+
+
+def test_round_bf16_matches_torch(oracle):
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(100000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 100000),
+                        np.array([0.0, -0.0, 1.0, 65504.0, 1e-40, 3.4e38], np.float32)]).astype(np.float32)
+    ref = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(oracle.round_bf16(x).view(np.uint32), ref.view(np.uint32))
+
+
+# ---- block formats --------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K"])
+def test_dequant_known_answer_blocks(oracle, gold, fmt):
+    """Blocks laid out by the reference's kernel indexing (cudakern.py) with exact expected values;
+    the oracle follows quant.py -- both readings of the layout must agree bit for bit."""
+    key = fmt.lower()
+    got = oracle.dequant(fmt, gold[f"known_{key}_raw"])
+    assert np.array_equal(got, gold[f"known_{key}_vals"])
+
+
+def test_dequant_iq2_xxs_reference_restatement(oracle, gold):
+    """tests/test_gguf_iq.py:43-54 `ref_iq2_xxs` on `zufallsbloecke` bytes, exact (:107-112)."""
+    assert np.array_equal(oracle.dequant("IQ2_XXS", gold["iq2_xxs_raw"]), gold["iq2_xxs_vals"])
+
+
+def test_dequant_tq2_0_reference_restatement(oracle, gold):
+    """tests/test_gguf_ternaer.py:62-69 `ref_tq2_0`, exact (:219-230)."""
+    assert np.array_equal(oracle.dequant("TQ2_0", gold["tq2_0_raw"]), gold["tq2_0_vals"])
+
+
+def test_tq2_0_pack_roundtrip_lossless(oracle, gold):
+    """pack_tq2_0 of ternary weights dequantises to the same weights (test_gguf_ternaer.py:239-245)."""
+    assert np.array_equal(oracle.dequant("TQ2_0", gold["tq2_0_ternary_raw"]), gold["tq2_0_ternary_w"])
+
+
+def test_iq2xxs_grid_invariants(gold):
+    """Table length (test_gguf_iq.py:125-128) and ggml's grid properties: sorted, distinct, every
+    byte one of 0x08, 0x19, 0x2b; the generated C tables equal the fixture's."""
+    g = gold["iq2xxs_grid"].astype(np.uint64)
+    assert g.size == 256 and np.all(np.diff(g.astype(object)) > 0)
+    b = set(int((int(v) >> (8 * j)) & 255) for v in g for j in range(8))
+    assert b == {0x08, 0x19, 0x2B}
+    root = os.path.dirname(GOLDEN)
+    for path in (os.path.join(root, "..", "oracle", "iq2xxs_grid.h"),
+                 os.path.join(root, "..", "nemicli-terminal_amd", "csrc", "iq2xxs_grid.inc")):
+        vals = [int(v, 16) for v in __import__("re").findall(r"0x([0-9a-f]{16})ull", open(path).read())]
+        assert vals == [int(v) for v in g], path
+
+
+def test_q4_k_scale_min_high_bits(oracle):
+    """Sub-blocks 4..7 take their scale's top two bits from bytes 0..3 and the min's from 4..7
+    (get_scale_min_k4): a block where only those bits are set must give sc = m = 48 there."""
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([1.0], np.float16).view(np.uint8)   # d = 1
+    b[2:4] = np.array([1.0], np.float16).view(np.uint8)   # dmin = 1
+    b[4:8] = 0xC0       # top bits of sc[4..7] = 3 -> 48
+    b[8:12] = 0xC0      # top bits of m[4..7] = 3 -> 48
+    b[16:144] = 0x11    # every nibble 1
+    v = oracle.dequant("Q4_K", b)
+    assert np.all(v[:128] == 0.0)              # sub-blocks 0..3: sc = m = 0
+    assert np.all(v[128:] == 48.0 * 1 - 48.0)  # d*sc*q - dmin*m = 0 as well ...
+    b[16 + 64:16 + 128] = 0x22                 # ... nibble 2 in groups 2, 3: 96 - 48
+    assert np.all(oracle.dequant("Q4_K", b)[128:] == 48.0)
+
+
+def test_q6_k_sign_and_offset(oracle):
+    """q = 0 -> -32 * d * sc and q = 63 -> +31 * d * sc, with a negative int8 sub-scale."""
+    b = np.zeros(210, np.uint8)
+    b[192:208] = np.array([-3] * 16, np.int8).view(np.uint8)
+    b[208:210] = np.array([0.5], np.float16).view(np.uint8)
+    assert np.all(oracle.dequant("Q6_K", b) == 0.5 * -3 * -32)
+    b[:192] = 0xFF
+    assert np.all(oracle.dequant("Q6_K", b) == 0.5 * -3 * 31)
+
+
+# ---- two-stage activation ----------------------------------------------------------------------------
+
+def _quant_numpy(x):
+    """Independent restatement with numpy float32 ops; the fused residual as exact float64
+    arithmetic rounded once to float32."""
+    x = x.astype(np.float32).reshape(-1, 32)
+    a = np.abs(x).max(axis=1, keepdims=True)
+    d = (a / np.float32(127)).astype(np.float32)
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = np.where(d > 0, np.rint(x / d), 0).astype(np.int32)
+        r = (x.astype(np.float64) - q.astype(np.float64) * d.astype(np.float64)).astype(np.float32)
+        s2 = (d * np.float32(1.0 / 254.0)).astype(np.float32)
+        q2 = np.where(d > 0, np.clip(np.rint(r / s2), -127, 127), 0).astype(np.int32)
+    t = x.copy()
+    o = 16
+    while o:
+        t[:, :o] = t[:, :o] + t[:, o:2 * o]
+        o //= 2
+    return q.astype(np.int8).ravel(), q2.astype(np.int8).ravel(), d.ravel(), t[:, 0]
+
+
+def test_quant_q8_closed_forms(oracle):
+    x = np.zeros(96, np.float32)
+    x[:32] = 0.75                       # all equal: d = a/127, q = 127, q2 = 0
+    x[64 + 5] = -2.0                    # single spike, others 0
+    xq, xq2, xd, xs = oracle.quant_q8(x)
+    assert np.all(xq[:32] == 127) and np.all(xq2[:32] == 0)
+    assert xd[0] == np.float32(0.75) / np.float32(127) and xs[0] == np.float32(24.0)
+    assert np.all(xq[32:64] == 0) and np.all(xq2[32:64] == 0) and xd[1] == 0 and xs[1] == 0
+    assert xq[69] == -127 and np.all(np.delete(xq[64:], 5) == 0) and xs[2] == -2.0
+
+
+def test_quant_q8_matches_numpy_and_bound(oracle):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(32 * 4096) * np.repeat(10.0 ** rng.uniform(-3, 2, 4096), 32)).astype(np.float32)
+    got = oracle.quant_q8(x)
+    ref = _quant_numpy(x)
+    for g, r in zip(got, ref):
+        assert np.array_equal(np.ascontiguousarray(g).view(np.uint8), np.ascontiguousarray(r).view(np.uint8))
+    xq, xq2, xd, xs = got
+    d = np.repeat(xd, 32).astype(np.float64)
+    rec = xq * d + xq2 * d / 254.0
+    # two stages: |x - reconstruction| <= d/508 plus fp32 rounding of the residual
+    assert np.all(np.abs(rec - x) <= d / 508.0 * 1.001 + 1e-30)
+    assert np.max(np.abs(xs - x.reshape(-1, 32).astype(np.float64).sum(1)) / np.abs(x).reshape(-1, 32).sum(1)) < 1e-6
+
+
+# ---- integer decomposition and the two mat-vec oracles -----------------------------------------------
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
+def test_block_sums_brute_force(oracle, fmt):
+    """s1/s2 per 16 values equal sums over integer weights recovered from the exact dequantised
+    values (value / per-group factor, + min for Q4_K): exact integer arithmetic."""
+    n_out, n_in = 3, 512
+    bv, bb = {"Q8_0": (32, 34)}.get(fmt, (256, {"Q4_K": 144, "Q6_K": 210}.get(fmt, 66)))
+    raw = random_blocks(fmt, n_out * n_in // bv, seed=5)
+    rng = np.random.default_rng(6)
+    xq = rng.integers(-127, 128, n_in).astype(np.int8)
+    xq2 = rng.integers(-127, 128, n_in).astype(np.int8)
+    s1, s2 = oracle.block_sums(fmt, raw, n_out, n_in, xq, xq2)
+    w = _int_weights(oracle, fmt, raw, n_out, n_in)
+    e1 = (w.astype(np.int64) * xq).reshape(n_out, -1, 16).sum(-1)
+    e2 = (w.astype(np.int64) * xq2).reshape(n_out, -1, 16).sum(-1)
+    assert np.array_equal(s1, e1) and np.array_equal(s2, e2)
+
+
+def _int_weights(oracle, fmt, raw, n_out, n_in):
+    """Integer weights from the dequantised values of blocks whose factors are rebuilt here from
+    the raw bytes in the layout of the reference's quant.py (Q4_K scales via get_scale_min_k4)."""
+    deq = oracle.dequant(fmt, raw).astype(np.float64).reshape(n_out, n_in)
+    if fmt == "Q8_0":
+        b = raw.reshape(-1, 34)
+        d = b[:, :2].copy().view(np.float16).astype(np.float64)
+        return np.rint(deq.reshape(-1, 32) / d).astype(np.int64).reshape(n_out, n_in)
+    if fmt == "TQ2_0":
+        b = raw.reshape(-1, 66)
+        d = b[:, 64:66].copy().view(np.float16).astype(np.float64)
+        return np.rint(deq.reshape(-1, 256) / d).astype(np.int64).reshape(n_out, n_in)
+    if fmt == "Q6_K":
+        b = raw.reshape(-1, 210)
+        d = b[:, 208:210].copy().view(np.float16).astype(np.float64)
+        sc = b[:, 192:208].copy().view(np.int8).astype(np.float64)
+        f = np.repeat(d * sc, 16, axis=1)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            w = np.where(f != 0, np.rint(deq.reshape(-1, 256) / f), 0)
+        # zero factor: the integer q - 32 is not recoverable from the value; rebuild it from bits
+        q = _q6_from_bits(b)
+        w = np.where(f != 0, w, q)
+        assert np.array_equal(w, q)   # both routes agree where the factor is nonzero
+        return w.astype(np.int64).reshape(n_out, n_in)
+    if fmt == "Q4_K":
+        b = raw.reshape(-1, 144)
+        qs = b[:, 16:].reshape(-1, 4, 32)
+        q = np.stack([qs & 15, qs >> 4], axis=2).reshape(-1, 256)   # sub-block 2i low, 2i+1 high
+        return q.astype(np.int64).reshape(n_out, n_in)
+    if fmt == "IQ2_XXS":
+        b = raw.reshape(-1, 66)
+        d = b[:, :2].copy().view(np.float16).astype(np.float64)
+        aux1 = b[:, 2:].reshape(-1, 8, 8)[:, :, 4:].copy().view(np.uint32).reshape(-1, 8)
+        db = d * (0.125 + 0.25 * (aux1 >> 28))
+        f = np.repeat(db, 32, axis=1)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            w = np.rint(deq.reshape(-1, 256) / f)
+        assert np.all(np.isin(np.abs(w), [8, 25, 43]))
+        return w.astype(np.int64).reshape(n_out, n_in)
+    raise KeyError(fmt)
+
+
+def _q6_from_bits(b):
+    ql, qh = b[:, :128].astype(np.int64), b[:, 128:192].astype(np.int64)
+    out = np.zeros((b.shape[0], 256), np.int64)
+    for n in range(2):
+        for k, (lo_src, lo_sh, hi_sh) in enumerate(((0, 0, 0), (32, 0, 2), (0, 4, 4), (32, 4, 6))):
+            lo = (ql[:, 64 * n + lo_src:64 * n + lo_src + 32] >> lo_sh) & 15
+            hi = (qh[:, 32 * n:32 * n + 32] >> hi_sh) & 3
+            out[:, 128 * n + 32 * k:128 * n + 32 * k + 32] = (lo | (hi << 4)) - 32
+    return out
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
+def test_mv_int_agrees_with_dequant_matmul(oracle, fmt):
+    """The integer-decomposition mat-vec (what the kernels compute, combined in fp64) and the
+    dequantise+matmul path agree to the two-stage input's precision; a wrong factor, sign or
+    dropped min term would show as an O(1) relative error."""
+    n_out, n_in = 64, 1024
+    bv = 32 if fmt == "Q8_0" else 256
+    raw = random_blocks(fmt, n_out * n_in // bv, seed=9)
+    x = np.random.default_rng(10).standard_normal((2, n_in)).astype(np.float32)
+    xq, xq2, xd, xs = oracle.quant_q8(x)
+    y_int = oracle.mv_int(fmt, raw, n_out, n_in, xq, xq2, xd, xs, ncols=2)
+    y_deq = oracle.mv_deq(fmt, raw, n_out, n_in, x)
+    assert oracle.rel_err_rows(y_int, y_deq).max() < 1e-4
+    # and the dequant path itself against a float64 numpy matmul of the dequantised matrix
+    w = oracle.dequant(fmt, raw).astype(np.float64).reshape(n_out, n_in)
+    assert np.allclose(y_deq, x.astype(np.float64) @ w.T, rtol=1e-12, atol=1e-12)
+
+
+def test_cpu_baseline_gemv(oracle):
+    rng = np.random.default_rng(2)
+    w = rng.standard_normal((300, 1280)).astype(np.float32)
+    x = rng.standard_normal(1280).astype(np.float32)
+    y = oracle.gemv_f32(w, x, threads=2)
+    assert np.allclose(y, w.astype(np.float64) @ x, rtol=1e-4, atol=1e-4)
+    raw = random_blocks("TQ2_0", 300 * 1280 // 256, seed=3)
+    y2 = oracle.deq_gemv_f32("TQ2_0", raw, 300, 1280, x, threads=2)
+    assert np.allclose(y2, oracle.mv_deq("TQ2_0", raw, 300, 1280, x)[0], rtol=1e-4, atol=1e-5)

@@ -43,10 +43,23 @@ __device__ __forceinline__ int dot4(u32 a, u32 b, int c) {
 
 __device__ __forceinline__ u32 bfe(u32 v, u32 off, u32 len) { return __builtin_amdgcn_ubfe(v, off, len); }
 
-__device__ __forceinline__ u32x4 ld4(const u8* p) { return *(const u32x4_a2*)p; }
-__device__ __forceinline__ u32x2 ld2(const u8* p) { return *(const u32x2_a2*)p; }
-__device__ __forceinline__ u32 ld1(const u8* p) { return *(const u32_a2*)p; }
-__device__ __forceinline__ u32 ld16(const u8* p) { return *(const u16*)p; }
+// Every pointer the kernels dereference in device memory is cast to the global address space, so
+// the loads are global_load (counted by vmcnt only) rather than flat loads, whose completion would
+// also hold back the waits for LDS reads.
+#define NMQ_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ const NMQ_GLOBAL T* gp(const void* p) {
+    return (const NMQ_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ NMQ_GLOBAL T* gpw(void* p) {
+    return (NMQ_GLOBAL T*)p;
+}
+__device__ __forceinline__ u32x4 ld4(const u8* p) { return *gp<u32x4_a2>(p); }
+__device__ __forceinline__ u32x4 ld4a(const u8* p) { return *gp<u32x4>(p); }  // 16-byte aligned
+__device__ __forceinline__ u32x2 ld2(const u8* p) { return *gp<u32x2_a2>(p); }
+__device__ __forceinline__ u32 ld1(const u8* p) { return *gp<u32_a2>(p); }
+__device__ __forceinline__ u32 ld16(const u8* p) { return *gp<u16>(p); }
 
 // q - 32 per byte for bytes 0..63 (Q6_K): ((q | 0x80) - 0x20) ^ 0x80 never borrows across bytes.
 __device__ __forceinline__ u32 sub32x4(u32 v) { return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
@@ -121,9 +134,9 @@ struct Fmt<NMQ_Q4_K> {
     __device__ static void load(const u8* row, int u, int /*row_units*/, Raw& r) {
         const u8* blk = row + (u >> 2) * BB;
         const int i = u & 3;
-        r.h = *(const u32x4*)blk;  // d, dmin, scales[12]: 16-byte aligned when the row is
-        r.a = *(const u32x4*)(blk + 16 + 32 * i);
-        r.b = *(const u32x4*)(blk + 32 + 32 * i);
+        r.h = ld4a(blk);  // d, dmin, scales[12]: 16-byte aligned when the row is
+        r.a = ld4a(blk + 16 + 32 * i);
+        r.b = ld4a(blk + 32 + 32 * i);
     }
     __device__ static void decode(const Raw& r, int u, const u64* /*tab*/, WUnit& o) {
         const u32 q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
@@ -153,6 +166,36 @@ struct Fmt<NMQ_Q4_K> {
         o.wm[1] = dmin * mn[1];
     }
 };
+
+// One-token fast path of Q4_K (mv1): decode and dot fused, branch free.  All eight 6-bit scales and
+// mins of the block are formed four at a time inside dwords (get_scale_min_k4 without byte loops):
+//   sc[0..3] = scales[0..3] & 63              m[0..3] = scales[4..7] & 63
+//   sc[4..7] = (scales[8..11] & 15) | (scales[0..3] >> 6) << 4
+//   m[4..7]  = (scales[8..11] >> 4) | (scales[4..7] >> 6) << 4
+// and the lane's two (sub-blocks 2i, 2i+1 = bytes t0, t0+1 of the low or high dword) are converted
+// straight from their bytes.  Runs 0,1 and 2,3 are summed in one dot4 chain each.
+__device__ __forceinline__ float q4k_dot1(const Fmt<NMQ_Q4_K>::Raw& r, const XSlice& x, bool hi, u32 t0sh) {
+    const u32 sl = r.h.y & 0x3f3f3f3fu, ml = r.h.z & 0x3f3f3f3fu;
+    const u32 sh = (r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u);
+    const u32 mh = ((r.h.w >> 4) & 0x0f0f0f0fu) | ((r.h.z >> 2) & 0x30303030u);
+    const u32 sv = (hi ? sh : sl) >> t0sh, mv = (hi ? mh : ml) >> t0sh;
+    const float sc0 = (float)(sv & 0xffu), sc1 = (float)((sv >> 8) & 0xffu);  // v_cvt_f32_ubyte0/1
+    const float m0 = (float)(mv & 0xffu), m1 = (float)((mv >> 8) & 0xffu);
+    const u32 q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    int a0 = 0, a1 = 0, b0 = 0, b1 = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const u32 lo = q[k] & 0x0f0f0f0fu, hn = (q[k] >> 4) & 0x0f0f0f0fu;
+        a0 = dot4(lo, x.q[k], a0);
+        b0 = dot4(lo, x.q2[k], b0);
+        a1 = dot4(hn, x.q[8 + k], a1);
+        b1 = dot4(hn, x.q2[8 + k], b1);
+    }
+    const float g0 = x.d[0] * ((float)a0 + FEIN * (float)b0);
+    const float g1 = x.d[1] * ((float)a1 + FEIN * (float)b1);
+    const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+    return d * (sc0 * g0 + sc1 * g1) - dmin * (m0 * x.s[0] + m1 * x.s[1]);
+}
 
 // Q6_K, 210-byte blocks (quant.py:140-159, mmvq.py:421-482): unit u = 4b + 2h + j takes
 // l = 16j .. 16j+15 of half h: ql[64h + l], ql[64h + 32 + l], qh[32h + l]; runs k = 0..3 are the
@@ -212,16 +255,16 @@ struct Fmt<NMQ_Q8_0> {
         const u32x4 a = ld4(p), b = ld4(p + 16);
         r.v[0] = a.x; r.v[1] = a.y; r.v[2] = a.z; r.v[3] = a.w;
         r.v[4] = b.x; r.v[5] = b.y; r.v[6] = b.z; r.v[7] = b.w;
-        if (2 * u + 1 < nblk) {
-            r.v[8] = ld1(p + 32);  // qs[30], qs[31] of block 0 and d of block 1
-            const u32x4 c = ld4(p + 36), e = ld4(p + 52);
-            r.v[9] = c.x; r.v[10] = c.y; r.v[11] = c.z; r.v[12] = c.w;
-            r.v[13] = e.x; r.v[14] = e.y; r.v[15] = e.z; r.v[16] = e.w;
-        } else {
-            r.v[8] = ld16(p + 32);  // only qs[30], qs[31]: block 1 is past the row end
-#pragma unroll
-            for (int k = 9; k < 17; ++k) r.v[k] = 0u;
-        }
+        // Block 1 is past the row end when the row has an odd number of blocks and u is its last
+        // unit: then block 0 is read a second time (a valid address, no branch around the loads)
+        // and the words are cleared.
+        const bool two = 2 * u + 1 < nblk;
+        const u8* p1 = two ? p + 32 : p;
+        const u32 v8 = ld1(p1), lo16 = ld16(p + 32);
+        const u32x4 c = ld4(p1 + 4), e = ld4(p1 + 20);
+        r.v[8] = two ? v8 : lo16;  // qs[30], qs[31] of block 0 (and d of block 1)
+        r.v[9] = two ? c.x : 0u; r.v[10] = two ? c.y : 0u; r.v[11] = two ? c.z : 0u; r.v[12] = two ? c.w : 0u;
+        r.v[13] = two ? e.x : 0u; r.v[14] = two ? e.y : 0u; r.v[15] = two ? e.z : 0u; r.v[16] = two ? e.w : 0u;
     }
     __device__ static void decode(const Raw& r, int /*u*/, const u64* /*tab*/, WUnit& o) {
 #pragma unroll

@@ -14,6 +14,8 @@
 // address table entry ids[m] when per_expert < 0) and it reads the input row m / x_group.
 #pragma once
 
+#include <stdlib.h>
+
 #include "nmq_device.hpp"
 
 namespace nmq {
@@ -55,8 +57,8 @@ __device__ __forceinline__ void stage_tile(u8* lds, const int8_t* xq, const int8
         for (int ch = tid; ch < ktp / 16; ch += nt) {
             u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
             if (ch * 16 < kt) {
-                a = *(const u32x4*)(q + 16 * ch);
-                b = *(const u32x4*)(q2 + 16 * ch);
+                a = *gp<u32x4>(q + 16 * ch);
+                b = *gp<u32x4>(q2 + 16 * ch);
             }
             const int ph = swz<STRIDED>(ch);
             *(u32x4*)(base + 16 * ph) = a;
@@ -67,8 +69,8 @@ __device__ __forceinline__ void stage_tile(u8* lds, const int8_t* xq, const int8
         const int64_t g0 = ((int64_t)c * n_in + k0) / 32;
         for (int i = tid; i < ktp / 32; i += nt) {
             const bool ok = i < kt / 32;
-            d[i] = ok ? xd[g0 + i] : 0.f;
-            s[i] = ok ? xs[g0 + i] : 0.f;
+            d[i] = ok ? gp<float>(xd)[g0 + i] : 0.f;
+            s[i] = ok ? gp<float>(xs)[g0 + i] : 0.f;
         }
     }
 }
@@ -120,19 +122,24 @@ template <int F, int NC, int T, int RW>
 __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
     using FM = Fmt<F>;
     constexpr bool S = FM::STRIDED;
-    constexpr int P = 64 / T;
+    constexpr int TW = T > 64 ? T / 64 : 1;  // waves per team
+    constexpr int P = T < 64 ? 64 / T : 1;   // teams per wave
+    constexpr int TL = T < 64 ? T : 64;      // lanes of a team inside one wave
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    __shared__ float red[T > 64 ? 4 * RW * NC : 1];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, W = blockDim.x >> 6;
-    const int team = lane / T, lt = lane % T;
+    const int team = T >= 64 ? wave / TW : wave * P + lane / T;
+    const int lt = T >= 64 ? (wave % TW) * 64 + lane : lane % T;
+    const int teams = T >= 64 ? W / TW : W * P;
     const int m = blockIdx.y;
 
     const u8* wbase = p.w;
     int64_t xrow = 0;
     if (p.ids) {
-        const int64_t e = p.ids[m];
-        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(((const int64_t*)p.w)[e]);
+        const int64_t e = gp<int64_t>(p.ids)[m];
+        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
         xrow = m / p.x_group;
     }
     const int8_t* xq = p.xq + xrow * p.n_in;
@@ -143,11 +150,11 @@ __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
 
     fill_tables<F>(tab);
     const int tok = (p.ktp * 9) / 4;
-    const int rows_iter = W * P * RW;
+    const int rows_iter = teams * RW;
     const int row_wg = blockIdx.x * p.groups * rows_iter;
 
     for (int g = 0; g < p.groups; ++g) {
-        const int r0 = row_wg + g * rows_iter + (wave * P + team) * RW;
+        const int r0 = row_wg + g * rows_iter + team * RW;
         float acc[RW][NC];
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
@@ -160,27 +167,37 @@ __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
         for (int tile = 0; tile < p.n_tiles; ++tile) {
             const int k0 = tile * p.kt;
             const int kt = min(p.kt, p.n_in - k0);
+            const int U = (kt + 63) >> 6;
+            const int u0 = k0 >> 6;
+            const int nit = (U + T - 1) / T;
+            // the first unit's weights of all RW rows are requested before the input is staged
+            typename FM::Raw raw[RW];
+            if (lt < U) {
+#pragma unroll
+                for (int rr = 0; rr < RW; ++rr) FM::load(rowp[rr], u0 + lt, p.nblk, raw[rr]);
+            }
             if (p.n_tiles > 1 || g == 0) {
                 __syncthreads();
                 stage_tile<S>(lds, xq, xq2, xd, xs, p.n_in, NC, k0, kt, p.ktp);
                 __syncthreads();
             }
-            const int U = (kt + 63) >> 6;
-            const int u0 = k0 >> 6;
-            for (int u = lt; u < U; u += T) {
-                WUnit wu[RW];
+            for (int it = 0; it < nit; ++it) {
+                const int u = lt + it * T;
+                if (u < U) {
+                    if (it > 0) {
 #pragma unroll
-                for (int rr = 0; rr < RW; ++rr) {
-                    typename FM::Raw raw;
-                    FM::load(rowp[rr], u0 + u, p.nblk, raw);
-                    FM::decode(raw, u0 + u, tab, wu[rr]);
-                }
+                        for (int rr = 0; rr < RW; ++rr) FM::load(rowp[rr], u0 + u, p.nblk, raw[rr]);
+                    }
+                    WUnit wu[RW];
 #pragma unroll
-                for (int c = 0; c < NC; ++c) {
-                    XSlice x;
-                    read_slice<S>(lds + c * tok, p.ktp, u, x);
+                    for (int rr = 0; rr < RW; ++rr) FM::decode(raw[rr], u0 + u, tab, wu[rr]);
 #pragma unroll
-                    for (int rr = 0; rr < RW; ++rr) acc[rr][c] += unit_dot<S, FM::HAS_MIN>(wu[rr], x);
+                    for (int c = 0; c < NC; ++c) {
+                        XSlice x;
+                        read_slice<S>(lds + c * tok, p.ktp, u, x);
+#pragma unroll
+                        for (int rr = 0; rr < RW; ++rr) acc[rr][c] += unit_dot<S, FM::HAS_MIN>(wu[rr], x);
+                    }
                 }
             }
         }
@@ -190,20 +207,226 @@ __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
             for (int c = 0; c < NC; ++c) {
                 float v = acc[rr][c];
 #pragma unroll
-                for (int o = T / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
+                for (int o = TL / 2; o > 0; o >>= 1) v += __shfl_xor(v, o);
                 acc[rr][c] = v;
             }
-        if (lt == 0) {
+        if (T > 64) {
+            // teams span TW waves: lane 0 of every wave posts its sums, the team's first wave adds them
+            if (lane == 0) {
+#pragma unroll
+                for (int rr = 0; rr < RW; ++rr)
+#pragma unroll
+                    for (int c = 0; c < NC; ++c) red[(wave * RW + rr) * NC + c] = acc[rr][c];
+            }
+            __syncthreads();
+            if (wave % TW == 0 && lane < RW * NC) {
+                const int rr = lane / NC, c = lane % NC;
+                float v = 0.f;
+#pragma unroll
+                for (int w2 = 0; w2 < TW; ++w2) v += red[((wave + w2) * RW + rr) * NC + c];
+                const int row = r0 + rr;
+                if (row < p.n_out) gpw<float>(y)[(int64_t)c * p.n_out + row] = v;
+            }
+            __syncthreads();
+        } else if (lt == 0) {
 #pragma unroll
             for (int rr = 0; rr < RW; ++rr) {
                 const int row = r0 + rr;
                 if (row < p.n_out) {
 #pragma unroll
-                    for (int c = 0; c < NC; ++c) y[(int64_t)c * p.n_out + row] = acc[rr][c];
+                    for (int c = 0; c < NC; ++c) gpw<float>(y)[(int64_t)c * p.n_out + row] = acc[rr][c];
                 }
             }
         }
     }
+}
+
+// ---- one token: x slice in registers, rows streamed with one step of prefetch ------------------
+// For NC = 1 a lane's units of the row (u = lt + it*T) are the same for every row, so its slice of
+// the input is read once into registers.  The input is staged once per workgroup in LDS (one copy
+// per CU rather than one per wave from L2).  Waves are persistent: wave gw of nw handles row steps
+// gw, gw + nw, ... (a step = P teams x RW rows) and requests the next step's weights before it
+// computes the current one, so HBM traffic and VALU work overlap.
+
+// Sum over the T lanes of a team (T = 16, 32 or 64): DPP within rows of 16, then xor shuffles.
+template <int T>
+__device__ __forceinline__ float team_sum(float v) {
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));  // xor 1
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // xor 2
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));  // 8-lane mirror
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));  // 16-lane mirror
+    if (T >= 32) v += __shfl_xor(v, 16);
+    if (T >= 64) v += __shfl_xor(v, 32);
+    return v;
+}
+
+template <int F, int T, int RW, int NITM>
+struct Mv1Step {
+    using FM = Fmt<F>;
+    typename FM::Raw raw[RW][NITM];
+    // Rows at or past n_out are replaced by row fb + rr (a row this wave has just read, so the
+    // surplus loads of the last steps hit cache lines nearby instead of all waves' one last row).
+    __device__ __forceinline__ void load(const u8* wbase, int64_t row_bytes, int r0, int n_out, int lt, int U,
+                                         int nblk, int fb) {
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) {
+            const int r = r0 + rr < n_out ? r0 + rr : min(fb + rr, n_out - 1);
+            const u8* rp = wbase + (int64_t)r * row_bytes;
+#pragma unroll
+            for (int it = 0; it < NITM; ++it) FM::load(rp, min(lt + it * T, U - 1), nblk, raw[rr][it]);
+        }
+    }
+};
+
+// Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
+struct LaneConst {
+    bool hi[4];     // Q4_K: the unit's sub-blocks are 4..7
+    u32 t0sh[4];    // Q4_K: bit offset of the first of its two scale bytes
+};
+
+template <int F, int T, int NITM>
+__device__ __forceinline__ LaneConst lane_const(int lt) {
+    LaneConst c{};
+#pragma unroll
+    for (int it = 0; it < NITM && it < 4; ++it) {
+        const int i = (lt + it * T) & 3;
+        c.hi[it] = i >= 2;
+        c.t0sh[it] = (u32)(8 * ((2 * i) & 3));
+    }
+    return c;
+}
+
+template <int F>
+__device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int u, const u64* tab, const XSlice& x,
+                                           const LaneConst& lc, int it) {
+    using FM = Fmt<F>;
+    if constexpr (F == NMQ_Q4_K) {
+        return q4k_dot1(raw, x, lc.hi[it], lc.t0sh[it]);
+    } else {
+        WUnit wu;
+        FM::decode(raw, u, tab, wu);
+        return unit_dot<FM::STRIDED, FM::HAS_MIN>(wu, x);
+    }
+}
+
+template <int F, int T, int RW, int NITM>
+__device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, const XSlice (&x)[NITM], int r0,
+                                            int n_out, int lt, int U, const u64* tab, float* y,
+                                            const LaneConst& lc) {
+    float acc[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+        acc[rr] = 0.f;
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            const int u = lt + it * T;
+            const float v = unit_dot1<F>(st.raw[rr][it], min(u, U - 1), tab, x[it], lc, it);
+            acc[rr] += u < U ? v : 0.f;
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) acc[rr] = team_sum<T>(acc[rr]);
+    if (lt == 0) {
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr)
+            if (r0 + rr < n_out) gpw<float>(y)[r0 + rr] = acc[rr];
+    }
+}
+
+template <int F, int T, int RW, int NITM>
+__global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
+    using FM = Fmt<F>;
+    constexpr int P = 64 / T;
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int team = lane / T, lt = lane % T;
+    const int m = blockIdx.y;
+    const u8* wbase = p.w;
+    int64_t xrow = 0;
+    if (p.ids) {
+        const int64_t e = gp<int64_t>(p.ids)[m];
+        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
+        xrow = m / p.x_group;
+    }
+    float* y = p.y + (int64_t)m * p.n_out;
+    const int U = (p.n_in + 63) >> 6;
+    const int gw = blockIdx.x * W + wave, nw = gridDim.x * W;
+    constexpr int SR = P * RW;  // rows per step
+    const int off = team * RW;
+
+    // Loads are issued unconditionally (rows and units clamped to valid addresses, surplus results
+    // discarded), so the compiler can wait for exactly the oldest step and keep the others in flight.
+    // Three step buffers rotate: while one step is computed, the next two are in flight.
+    Mv1Step<F, T, RW, NITM> a, b, c;
+    const int stride = nw * SR;
+    int base = gw * SR;
+    a.load(wbase, p.row_bytes, base + off, p.n_out, lt, U, p.nblk, base + off);
+    b.load(wbase, p.row_bytes, base + stride + off, p.n_out, lt, U, p.nblk, base + off);
+
+    fill_tables<F>(tab);
+    stage_tile<FM::STRIDED>(lds, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
+                            p.xs + xrow * (p.n_in / 32), p.n_in, 1, 0, p.n_in, p.ktp);
+    __syncthreads();
+    XSlice x[NITM];
+#pragma unroll
+    for (int it = 0; it < NITM; ++it) {
+        const int u = lt + it * T;
+        if (u < U) read_slice<FM::STRIDED>(lds, p.ktp, u, x[it]);
+    }
+
+    const LaneConst lc = lane_const<F, T, NITM>(lt);
+    while (base < p.n_out) {  // wave-uniform
+        c.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
+        mv1_compute<F, T, RW, NITM>(a, x, base + off, p.n_out, lt, U, tab, y, lc);
+        base += stride;
+        if (base >= p.n_out) break;
+        a.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
+        mv1_compute<F, T, RW, NITM>(b, x, base + off, p.n_out, lt, U, tab, y, lc);
+        base += stride;
+        if (base >= p.n_out) break;
+        b.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
+        mv1_compute<F, T, RW, NITM>(c, x, base + off, p.n_out, lt, U, tab, y, lc);
+        base += stride;
+    }
+}
+
+// ---- one token, one chunk per wave -------------------------------------------------------------
+// Each wave owns one chunk of P*RW rows: it requests all of the chunk's weights first (before the
+// input is staged, so the HBM latency overlaps the staging), then computes the rows in order as
+// their data arrives.  Used when the matrix fits in the resident waves of one launch (then every
+// weight byte of the matvec is in flight at once, the shape a streaming read needs at this size).
+template <int F, int T, int RW>
+__global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
+    using FM = Fmt<F>;
+    constexpr int P = 64 / T;
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    // the wave index is uniform across the wave: readfirstlane lets the row addressing run on SALU
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int team = lane / T, lt = lane % T;
+    const int m = blockIdx.y;
+    const u8* wbase = p.w;
+    int64_t xrow = 0;
+    if (p.ids) {
+        const int64_t e = gp<int64_t>(p.ids)[m];
+        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
+        xrow = m / p.x_group;
+    }
+    float* y = p.y + (int64_t)m * p.n_out;
+    const int U = (p.n_in + 63) >> 6;
+    const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
+    Mv1Step<F, T, RW, 1> a;
+    a.load(wbase, p.row_bytes, r0, p.n_out, lt, U, p.nblk, r0);
+
+    fill_tables<F>(tab);
+    stage_tile<FM::STRIDED>(lds, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
+                            p.xs + xrow * (p.n_in / 32), p.n_in, 1, 0, p.n_in, p.ktp);
+    __syncthreads();
+    XSlice x[1];
+    read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
+    const LaneConst lc = lane_const<F, T, 1>(lt);
+    mv1_compute<F, T, RW, 1>(a, x, r0, p.n_out, lt, U, tab, y, lc);
 }
 
 // ---- host side --------------------------------------------------------------------------------
@@ -221,22 +444,192 @@ inline MvKernel pick_t(int T) {
     switch (T) {
         case 16: return mv_kernel<F, NC, 16, RW>;
         case 32: return mv_kernel<F, NC, 32, RW>;
-        default: return mv_kernel<F, NC, 64, RW>;
+        case 64: return mv_kernel<F, NC, 64, RW>;
+        case 128: return mv_kernel<F, NC, 128, RW>;
+        default: return mv_kernel<F, NC, 256, RW>;
     }
 }
 
-template <int F>
-inline MvKernel pick_kernel(int nc, int T) {
-    switch (nc) {
-        case 1: return pick_t<F, 1, 1>(T);
-        case 2: return pick_t<F, 2, 2>(T);
-        case 3: return pick_t<F, 3, 2>(T);
-        case 4: return pick_t<F, 4, 2>(T);
-        case 5: return pick_t<F, 5, 2>(T);
-        case 6: return pick_t<F, 6, 2>(T);
-        case 7: return pick_t<F, 7, 2>(T);
-        default: return pick_t<F, 8, 2>(T);
+template <int F, int NC>
+inline MvKernel pick_rw(int rw, int T) {
+    if (NC <= 2) {
+        switch (rw) {
+            case 1: return pick_t<F, NC, 1>(T);
+            case 2: return pick_t<F, NC, 2>(T);
+            default: return pick_t<F, NC, 4>(T);
+        }
     }
+    return rw == 1 ? pick_t<F, NC, 1>(T) : pick_t<F, NC, 2>(T);
+}
+
+template <int F>
+inline MvKernel pick_kernel(int nc, int rw, int T) {
+    switch (nc) {
+        case 1: return pick_rw<F, 1>(rw, T);
+        case 2: return pick_rw<F, 2>(rw, T);
+        case 3: return pick_rw<F, 3>(rw, T);
+        case 4: return pick_rw<F, 4>(rw, T);
+        case 5: return pick_rw<F, 5>(rw, T);
+        case 6: return pick_rw<F, 6>(rw, T);
+        case 7: return pick_rw<F, 7>(rw, T);
+        default: return pick_rw<F, 8>(rw, T);
+    }
+}
+
+// Launch shape for one call (exposed for the tuning tests): team width T (lanes per row), rows per
+// team RW, waves per workgroup W, row groups per workgroup and the K tile.
+struct MvShape {
+    int T, rw, W, groups, kt, ktp, n_tiles, grid_x;
+    size_t lds;
+};
+
+template <int F>
+inline MvShape plan_mv(int n_out, int n_in, int nc, int n_mats, const DeviceInfo& di) {
+    using FM = Fmt<F>;
+    MvShape s{};
+    // K tile: the whole row when the input of all tokens fits the LDS budget
+    const int budget = nc == 1 ? 40 * 1024 : di.lds_max;
+    const int step = FM::BV == 256 ? 256 : 64;
+    int kt = (int)((int64_t)budget * 4 / 9 / nc) / 128 * 128 / step * step;
+    if (kt < step) kt = step;
+    if (kt >= n_in) kt = n_in;
+    s.kt = kt;
+    s.ktp = (kt + 127) / 128 * 128;
+    s.n_tiles = (n_in + kt - 1) / kt;
+    const int U = (kt + 63) / 64;  // units per row in a tile
+    s.T = U <= 16 ? 16 : U <= 32 ? 32 : U <= 64 ? 64 : U <= 128 ? 128 : 256;
+    // rows per team: as many as keep >= 8 (RW=4) or >= 4 (RW=2) waves per CU busy
+    const int64_t rows = (int64_t)n_out * n_mats;
+    auto waves = [&](int rw) { return (rows + rw - 1) / rw * s.T / 64; };
+    const int rw_max = nc <= 2 ? 4 : 2;
+    s.rw = 1;
+    if (rw_max >= 4 && waves(4) >= 8 * di.cus) s.rw = 4;
+    else if (waves(2) >= 4 * di.cus) s.rw = 2;
+    const int TW = s.T > 64 ? s.T / 64 : 1;
+    const int P = s.T < 64 ? 64 / s.T : 1;
+    int W = 4;
+    // fewer waves per workgroup for small problems, so that more workgroups spread over the CUs
+    while (W > TW && (int64_t)(n_out + (W / TW) * P * s.rw - 1) / ((W / TW) * P * s.rw) * n_mats < 2 * di.cus) W /= 2;
+    if (W < TW) W = TW;
+    s.W = W;
+    const int rows_iter = (W / TW) * P * s.rw;
+    const int iters = (n_out + rows_iter - 1) / rows_iter;
+    int groups = 1;
+    if (s.n_tiles == 1 && (int64_t)iters * n_mats > 16 * di.cus) groups = (int)((int64_t)iters * n_mats / (8 * di.cus));
+    s.groups = groups < 1 ? 1 : (groups > 64 ? 64 : groups);
+    s.grid_x = (iters + s.groups - 1) / s.groups;
+    s.lds = (size_t)nc * ((size_t)s.ktp * 9 / 4);
+    return s;
+}
+
+template <int F, int T, int RW>
+inline MvKernel pick_mv1_nit(int nitm) {
+    switch (nitm) {
+        case 1: return mv1_kernel<F, T, RW, 1>;
+        case 2: return mv1_kernel<F, T, RW, 2>;
+        default: return mv1_kernel<F, T, RW, 4>;
+    }
+}
+template <int F, int T>
+inline MvKernel pick_mv1_rw(int rw, int nitm) {
+    return rw == 1 ? pick_mv1_nit<F, T, 1>(nitm) : pick_mv1_nit<F, T, 2>(nitm);
+}
+template <int F>
+inline MvKernel pick_mv1(int T, int rw, int nitm) {
+    switch (T) {
+        case 16: return pick_mv1_rw<F, 16>(rw, nitm);
+        case 32: return pick_mv1_rw<F, 32>(rw, nitm);
+        default: return pick_mv1_rw<F, 64>(rw, nitm);
+    }
+}
+
+// Tuning overrides for timing runs (unset in normal use): NMQ_MV1=0 disables the one-token
+// kernel, NMQ_MV1_WPC sets its resident waves per CU, NMQ_MV1_RW its rows per team.
+inline int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+struct Mv1Shape {
+    bool ok;
+    int T, rw, nitm, W, grid_x, ktp;
+    size_t lds;
+};
+
+inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
+    Mv1Shape s{};
+    if (!env_int("NMQ_MV1", 1)) return s;
+    const int U = (n_in + 63) / 64;
+    s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    const int nit = (U + s.T - 1) / s.T;
+    if (nit > env_int("NMQ_MV1_MAXNIT", 2)) return s;
+    s.nitm = nit <= 1 ? 1 : (nit <= 2 ? 2 : 4);
+    s.rw = env_int("NMQ_MV1_RW", 1);
+    s.rw = s.rw == 2 ? 2 : 1;
+    const int P = 64 / s.T;
+    const int64_t steps = ((int64_t)n_out + P * s.rw - 1) / (P * s.rw);  // per instance
+    const int wpc = env_int("NMQ_MV1_WPC", 16);
+    int64_t waves = (int64_t)wpc * di.cus / n_mats;
+    if (waves < 1) waves = 1;
+    if (waves > steps) waves = steps;
+    const int wmax = env_int("NMQ_MV1_W", 8);
+    s.W = (int)(waves < wmax ? waves : wmax);
+    s.grid_x = (int)((waves + s.W - 1) / s.W);
+    s.ktp = (n_in + 127) / 128 * 128;
+    s.lds = (size_t)s.ktp * 9 / 4;
+    s.ok = s.lds <= (size_t)di.lds_max;
+    return s;
+}
+
+template <int F, int T>
+inline MvKernel pick_mvc_rw(int rw) {
+    switch (rw) {
+        case 1: return mvc_kernel<F, T, 1>;
+        case 2: return mvc_kernel<F, T, 2>;
+        case 4: return mvc_kernel<F, T, 4>;
+        default: return mvc_kernel<F, T, 8>;
+    }
+}
+template <int F>
+inline MvKernel pick_mvc(int T, int rw) {
+    switch (T) {
+        case 16: return pick_mvc_rw<F, 16>(rw);
+        case 32: return pick_mvc_rw<F, 32>(rw);
+        default: return pick_mvc_rw<F, 64>(rw);
+    }
+}
+
+// Chunk mode (mvc_kernel) for one token.  The rows are spread evenly over about one workgroup per
+// CU (per instance for expert batches): rows per workgroup R = ceil(rows / WGs), then the smallest
+// rows-per-team RW with R <= P*RW*16 (at most 16 waves, 8 when RW = 8), so every CU streams the
+// same number of rows and all of them are in flight at once.
+inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
+    Mv1Shape s{};
+    const int U = (n_in + 63) / 64;
+    s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    if (U > s.T) return s;  // one unit per lane only
+    const int P = 64 / s.T;
+    const int wg_per_cu = env_int("NMQ_MVC_WGPC", 1);
+    int64_t wgs = (int64_t)di.cus * wg_per_cu / n_mats;
+    if (wgs < 1) wgs = 1;
+    const int64_t R = ((int64_t)n_out + wgs - 1) / wgs;  // rows per workgroup
+    int rw = env_int("NMQ_MVC_RW", 0);
+    if (rw == 0) {
+        rw = 1;
+        while (rw < 8 && R > (int64_t)P * rw * 16) rw *= 2;
+    }
+    const int wmax = rw >= 8 ? 8 : 16;
+    int64_t W = (R + P * rw - 1) / (P * rw);
+    if (W > wmax) W = wmax;
+    if (W < 1) W = 1;
+    s.rw = rw;
+    s.W = (int)W;
+    const int64_t rows_wg = (int64_t)P * rw * W;
+    s.grid_x = (int)((n_out + rows_wg - 1) / rows_wg);
+    s.ktp = (n_in + 127) / 128 * 128;
+    s.lds = (size_t)s.ktp * 9 / 4;
+    s.ok = s.lds <= (size_t)di.lds_max;
+    return s;
 }
 
 // One launch of NC <= NMQ_MAX_COLS tokens (n_mats instances along blockIdx.y).
@@ -244,36 +637,38 @@ template <int F>
 int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     using FM = Fmt<F>;
     const DeviceInfo di = device_info();
-    const int rw = nc == 1 ? 1 : 2;
-    const int units = (p.n_in + 63) / 64;
-    const int T = units >= 48 ? 64 : (units >= 24 ? 32 : 16);
-    const int P = 64 / T;
-    // K tile: the whole row when the input of all tokens fits the LDS budget
-    const int budget = nc == 1 ? 40 * 1024 : di.lds_max;
-    const int step = FM::BV == 256 ? 256 : 64;
-    int kt = (int)((int64_t)budget * 4 / 9 / nc) / 128 * 128 / step * step;
-    if (kt < step) kt = step;
-    if (kt >= p.n_in) kt = p.n_in;
-    p.kt = kt;
-    p.ktp = (kt + 127) / 128 * 128;
-    p.n_tiles = (p.n_in + kt - 1) / kt;
     p.nblk = p.n_in / FM::BV;
     p.row_bytes = (int64_t)p.nblk * FM::BB;
-    int W = 4;
-    while (W > 1 && (p.n_out + W * P * rw - 1) / (W * P * rw) * n_mats < 2 * di.cus) W /= 2;
-    const int rows_iter = W * P * rw;
-    const int iters = (p.n_out + rows_iter - 1) / rows_iter;
-    int groups = 1;
-    if (p.n_tiles == 1) {
-        const int target = 4 * di.cus;
-        groups = iters * n_mats / target;
-        groups = groups < 1 ? 1 : (groups > 64 ? 64 : groups);
+    // One token: chunk mode while the rows per CU are few (every weight in flight at once), the
+    // persistent prefetching kernel for larger matrices (measured on MI355X: chunk mode is faster up
+    // to 4096 rows of 4096 values, the persistent kernel from 12288 rows).
+    const int64_t rows_per_cu = ((int64_t)p.n_out * n_mats + di.cus - 1) / di.cus;
+    const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > 24 ? 2 : 1);
+    if (nc == 1 && mode == 1) {
+        const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di);
+        if (sc.ok) {
+            p.ktp = sc.ktp;
+            MvKernel k = pick_mvc<F>(sc.T, sc.rw);
+            hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(64 * sc.W), sc.lds, stream, p);
+            return (int)hipGetLastError();
+        }
     }
-    p.groups = groups;
-    const dim3 grid((unsigned)((iters + groups - 1) / groups), (unsigned)n_mats);
-    const size_t lds = (size_t)nc * ((size_t)p.ktp * 9 / 4);
-    MvKernel k = pick_kernel<F>(nc, T);
-    hipLaunchKernelGGL(k, grid, dim3(64 * W), lds, stream, p);
+    if (nc == 1 && mode != 0) {
+        const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
+        if (s1.ok) {
+            p.ktp = s1.ktp;
+            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm);
+            hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(64 * s1.W), s1.lds, stream, p);
+            return (int)hipGetLastError();
+        }
+    }
+    const MvShape s = plan_mv<F>(p.n_out, p.n_in, nc, n_mats, di);
+    p.kt = s.kt;
+    p.ktp = s.ktp;
+    p.n_tiles = s.n_tiles;
+    p.groups = s.groups;
+    MvKernel k = pick_kernel<F>(nc, s.rw, s.T);
+    hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x, (unsigned)n_mats), dim3(64 * s.W), s.lds, stream, p);
     return (int)hipGetLastError();
 }
 

@@ -56,6 +56,17 @@ def make_weights(fmt, rows, n_in, seed):
     return encode.encode(fmt, w, threads=min(16, len(os.sched_getaffinity(0))))
 
 
+def traffic_bytes():
+    """HBM bytes per launch of the headline kernel, from the committed FETCH_SIZE / WRITE_SIZE counter
+    runs (profiles/q4k_14336x4096_batch1_traffic.md), or None when they are absent."""
+    path = os.path.join(ROOT, "profiles", "q4k_14336x4096_batch1_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def cpu_baseline(raw, fmt, rows, n_in, x, budget_s):
     """The oracle's restatement of the reference CPU path (models/common.py:190, 526-527): dequantise
     once, then fp32 GEMV per call, timed for about budget_s seconds."""
@@ -194,13 +205,51 @@ def main():
         cfg["us_per_layer"] = round(us_layer, 3)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
-        del layers, mats
+        del layers
+        # per-matrix breakdown: each mat-vec timed alone, rotating over its own copies (> 2x the LLC)
+        parts = {}
+        for name, f, r, k, _, inp in LAYER:
+            ei = eg[inp]
+            nc_ = max(2, -(-2 * LLC_BYTES // mats[name].numel()))
+            cps = [mats[name]] + [mats[name].clone() for _ in range(nc_ - 1)]
+
+            def one(i, f=f, r=r, k=k, ei=ei, cps=cps, name=name):
+                rc = L.nmq_mv(TYPE[f], cps[i % len(cps)].data_ptr(), ei.xq.data_ptr(), ei.xq2.data_ptr(),
+                              ei.xd.data_ptr(), ei.xs.data_ptr(), ys[name].data_ptr(), r, k, 1, stream)
+                if rc:
+                    _native.check(rc)
+            for i in range(20):
+                one(i)
+            torch.cuda.synchronize()
+            t0.record()
+            for i in range(reps):
+                one(i)
+            t1.record()
+            torch.cuda.synchronize()
+            us = t0.elapsed_time(t1) / reps * 1e3
+            parts[name] = {"format": f, "shape": [r, k], "us": round(us, 3),
+                           "pct_hbm_peak": round(100 * alg_bytes(f, r, k) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)}
+            del cps
+        xq_in = xin["x_attn"]
+        for i in range(20):
+            L.nmq_quant_q8(xq_in.data_ptr(), 1, eg["x_attn"].xq.data_ptr(), eg["x_attn"].xq2.data_ptr(),
+                           eg["x_attn"].xd.data_ptr(), eg["x_attn"].xs.data_ptr(), 4096, stream)
+        torch.cuda.synchronize()
+        t0.record()
+        for i in range(reps):
+            L.nmq_quant_q8(xq_in.data_ptr(), 1, eg["x_attn"].xq.data_ptr(), eg["x_attn"].xq2.data_ptr(),
+                           eg["x_attn"].xd.data_ptr(), eg["x_attn"].xs.data_ptr(), 4096, stream)
+        t1.record()
+        torch.cuda.synchronize()
+        parts["quant_q8_4096"] = {"us": round(t0.elapsed_time(t1) / reps * 1e3, 3)}
+        cfg["layer_parts"] = parts
+        del mats
 
     out = {"metric": METRIC, "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(ms, 6), "higher_is_better": True, "scaling": "weak",
            "vs_baseline": None, "dtype": "int8", "data": "synthetic", "config": cfg,
            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}}
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes()}}
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(raw, fmt, rows, n_in, x.cpu().numpy(), args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -17,15 +17,15 @@ static bool g_info_ok[64];
 
 DeviceInfo device_info() {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceInfo{256, 64 * 1024};
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return DeviceInfo{256, 60 * 1024, 64 * 1024};
     std::lock_guard<std::mutex> lk(g_info_mu);
     if (!g_info_ok[dev]) {
         int cus = 256, lds = 64 * 1024;
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) cus = 256;
+        if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) lds = 64 * 1024;
         // static LDS of the kernels (IQ2 tables) comes on top of the dynamic part
-        lds = (lds > 64 * 1024 ? 64 * 1024 : lds) - 4096;
-        g_info[dev] = DeviceInfo{cus, lds};
+        const int small = (lds > 64 * 1024 ? 64 * 1024 : lds) - 4096;
+        g_info[dev] = DeviceInfo{cus, small, lds};
         g_info_ok[dev] = true;
     }
     return g_info[dev];

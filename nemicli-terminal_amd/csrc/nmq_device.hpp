@@ -33,6 +33,15 @@ typedef u32 u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr float FEIN = 1.0f / 254.0f;  // scale of the second input stage relative to xd
 
+// Workgroup barrier that orders LDS only.  __syncthreads() also waits for every global read the wave
+// has in flight (on this GPU family reads and writes share one counter and its fence waits for it),
+// which would stall a kernel that issues its weight reads before the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (u16)(bits16 & 0xffffu));
 }

@@ -1,0 +1,412 @@
+// Small-batch mat-vec on the matrix cores: 2..8 tokens per launch with v_mfma_i32_16x16x32_i8.
+//
+// One MFMA multiplies a 16 x 32 int8 input tile with a 32 x 16 int8 weight tile and produces the
+// 16 x 16 int32 sums.  The 16 input rows are the two stages of 8 tokens (row 2t: xq of token t, row
+// 2t + 1: xq2 of token t; rows of absent tokens hold whatever LDS holds and their sums are never
+// stored); the 16 columns are 16 weight rows.  K = 32 is one scale group of every format here (Q6_K:
+// two groups of 16, handled as two MFMAs whose input is masked to one half each), so each MFMA's sums
+// get exactly one weight factor per weight row.
+//
+// Operand layouts (lane l of the wave; checked on gfx950 with an in-bounds probe):
+//   A[row = l % 16][k = 8 (l / 16) + j] = byte j of the lane's 64-bit operand
+//   B[k = 8 (l / 16) + j][col = l % 16]
+//   C[row = 4 (l / 16) + r][col = l % 16] = element r of the 4 x int32 result
+// So lane l loads 8 bytes of weight row l % 16 per step, and its C registers hold, for that weight
+// row, tokens 2 (l / 16) and 2 (l / 16) + 1 with both stages: the lane combines them with its own
+// row's weight factors, without exchanges between lanes.
+//
+// Work split: a wave owns one 16-row tile and one of KS slices of the row's blocks; a workgroup holds
+// TPW tiles x KS slices (W = TPW*KS waves) and stages the input of all tokens once, as ready-made A
+// fragments ([step][k-block][input row], 512 bytes per 32 values, conflict-free 64-bit reads).  The
+// KS partial sums of a tile are added through LDS.
+#pragma once
+
+#include <algorithm>
+
+#include "nmq_device.hpp"
+
+namespace nmq {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+struct MvmParams {
+    const u8* w;
+    const int8_t* xq;
+    const int8_t* xq2;
+    const float* xd;
+    const float* xs;
+    float* y;
+    int n_out, n_in, nc;
+    int ks;       // K slices per tile
+    int tpw;      // tiles per workgroup
+    int64_t row_bytes;
+    int nblk;     // 256-value blocks per row
+};
+
+// Per-format pieces of the MFMA path.  Steps are 32 values; GS = values per scale group (Q6_K: 16,
+// two groups per step).  load(): the lane's bytes of one 256-value block of its row, k-block kb.
+// frag(): the 64-bit weight operand of step s.  fac(): fp32 (weight factor, min factor) of group g.
+// NBMAX: blocks one lane holds in registers at once; NBRING: the same for slices cycled through buffers.
+// MIN_NC: fewest tokens per launch for which this path beats the dot4 kernel (measured on MI355X at
+// 4096 and 12288/14336 rows of 4096 values).
+template <int F>
+struct Mfma;
+
+template <>
+struct Mfma<NMQ_Q4_K> {
+    static constexpr int BB = 144, STEPS = 8, GS = 32, NBMAX = 4, NBRING = 4, MIN_NC = 3;
+    struct Raw {
+        u32x2 q[4];  // [i]: qs[32i + 8kb .. +8]
+        u32x4 h;     // d, dmin, scales[12]
+    };
+    __device__ static void load(const u8* blk, int kb, Raw& r) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) r.q[i] = *gp<u32x2>(blk + 16 + 32 * i + 8 * kb);
+        r.h = ld4a(blk);
+    }
+    // step s: values 32s + l, nibble (s & 1) of qs[32 (s >> 1) + l]
+    __device__ static u64 frag(const Raw& r, int s) {
+        const u32x2 v = r.q[s >> 1];
+        const int sh = 4 * (s & 1);
+        return (u64)((v.x >> sh) & 0x0f0f0f0fu) | ((u64)((v.y >> sh) & 0x0f0f0f0fu) << 32);
+    }
+    // get_scale_min_k4 on the 12 scale bytes, four groups per dword
+    __device__ static float2 fac(const Raw& r, int g) {
+        const u32 sv = g < 4 ? (r.h.y & 0x3f3f3f3fu) : ((r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u));
+        const u32 mv = g < 4 ? (r.h.z & 0x3f3f3f3fu) : (((r.h.w >> 4) & 0x0f0f0f0fu) | ((r.h.z >> 2) & 0x30303030u));
+        const int b = 8 * (g & 3);
+        return make_float2(h2f(r.h.x) * (float)((sv >> b) & 0xffu), h2f(r.h.x >> 16) * (float)((mv >> b) & 0xffu));
+    }
+};
+
+template <>
+struct Mfma<NMQ_Q6_K> {
+    static constexpr int BB = 210, STEPS = 8, GS = 16, NBMAX = 4, NBRING = 2, MIN_NC = 4;
+    struct Raw {
+        u32x2 ql[4];  // [2n + (k&1)]: ql[64n + 32(k&1) + 8kb .. +8]
+        u32x2 qh[2];  // [n]: qh[32n + 8kb .. +8]
+        u32x4 sc;     // 16 int8 scales
+        u32 d;
+    };
+    __device__ static void load(const u8* blk, int kb, Raw& r) {
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            r.ql[2 * n] = ld2(blk + 64 * n + 8 * kb);
+            r.ql[2 * n + 1] = ld2(blk + 64 * n + 32 + 8 * kb);
+            r.qh[n] = ld2(blk + 128 + 32 * n + 8 * kb);
+        }
+        r.sc = ld4(blk + 192);
+        r.d = ld16(blk + 208);
+    }
+    // step s = 4n + k covers values 128n + 32k + l (l = 8kb + j): q = nibble (k >> 1) of
+    // ql[64n + 32(k&1) + l] | bits 2k of qh[32n + l] << 4, minus 32
+    __device__ static u64 frag(const Raw& r, int s) {
+        const int n = s >> 2, k = s & 3;
+        const u32x2 l = r.ql[2 * n + (k & 1)], h = r.qh[n];
+        const int ls = 4 * (k >> 1), hs = 2 * k;
+        const u32 lo = sub32x4(((l.x >> ls) & 0x0f0f0f0fu) | (((h.x >> hs) & 0x03030303u) << 4));
+        const u32 hi = sub32x4(((l.y >> ls) & 0x0f0f0f0fu) | (((h.y >> hs) & 0x03030303u) << 4));
+        return (u64)lo | ((u64)hi << 32);
+    }
+    // group g = values 16g .. 16g + 15
+    __device__ static float2 fac(const Raw& r, int g) {
+        const u32 w = (g >> 2) == 0 ? r.sc.x : (g >> 2) == 1 ? r.sc.y : (g >> 2) == 2 ? r.sc.z : r.sc.w;
+        return make_float2(h2f(r.d) * (float)(int8_t)(w >> (8 * (g & 3))), 0.f);
+    }
+};
+
+template <>
+struct Mfma<NMQ_Q8_0> {
+    // a 256-value block of this path is 8 GGUF blocks, one step each
+    static constexpr int BB = 8 * 34, STEPS = 8, GS = 32, NBMAX = 2, NBRING = 2, MIN_NC = 5;
+    struct Raw {
+        u32x2 q[8];
+        u32 d[8];
+    };
+    __device__ static void load(const u8* blk, int kb, Raw& r) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            r.q[s] = ld2(blk + 34 * s + 2 + 8 * kb);
+            r.d[s] = ld16(blk + 34 * s);
+        }
+    }
+    __device__ static u64 frag(const Raw& r, int s) { return (u64)r.q[s].x | ((u64)r.q[s].y << 32); }
+    __device__ static float2 fac(const Raw& r, int g) { return make_float2(h2f(r.d[g]), 0.f); }
+};
+
+template <>
+struct Mfma<NMQ_TQ2_0> {
+    static constexpr int BB = 66, STEPS = 8, GS = 32, NBMAX = 8, NBRING = 8, MIN_NC = 2;
+    struct Raw {
+        u32x2 q[2];  // [n]: qs[32n + 8kb .. +8]
+        u32 d;
+    };
+    __device__ static void load(const u8* blk, int kb, Raw& r) {
+        r.q[0] = ld2(blk + 8 * kb);
+        r.q[1] = ld2(blk + 32 + 8 * kb);
+        r.d = ld16(blk + 64);
+    }
+    // step s = 4n + l: values 128n + 32l + m, codes at shift 2l of qs[32n + m]
+    __device__ static u64 frag(const Raw& r, int s) {
+        const u32x2 v = r.q[s >> 2];
+        const int sh = 2 * (s & 3);
+        return (u64)sub1x4((v.x >> sh) & 0x03030303u) | ((u64)sub1x4((v.y >> sh) & 0x03030303u) << 32);
+    }
+    __device__ static float2 fac(const Raw& r, int) { return make_float2(h2f(r.d), 0.f); }
+};
+
+template <>
+struct Mfma<NMQ_IQ2_XXS> {
+    static constexpr int BB = 66, STEPS = 8, GS = 32, NBMAX = 4, NBRING = 4, MIN_NC = 4;
+    struct Raw {
+        u32x2 a[8];  // {aux0, aux1} of each 32-value sub-block
+        u32 d;
+    };
+    __device__ static void load(const u8* blk, int /*kb*/, Raw& r) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) r.a[s] = ld2(blk + 2 + 8 * s);
+        r.d = ld16(blk);
+    }
+    // k-block kb of sub-block s is grid entry kb: 8 unsigned grid bytes with 8 signs (7 + parity)
+    __device__ static u64 frag_iq(const Raw& r, int s, int kb, const u64* tab) {
+        const u64 g = tab[bfe(r.a[s].x, 8 * kb, 8)];
+        const u64 m = tab[256 + bfe(r.a[s].y, 7 * kb, 7)];
+        const u32 glo = (u32)g, ghi = (u32)(g >> 32), mlo = (u32)m, mhi = (u32)(m >> 32);
+        return (u64)((glo ^ mlo) + (mlo & 0x01010101u)) | ((u64)((ghi ^ mhi) + (mhi & 0x01010101u)) << 32);
+    }
+    __device__ static float2 fac(const Raw& r, int g) {
+        return make_float2(h2f(r.d) * (0.125f + 0.25f * (float)(r.a[g].y >> 28)), 0.f);
+    }
+};
+
+// LDS layout of the input: A fragments then (xd, xs) pairs.
+//   frag[s][kb][n] (u64): s = 32-value step of the row; input row n = xq (n even) or xq2 (n odd) of
+//   token n / 2, values 32s + 8kb .. + 8
+//   xsc[s][t] (float2): (xd / 254, xs) of token t, step s
+// Staged in rounds: per round each thread reads 4 16-byte chunks (16 input rows x n_in / 16 chunks in
+// all, 16 rows x 4 chunks per wave access) and one (xd, xs) pair.  Every read is issued (threads with
+// nothing to read re-read the start of xq), so a round's reads can be issued before the weight reads
+// and waited for alone.  Rows of absent tokens (t >= nc) are left unwritten.
+struct XStage {
+    u32x4 v[4];
+    float2 f;
+};
+
+__device__ __forceinline__ void stage_load(XStage& st, int r, const MvmParams& p) {
+    const int T = blockDim.x, S = p.n_in / 32;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = (4 * r + j) * T + (int)threadIdx.x;
+        const int n = i & 15, c = i >> 4, t = n >> 1;
+        const bool ok = i < p.n_in && t < p.nc;
+        const int8_t* src = ok ? ((n & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in + 16 * c : p.xq;
+        st.v[j] = *gp<u32x4>(src);
+    }
+    const int i = r * T + (int)threadIdx.x;
+    const int t = i & 7, s = i >> 3;
+    const int64_t o = (i < 8 * S && t < p.nc) ? (int64_t)t * S + s : 0;
+    st.f = make_float2(gp<float>(p.xd)[o], gp<float>(p.xs)[o]);
+}
+
+__device__ __forceinline__ void stage_store(const XStage& st, int r, u8* lds, const MvmParams& p) {
+    const int T = blockDim.x, S = p.n_in / 32;
+    u64* frag = (u64*)lds;
+    float2* xsc = (float2*)(lds + (size_t)S * 512);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = (4 * r + j) * T + (int)threadIdx.x;
+        const int n = i & 15, c = i >> 4, t = n >> 1;
+        if (i < p.n_in && t < p.nc) {
+            // values 16c .. 16c + 15: step c / 2, k-blocks 2 (c & 1) and 2 (c & 1) + 1
+            u64* d = frag + ((c >> 1) * 4 + 2 * (c & 1)) * 16 + n;
+            d[0] = (u64)st.v[j].x | ((u64)st.v[j].y << 32);
+            d[16] = (u64)st.v[j].z | ((u64)st.v[j].w << 32);
+        }
+    }
+    const int i = r * T + (int)threadIdx.x;
+    if (i < 8 * S && (i & 7) < p.nc) xsc[i] = make_float2(st.f.x * FEIN, st.f.y);
+}
+
+// One 256-value block of the lane's weight row into its sums of tokens 2kb and 2kb + 1:
+//   y += w_g * (xd_g / 254) * (254 S1 + S2) - m_g * xs_g   per 32-value group g (Q6_K: per 16, no m term)
+// (254 S1 + S2 is exact in int32: |S1|, |S2| <= 32 * 127 * 63.)
+// The LDS operands of each step are read one step ahead.
+template <int F>
+__device__ __forceinline__ void mvm_block(const typename Mfma<F>::Raw& cur, int b, const u64* tab, const u64* frag,
+                                          const float2* xsc, int lane, float& acc0, float& acc1) {
+    using M = Mfma<F>;
+    const int kb = lane >> 4, n = lane & 15;
+    u64 xv[2];
+    float4 xf[2];
+    xv[0] = frag[(b * M::STEPS * 4 + kb) * 16 + n];
+    xf[0] = *(const float4*)(xsc + b * M::STEPS * 8 + 2 * kb);
+#pragma unroll
+    for (int s = 0; s < M::STEPS; ++s) {
+        if (s + 1 < M::STEPS) {
+            const int gn = b * M::STEPS + s + 1;
+            xv[(s + 1) & 1] = frag[(gn * 4 + kb) * 16 + n];
+            xf[(s + 1) & 1] = *(const float4*)(xsc + gn * 8 + 2 * kb);  // (xd, xs) of tokens 2kb, 2kb+1
+        }
+        __builtin_amdgcn_sched_barrier(0);  // the next step's reads stay ahead of this step's work
+        u64 wv;
+        if constexpr (F == NMQ_IQ2_XXS) wv = M::frag_iq(cur, s, kb, tab);
+        else wv = M::frag(cur, s);
+        const u64 x = xv[s & 1];
+        const float4 f = xf[s & 1];
+        if constexpr (M::GS == 16) {
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const u64 xm = (kb >> 1) == half ? x : 0ull;
+                i32x4 c = {0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xm, (long)wv, c, 0, 0, 0);
+                const float w = M::fac(cur, 2 * s + half).x;
+                acc0 = fmaf(w * f.x, (float)__mul24(c[0], 254) + (float)c[1], acc0);
+                acc1 = fmaf(w * f.z, (float)__mul24(c[2], 254) + (float)c[3], acc1);
+            }
+        } else {
+            i32x4 c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+            const float2 w = M::fac(cur, s);
+            acc0 = fmaf(w.x * f.x, (float)(__mul24(c[0], 254) + c[1]), fmaf(-w.y, f.y, acc0));
+            acc1 = fmaf(w.x * f.z, (float)(__mul24(c[2], 254) + c[3]), fmaf(-w.y, f.w, acc1));
+        }
+    }
+}
+
+// NB blocks of the wave's slice are held in registers.  RING = false: the slice has exactly NB blocks,
+// all requested before the input is staged.  RING = true: any number of blocks, each buffer refilled
+// NB blocks ahead once used (requests past the slice re-read its last block, so every wave issues the
+// same loads and the waits count exactly).
+template <int F, int NB, bool RING>
+__global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
+    using M = Mfma<F>;
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int S = p.n_in / 32;
+    const u64* frag = (const u64*)lds;
+    const float2* xsc = (const float2*)(lds + (size_t)S * 512);
+    float* red = (float*)lds;  // W x 64 x 2 sums, after the blocks
+
+    const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
+    const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
+    const int n = lane & 15, kb = lane >> 4;
+    const int bpr = p.nblk / p.ks;  // blocks of this wave's slice
+    const int b0 = slice * bpr, last = b0 + bpr - 1;
+    const u8* rowp = p.w + (int64_t)min(row0 + n, p.n_out - 1) * p.row_bytes;
+
+    // input reads of the first round, then the weight reads: the first round's stores wait only for
+    // the older input reads while the weights stream in
+    const int rounds = (p.n_in + 4 * (int)blockDim.x - 1) / (4 * (int)blockDim.x);
+    XStage st;
+    stage_load(st, 0, p);
+    const u64 gv = tab_load<F>();
+    // Every wave's input reads are issued before any wave's weight reads: the CU's vector cache
+    // returns data in request order, so input requested after another wave's weights would wait
+    // for them.  (The barrier waits for issue only, not for the data.)
+    lds_barrier();
+
+    typename M::Raw buf[NB];
+#pragma unroll
+    for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    tab_store<F>(tab, gv);
+    stage_store(st, 0, lds, p);
+    for (int r = 1; r < rounds; ++r) {
+        stage_load(st, r, p);
+        stage_store(st, r, lds, p);
+    }
+    lds_barrier();
+
+    float acc0 = 0.f, acc1 = 0.f;
+    if constexpr (RING) {
+        for (int j0 = 0; j0 < bpr; j0 += NB) {
+#pragma unroll
+            for (int u = 0; u < NB; ++u) {
+                if (j0 + u < bpr) mvm_block<F>(buf[u], b0 + j0 + u, tab, frag, xsc, lane, acc0, acc1);
+                M::load(rowp + (int64_t)min(b0 + j0 + u + NB, last) * M::BB, kb, buf[u]);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) mvm_block<F>(buf[u], b0 + u, tab, frag, xsc, lane, acc0, acc1);
+    }
+
+    // add the KS slices of each tile; lane (n, kb) holds weight row row0 + n, tokens 2kb and 2kb + 1
+    // (the sums take the place of the staged input, once every wave is done with it)
+    lds_barrier();
+    red[(wave * 64 + lane) * 2] = acc0;
+    red[(wave * 64 + lane) * 2 + 1] = acc1;
+    lds_barrier();
+    if (slice == 0) {
+        float s0 = 0.f, s1 = 0.f;
+        for (int q = 0; q < p.ks; ++q) {
+            const int ri = ((tile_in_wg * p.ks + q) * 64 + lane) * 2;
+            s0 += red[ri];
+            s1 += red[ri + 1];
+        }
+        const int r = row0 + n, t = 2 * kb;
+        if (r < p.n_out) {
+            if (t < p.nc) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = s0;
+            if (t + 1 < p.nc) gpw<float>(p.y)[(int64_t)(t + 1) * p.n_out + r] = s1;
+        }
+    }
+}
+
+// ---- host side ------------------------------------------------------------------------------------
+
+struct MvmShape {
+    bool ok;
+    int ks, tpw, grid_x, nb;
+    bool ring;
+    size_t lds;
+};
+
+// Tiles of 16 rows; K slices per tile and tiles per workgroup chosen for about one workgroup of up
+// to 16 waves per CU (the staged input takes most of the LDS).  A slice of up to NBMAX blocks is held
+// in registers whole; longer slices cycle through NBRING buffers.
+template <int F>
+inline MvmShape plan_mvm(int n_out, int n_in, int nc, int cus, int lds_max) {
+    MvmShape s{};
+    const int mode = env_int("NMQ_MVM", 1);  // 0: never, 1: from MIN_NC tokens, 2: from 2 tokens
+    if (mode == 0 || nc < (mode == 2 ? 2 : Mfma<F>::MIN_NC) || nc > 8 || n_in % 256) return s;
+    const int nblk = n_in / 256;
+    const int tiles = (n_out + 15) / 16;
+    int tpw = env_int("NMQ_MVM_TPW", 0);
+    if (tpw <= 0) tpw = (tiles + cus - 1) / cus;
+    if (tpw > 16) tpw = 16;
+    int ks = env_int("NMQ_MVM_KS", 0);
+    if (ks <= 0) {
+        ks = 1;
+        while (ks * 2 * tpw <= 16 && nblk % (ks * 2) == 0) ks *= 2;
+    }
+    if (nblk % ks || ks * tpw > 16) return s;
+    const int bpr = nblk / ks;
+    const int W = ks * tpw;
+    s.ks = ks;
+    s.tpw = tpw;
+    s.grid_x = (tiles + tpw - 1) / tpw;
+    s.ring = !(bpr <= Mfma<F>::NBMAX && (bpr & (bpr - 1)) == 0);
+    s.nb = s.ring ? Mfma<F>::NBRING : bpr;
+    s.lds = std::max((size_t)(n_in / 32) * 576, (size_t)W * 512);
+    s.ok = s.lds + 4096 <= (size_t)lds_max;
+    return s;
+}
+
+template <int F>
+int launch_mvm(const MvmShape& s, MvmParams p, hipStream_t stream) {
+    p.ks = s.ks;
+    p.tpw = s.tpw;
+    constexpr int NBM = Mfma<F>::NBMAX;
+    void (*k)(MvmParams);
+    if (s.ring) k = mvm_kernel<F, Mfma<F>::NBRING, true>;
+    else if (s.nb == 1) k = mvm_kernel<F, 1, false>;
+    else if (s.nb == 2) k = mvm_kernel<F, (NBM >= 2 ? 2 : 1), false>;
+    else if (s.nb == 4) k = mvm_kernel<F, (NBM >= 4 ? 4 : 1), false>;
+    else k = mvm_kernel<F, NBM, false>;
+    hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
+    return (int)hipGetLastError();
+}
+
+}  // namespace nmq

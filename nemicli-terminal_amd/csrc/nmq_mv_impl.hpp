@@ -110,6 +110,86 @@ __device__ __forceinline__ void read_slice(const u8* base, int ktp, int u, XSlic
     }
 }
 
+// One token, whole row, in rounds of one 16-byte chunk of xq and of xq2 and one (xd, xs) pair per
+// thread.  Every read of a round is issued (threads past the row re-read its start), so a kernel can
+// issue round 0 before its weight reads and wait for it alone; the stores apply stage_tile's layout.
+struct XRound {
+    u32x4 a, b;
+    float d, s;
+};
+
+__device__ __forceinline__ void stage1_load(XRound& r, int rnd, const int8_t* xq, const int8_t* xq2, const float* xd,
+                                            const float* xs, int n_in) {
+    const int i = rnd * (int)blockDim.x + (int)threadIdx.x;
+    const int ch = 16 * i < n_in ? i : 0;
+    r.a = *gp<u32x4>(xq + 16 * ch);
+    r.b = *gp<u32x4>(xq2 + 16 * ch);
+    const int g = i < n_in / 32 ? i : 0;
+    r.d = gp<float>(xd)[g];
+    r.s = gp<float>(xs)[g];
+}
+
+template <bool STRIDED>
+__device__ __forceinline__ void stage1_store(const XRound& r, int rnd, u8* lds, int n_in, int ktp) {
+    const int i = rnd * (int)blockDim.x + (int)threadIdx.x;
+    if (i < ktp / 16) {
+        const bool ok = 16 * i < n_in;
+        const int ph = swz<STRIDED>(i);
+        *(u32x4*)(lds + 16 * ph) = ok ? r.a : u32x4{0u, 0u, 0u, 0u};
+        *(u32x4*)(lds + ktp + 16 * ph) = ok ? r.b : u32x4{0u, 0u, 0u, 0u};
+    }
+    if (i < ktp / 32) {
+        const bool ok = i < n_in / 32;
+        float* d = (float*)(lds + 2 * ktp);
+        d[i] = ok ? r.d : 0.f;
+        d[ktp / 32 + i] = ok ? r.s : 0.f;
+    }
+}
+
+// IQ2_XXS tables in LDS (grid[256], then sign masks[128]), split like the input staging: tab_load()
+// reads this thread's grid entry (always a valid address), tab_store() writes the tables.
+template <int F>
+__device__ __forceinline__ u64 tab_load() {
+    return F == NMQ_IQ2_XXS ? IQ2XXS_GRID[min((int)threadIdx.x, 255)] : 0ull;
+}
+
+template <int F>
+__device__ __forceinline__ void tab_store(u64* tab, u64 gv) {
+    if (F != NMQ_IQ2_XXS) return;
+    if (blockDim.x >= 256) {
+        if (threadIdx.x < 256) tab[threadIdx.x] = gv;
+    } else {
+        for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = IQ2XXS_GRID[i];
+    }
+    for (int i = threadIdx.x; i < 128; i += blockDim.x) tab[256 + i] = iq2_sign_mask((u32)i);
+}
+
+// Input staging of the one-token kernels around their first weight reads: round 0 of the input and
+// the table entry go out first, the weight reads (issue()) next, and the stores wait only for the
+// older input reads; later rounds (rows longer than 16 values per thread) follow.
+template <int F, typename Issue>
+__device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
+    using FM = Fmt<F>;
+    const int8_t* xq = p.xq + xrow * p.n_in;
+    const int8_t* xq2 = p.xq2 + xrow * p.n_in;
+    const float* xd = p.xd + xrow * (p.n_in / 32);
+    const float* xs = p.xs + xrow * (p.n_in / 32);
+    XRound r;
+    stage1_load(r, 0, xq, xq2, xd, xs, p.n_in);
+    const u64 gv = tab_load<F>();
+    __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    tab_store<F>(tab, gv);
+    stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp);
+    const int rounds = (p.ktp / 16 + (int)blockDim.x - 1) / (int)blockDim.x;
+    for (int k = 1; k < rounds; ++k) {
+        stage1_load(r, k, xq, xq2, xd, xs, p.n_in);
+        stage1_store<FM::STRIDED>(r, k, lds, p.n_in, p.ktp);
+    }
+    lds_barrier();
+}
+
 template <int F>
 __device__ __forceinline__ void fill_tables(u64* tab) {
     if (F == NMQ_IQ2_XXS) {
@@ -361,13 +441,10 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     Mv1Step<F, T, RW, NITM> a, b, c;
     const int stride = nw * SR;
     int base = gw * SR;
-    a.load(wbase, p.row_bytes, base + off, p.n_out, lt, U, p.nblk, base + off);
-    b.load(wbase, p.row_bytes, base + stride + off, p.n_out, lt, U, p.nblk, base + off);
-
-    fill_tables<F>(tab);
-    stage_tile<FM::STRIDED>(lds, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
-                            p.xs + xrow * (p.n_in / 32), p.n_in, 1, 0, p.n_in, p.ktp);
-    __syncthreads();
+    stage1_around<F>(lds, tab, p, xrow, [&] {
+        a.load(wbase, p.row_bytes, base + off, p.n_out, lt, U, p.nblk, base + off);
+        b.load(wbase, p.row_bytes, base + stride + off, p.n_out, lt, U, p.nblk, base + off);
+    });
     XSlice x[NITM];
 #pragma unroll
     for (int it = 0; it < NITM; ++it) {
@@ -392,9 +469,9 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 }
 
 // ---- one token, one chunk per wave -------------------------------------------------------------
-// Each wave owns one chunk of P*RW rows: it requests all of the chunk's weights first (before the
-// input is staged, so the HBM latency overlaps the staging), then computes the rows in order as
-// their data arrives.  Used when the matrix fits in the resident waves of one launch (then every
+// Each wave owns one chunk of P*RW rows: it requests all of the chunk's weights while the input is
+// staged (the HBM latency overlaps the staging), then computes the rows in order as their data
+// arrives.  Used when the matrix fits in the resident waves of one launch (then every
 // weight byte of the matvec is in flight at once, the shape a streaming read needs at this size).
 template <int F, int T, int RW>
 __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
@@ -417,12 +494,7 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
     const int U = (p.n_in + 63) >> 6;
     const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
     Mv1Step<F, T, RW, 1> a;
-    a.load(wbase, p.row_bytes, r0, p.n_out, lt, U, p.nblk, r0);
-
-    fill_tables<F>(tab);
-    stage_tile<FM::STRIDED>(lds, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
-                            p.xs + xrow * (p.n_in / 32), p.n_in, 1, 0, p.n_in, p.ktp);
-    __syncthreads();
+    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(wbase, p.row_bytes, r0, p.n_out, lt, U, p.nblk, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
     const LaneConst lc = lane_const<F, T, 1>(lt);
@@ -433,7 +505,8 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
 
 struct DeviceInfo {
     int cus;
-    int lds_max;  // bytes of dynamic LDS one workgroup may use
+    int lds_max;      // bytes of dynamic LDS one workgroup may use (<= 64 KB)
+    int lds_max_big;  // bytes of LDS one workgroup may use in total (160 KB on gfx950)
 };
 DeviceInfo device_info();
 
@@ -550,6 +623,10 @@ inline int env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
+}  // namespace nmq
+#include "nmq_mfma.hpp"
+namespace nmq {
+
 struct Mv1Shape {
     bool ok;
     int T, rw, nitm, W, grid_x, ktp;
@@ -639,6 +716,18 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     const DeviceInfo di = device_info();
     p.nblk = p.n_in / FM::BV;
     p.row_bytes = (int64_t)p.nblk * FM::BB;
+    // 2..8 tokens of one matrix: the matrix cores (see nmq_mfma.hpp)
+    if (nc >= 2 && p.ids == nullptr) {
+        const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
+        if (sm.ok) {
+            MvmParams q{};
+            q.w = p.w; q.xq = p.xq; q.xq2 = p.xq2; q.xd = p.xd; q.xs = p.xs; q.y = p.y;
+            q.n_out = p.n_out; q.n_in = p.n_in; q.nc = nc;
+            q.row_bytes = p.row_bytes;
+            q.nblk = p.n_in / 256;
+            return launch_mvm<F>(sm, q, stream);
+        }
+    }
     // One token: chunk mode while the rows per CU are few (every weight in flight at once), the
     // persistent prefetching kernel for larger matrices (measured on MI355X: chunk mode is faster up
     // to 4096 rows of 4096 values, the persistent kernel from 12288 rows).

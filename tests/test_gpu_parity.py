@@ -150,6 +150,52 @@ def test_mv_tokens(nmq, oracle, fmt, nc):
     _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("split", [(1, 16), (1, 8), (1, 4), (1, 2), (1, 1), (2, 4), (4, 4), (3, 2)])
+def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
+    """2..8 tokens on the matrix cores with every (tiles per workgroup, K slices) split: slices of
+    16, 8, 4, 2 and 1 blocks (held whole or cycled through buffers), a partial last tile, and
+    workgroups whose last tiles lie past the matrix."""
+    tpw, ks = split
+    n_out, n_in = 200, 4096
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=61 + ks)
+    from ggufengine_amd.gguf_types import TYPE_ID
+    monkeypatch.setenv("NMQ_MVM", "2")   # the matrix-core path from 2 tokens on, whatever the format
+    monkeypatch.setenv("NMQ_MVM_TPW", str(tpw))
+    monkeypatch.setenv("NMQ_MVM_KS", str(ks))
+    for nc in (2, 7, 8):
+        x = np.random.default_rng(62 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        x[:, 7] = 30.0
+        e = quant_dev(dev(x))
+        y = torch.full((nc, n_out), float("nan"), device="cuda")
+        say("mv tokens mfma", fmt, split, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                   e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                   nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
+    """2..8 tokens on the dot4 kernel (the path below each format's matrix-core threshold), forced for
+    every token count."""
+    n_out, n_in = 200, 4096
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=71)
+    from ggufengine_amd.gguf_types import TYPE_ID
+    monkeypatch.setenv("NMQ_MVM", "0")
+    for nc in (2, 5, 8):
+        x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        e = quant_dev(dev(x))
+        y = torch.full((nc, n_out), float("nan"), device="cuda")
+        say("mv tokens dot4", fmt, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                   e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                   nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q8_0"])
 def test_mv_long_rows_several_tiles(nmq, oracle, fmt):
     """8 tokens of 14336 values exceed the LDS budget: the input goes through in K tiles."""

@@ -413,7 +413,7 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
     }
 }
 
-template <int F, int T, int RW, int NITM>
+template <int F, int T, int RW, int NITM, int NBUF>
 __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
@@ -437,13 +437,15 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 
     // Loads are issued unconditionally (rows and units clamped to valid addresses, surplus results
     // discarded), so the compiler can wait for exactly the oldest step and keep the others in flight.
-    // Three step buffers rotate: while one step is computed, the next two are in flight.
-    Mv1Step<F, T, RW, NITM> a, b, c;
+    // NBUF step buffers rotate: while one step is computed, the next NBUF - 1 are in flight (the first
+    // NBUF - 1 go out while the input is staged).
+    Mv1Step<F, T, RW, NITM> buf[NBUF];
     const int stride = nw * SR;
     int base = gw * SR;
     stage1_around<F>(lds, tab, p, xrow, [&] {
-        a.load(wbase, p.row_bytes, base + off, p.n_out, lt, U, p.nblk, base + off);
-        b.load(wbase, p.row_bytes, base + stride + off, p.n_out, lt, U, p.nblk, base + off);
+#pragma unroll
+        for (int i = 0; i < NBUF - 1; ++i)
+            buf[i].load(wbase, p.row_bytes, base + i * stride + off, p.n_out, lt, U, p.nblk, base + off);
     });
     XSlice x[NITM];
 #pragma unroll
@@ -453,18 +455,15 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     }
 
     const LaneConst lc = lane_const<F, T, NITM>(lt);
-    while (base < p.n_out) {  // wave-uniform
-        c.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
-        mv1_compute<F, T, RW, NITM>(a, x, base + off, p.n_out, lt, U, tab, y, lc);
-        base += stride;
-        if (base >= p.n_out) break;
-        a.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
-        mv1_compute<F, T, RW, NITM>(b, x, base + off, p.n_out, lt, U, tab, y, lc);
-        base += stride;
-        if (base >= p.n_out) break;
-        b.load(wbase, p.row_bytes, base + 2 * stride + off, p.n_out, lt, U, p.nblk, base + off);
-        mv1_compute<F, T, RW, NITM>(c, x, base + off, p.n_out, lt, U, tab, y, lc);
-        base += stride;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            if (base >= p.n_out) return;  // wave-uniform
+            buf[(i + NBUF - 1) % NBUF].load(wbase, p.row_bytes, base + (NBUF - 1) * stride + off, p.n_out, lt, U,
+                                            p.nblk, base + off);
+            mv1_compute<F, T, RW, NITM>(buf[i], x, base + off, p.n_out, lt, U, tab, y, lc);
+            base += stride;
+        }
     }
 }
 
@@ -596,23 +595,23 @@ inline MvShape plan_mv(int n_out, int n_in, int nc, int n_mats, const DeviceInfo
 }
 
 template <int F, int T, int RW>
-inline MvKernel pick_mv1_nit(int nitm) {
+inline MvKernel pick_mv1_nit(int nitm, int nbuf) {
     switch (nitm) {
-        case 1: return mv1_kernel<F, T, RW, 1>;
-        case 2: return mv1_kernel<F, T, RW, 2>;
-        default: return mv1_kernel<F, T, RW, 4>;
+        case 1: return nbuf == 4 ? mv1_kernel<F, T, RW, 1, 4> : mv1_kernel<F, T, RW, 1, 3>;
+        case 2: return nbuf == 4 ? mv1_kernel<F, T, RW, 2, 4> : mv1_kernel<F, T, RW, 2, 3>;
+        default: return mv1_kernel<F, T, RW, 4, 3>;
     }
 }
 template <int F, int T>
-inline MvKernel pick_mv1_rw(int rw, int nitm) {
-    return rw == 1 ? pick_mv1_nit<F, T, 1>(nitm) : pick_mv1_nit<F, T, 2>(nitm);
+inline MvKernel pick_mv1_rw(int rw, int nitm, int nbuf) {
+    return rw == 1 ? pick_mv1_nit<F, T, 1>(nitm, nbuf) : pick_mv1_nit<F, T, 2>(nitm, nbuf);
 }
 template <int F>
-inline MvKernel pick_mv1(int T, int rw, int nitm) {
+inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf) {
     switch (T) {
-        case 16: return pick_mv1_rw<F, 16>(rw, nitm);
-        case 32: return pick_mv1_rw<F, 32>(rw, nitm);
-        default: return pick_mv1_rw<F, 64>(rw, nitm);
+        case 16: return pick_mv1_rw<F, 16>(rw, nitm, nbuf);
+        case 32: return pick_mv1_rw<F, 32>(rw, nitm, nbuf);
+        default: return pick_mv1_rw<F, 64>(rw, nitm, nbuf);
     }
 }
 
@@ -629,7 +628,7 @@ namespace nmq {
 
 struct Mv1Shape {
     bool ok;
-    int T, rw, nitm, W, grid_x, ktp;
+    int T, rw, nitm, nbuf, W, grid_x, ktp;
     size_t lds;
 };
 
@@ -643,6 +642,7 @@ inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     s.nitm = nit <= 1 ? 1 : (nit <= 2 ? 2 : 4);
     s.rw = env_int("NMQ_MV1_RW", 1);
     s.rw = s.rw == 2 ? 2 : 1;
+    s.nbuf = env_int("NMQ_MV1_NBUF", 3) == 4 && s.nitm * s.rw <= 2 ? 4 : 3;
     const int P = 64 / s.T;
     const int64_t steps = ((int64_t)n_out + P * s.rw - 1) / (P * s.rw);  // per instance
     const int wpc = env_int("NMQ_MV1_WPC", 16);
@@ -746,7 +746,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
         if (s1.ok) {
             p.ktp = s1.ktp;
-            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm);
+            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf);
             hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(64 * s1.W), s1.lds, stream, p);
             return (int)hipGetLastError();
         }

@@ -1,0 +1,117 @@
+"""
+The reference's expert path around the gathered mat-vec, on this library's kernels:
+
+  - `PackedExperts` (models/common.py:434-480): an expert tensor (n_exp, n_out, n_in) in GGUF block
+    format; `matvec(ids, x)` applies the experts `ids` to one shared input, `matvec_je(ids, a)` each
+    to its own input, both through `cudakern.mv` (the expert-id-gathered kernel, ids read on the GPU).
+  - `auswahl(logits, k)`: the softmax router of `_Schicht._auswahl` (models/baukasten.py:171-190)
+    without the grouped and sigmoid variants: p = softmax(logits), the k largest, their p optionally
+    renormalised to sum 1 (+1e-20), times the weights scale.
+  - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  One token:
+    gate/up on the shared input, down on each expert's own activation.  Several tokens: every
+    (token, slot) pair on its own, in (token, slot) order, the weighted sum per token in that fixed
+    order; the shared input of a token is read by its k slots (x_group = k) instead of repeated.
+
+Every expert product runs on libnmq's HIP kernels; without the library the constructor raises.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _native, cudakern
+from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
+from .mmvq import Eingang, _starten
+
+
+class PackedExperts:
+    """Expert tensor (n_exp, n_out, n_in) kept in its GGUF block format (reference common.py:434-480)."""
+
+    def __init__(self, raw: torch.Tensor, ggml_type: int, n_exp: int, n_out: int, n_in: int,
+                 dtype: torch.dtype = torch.bfloat16):
+        if ggml_type not in GGML_TYPES:
+            raise GGUFError(f"PackedExperts: type {ggml_type} is not one of this library's formats")
+        name, bs, ts = GGML_TYPES[ggml_type]
+        if n_in % bs or raw.numel() != n_exp * n_out * (n_in // bs) * ts:
+            raise GGUFError(f"PackedExperts: {raw.numel()} bytes do not hold {n_exp}x{n_out}x{n_in} {name}")
+        if not raw.is_cuda or not cudakern.verfuegbar(raw.device, name, n_in):
+            raise RuntimeError("PackedExperts: libnmq.so is not loaded or the device is not gfx950")
+        self.raw = raw.view(n_exp, -1)
+        self.geraet = raw.device
+        self.ggml_type = ggml_type
+        self.n_exp, self.n_out, self.n_in = n_exp, n_out, n_in
+        self.dtype = dtype
+        self.name = name
+        self.kernel = True
+        self.adressen: Optional[torch.Tensor] = None   # optional address table (n_exp,) int64 on the GPU
+
+    def __len__(self) -> int:
+        return self.n_exp
+
+    def matvec(self, ids: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """The experts `ids` (k,) applied to one shared input x (n_in,) -> (k, n_out) float32."""
+        return cudakern.mv(self.name, self.raw, ids, x.reshape(-1), self.n_out, self.n_in, self.adressen)
+
+    def matvec_je(self, ids: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
+        """Expert ids[j] applied to its own input a[j]: (k, n_in) -> (k, n_out) float32."""
+        return cudakern.mv(self.name, self.raw, ids, a.reshape(ids.numel(), -1), self.n_out, self.n_in,
+                           self.adressen)
+
+    def matvec_tokens(self, ids: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """ids (L, k), x (L, n_in): expert ids[t, j] applied to token t's input -> (L*k, n_out) float32,
+        rows in (token, slot) order (each token's input quantised once, read by its k slots)."""
+        L_, k = ids.shape
+        flat = ids.reshape(-1).to(x.device, torch.int64).contiguous()
+        e = Eingang(x.reshape(L_, self.n_in).to(torch.bfloat16).contiguous())
+        y = torch.empty(L_ * k, self.n_out, dtype=torch.float32, device=x.device)
+        if self.adressen is None:
+            quelle, per = self.raw, self.raw.shape[1]
+        else:
+            quelle, per = self.adressen.to(x.device, torch.int64).contiguous(), -1
+        _starten("mv_experts", _native.lib().nmq_mv_experts, TYPE_ID[self.name], quelle.data_ptr(), flat.data_ptr(),
+                 L_ * k, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, y.data_ptr(),
+                 self.n_out, self.n_in, _native.stream_ptr(x.device))
+        return y
+
+
+def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float = 1.0
+            ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Softmax router (reference baukasten.py:171-190, softmax gating, no groups):
+    logits (L, n_exp) -> (ids (L, k) int64, weights (L, k) float32)."""
+    p = torch.softmax(logits.float(), dim=-1)
+    idx = p.topk(k, dim=-1)[1]
+    w = p.gather(-1, idx)
+    if normieren:
+        w = w / (w.sum(-1, keepdim=True) + 1e-20)
+    return idx, w * scale
+
+
+class Experten:
+    """Expert MLP of a MoE layer, gate/up/down in block format (reference moe.py:252-321, silu gate)."""
+
+    def __init__(self, gate: PackedExperts, up: PackedExperts, down: PackedExperts):
+        if not (gate.n_exp == up.n_exp == down.n_exp and gate.n_out == up.n_out == down.n_in
+                and gate.n_in == up.n_in == down.n_out):
+            raise GGUFError("Experten: gate/up/down shapes do not fit together")
+        self.gate, self.up, self.down = gate, up, down
+        self.n_exp = gate.n_exp
+
+    @staticmethod
+    def _gu(h_gate: torch.Tensor, h_up: torch.Tensor) -> torch.Tensor:
+        return F.silu(h_gate) * h_up
+
+    def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights."""
+        L_, E = x.shape
+        if L_ == 1:
+            ids = idx[0]
+            g = self.gate.matvec(ids, x[0])
+            u = self.up.matvec(ids, x[0])
+            y = self.down.matvec_je(ids, self._gu(g, u))                       # (k, E)
+            return (y * w[0].float().unsqueeze(-1)).sum(0, keepdim=True)
+        g = self.gate.matvec_tokens(idx, x)
+        u = self.up.matvec_tokens(idx, x)
+        y = self.down.matvec_je(idx.reshape(-1), self._gu(g, u))              # (L*k, E)
+        return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)

@@ -96,6 +96,211 @@ def cpu_baseline(raw, fmt, rows, n_in, x, budget_s):
                       f"{calls} calls ({el:.1f} s, {per * 1e6:.0f} us/call) on {threads} threads of {cpu}"}
 
 
+# ---- the other configurations: one JSON record per case on stdout ---------------------------------
+
+def _events_us(fn, steps, warmup):
+    """us per call of fn(i) (launches on the current stream), HIP events around `steps` calls."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps * 1e3
+
+
+def _copies(t, total_bytes=None):
+    """t and clones of it, together more than twice the last-level cache."""
+    n = max(2, -(-2 * LLC_BYTES // (total_bytes or t.numel() * t.element_size())))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
+def _record(config, case, fmt, us, ab, err, **extra):
+    gbs = ab / (us * 1e-6) / 1e9
+    rec = {"config": config, "case": case, "format": fmt, "us": round(us, 3), "algorithmic_bytes": ab,
+           "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}
+    if err is not None:
+        rec["max_rel_err_vs_oracle"] = err
+    rec.update(extra)
+    print(json.dumps(rec), flush=True)
+
+
+def _mv_case(L, stream, fmt, ws, raw_np, rows, n_in, x_np, steps, warmup, env=None):
+    """Time nmq_mv on n = x_np.shape[0] tokens rotating over the weight copies ws; parity of the last
+    output against the oracle.  env: tuning variables set for this case only."""
+    import torch
+    import oracle
+    from ggufengine_amd import _native, mmvq
+    saved = {k: os.environ.get(k) for k in (env or {})}
+    os.environ.update(env or {})
+    try:
+        dev = ws[0].device
+        n = x_np.shape[0]
+        e = mmvq.Eingang(torch.from_numpy(x_np).to(dev))
+        y = torch.empty(n, rows, dtype=torch.float32, device=dev)
+        ep = [e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr()]
+
+        def go(i):
+            rc = L.nmq_mv(TYPE[fmt], ws[i % len(ws)].data_ptr(), *ep, y.data_ptr(), rows, n_in, n, stream)
+            if rc:
+                _native.check(rc)
+        us = _events_us(go, steps, warmup)
+        err = float(oracle.rel_err_rows(y.cpu().numpy(), oracle.mv_deq(fmt, raw_np, rows, n_in, x_np)).max())
+        return us, err
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+def _x(seed, shape):
+    import numpy as np
+    return np.random.Generator(np.random.PCG64(seed)).standard_normal(shape, dtype=np.float32)
+
+
+def run_configs(which, steps, warmup):
+    import numpy as np
+    import torch
+    from ggufengine_amd import _native, encode
+    if not _native.available("cuda"):
+        raise SystemExit("libnmq.so not loaded or device is not gfx950")
+    L = _native.lib()
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    threads = min(16, len(os.sched_getaffinity(0)))
+
+    if which in ("q8_0", "all"):
+        # Q8_0 4096x4096, W ~N(0,0.02) (seed 11), x ~N(0,1) (seed 12), batch 1
+        raw = make_weights("Q8_0", 4096, 4096, 11)
+        ws = _copies(torch.from_numpy(raw).cuda())
+        us, err = _mv_case(L, stream, "Q8_0", ws, raw, 4096, 4096, _x(12, (1, 4096)), steps, warmup)
+        del ws
+        _record("q8_0", "Q8_0 4096x4096 batch 1", "Q8_0", us, alg_bytes("Q8_0", 4096, 4096), err)
+
+    if which in ("speculative", "all"):
+        # speculative verification: Q4_K 14336x4096 (seed 31) and 4096x4096 (seed 32), n in 1,2,4,8 (seed 33)
+        for rows, seed in ((14336, 31), (4096, 32)):
+            raw = make_weights("Q4_K", rows, 4096, seed)
+            ws = _copies(torch.from_numpy(raw).cuda())
+            X = _x(33, (8, 4096))
+            for n in (1, 2, 4, 8):
+                us, err = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup)
+                extra = {}
+                if n > 1:
+                    us4, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "0"})
+                    usm, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "2"})
+                    extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
+                _record("speculative", f"Q4_K {rows}x4096 n={n}", "Q4_K", us, alg_bytes("Q4_K", rows, 4096, n), err,
+                        **extra)
+            del ws
+
+    if which in ("lowbit", "all"):
+        # TQ2_0: codes i.i.d. P(0)=0.4, P(+-1)=0.3, d = fp16(|N(0,0.02)|) (seed 51); IQ2_XXS from N(0,0.02)
+        # (seed 52); x seed 53
+        for rows in (4096, 12288):
+            g = np.random.Generator(np.random.PCG64(51))
+            nb = rows * 4096 // 256
+            codes = g.choice(np.array([0, 1, 2], dtype=np.uint8), size=(nb, 256), p=[0.3, 0.4, 0.3])
+            d16 = np.abs(g.standard_normal(nb, dtype=np.float32) * np.float32(0.02)).astype(np.float16)
+            raws = {"TQ2_0": encode.pack_ternary(codes, d16), "IQ2_XXS": make_weights("IQ2_XXS", rows, 4096, 52)}
+            for fmt, raw in raws.items():
+                ws = _copies(torch.from_numpy(raw).cuda())
+                us, err = _mv_case(L, stream, fmt, ws, raw, rows, 4096, _x(53, (1, 4096)), steps, warmup)
+                _record("lowbit", f"{fmt} {rows}x4096 batch 1", fmt, us, alg_bytes(fmt, rows, 4096), err)
+                del ws
+
+    if which in ("moe", "all"):
+        run_moe(steps, warmup, threads)
+
+
+def run_moe(steps, warmup, threads):
+    """Qwen3-30B-A3B-style expert layer: 128 experts, gate/up 768x2048 Q4_K, down 2048x768 Q6_K
+    (seed 41), router logits ~N(0,1) (seed 42) -> top-8 softmax renormalised, x ~N(0,1) (seed 43),
+    1 and 4 tokens.  Timed: the whole expert layer after routing (2 activation quantisations, 3
+    gathered mat-vec launches, silu * up, weighted combine) captured as a HIP graph per copy of the
+    expert tensors and replayed, alternating copies; the eager Python-driven time is reported beside it."""
+    import numpy as np
+    import torch
+    import oracle
+    from ggufengine_amd import encode, experts
+    n_exp, k, E, FF = 128, 8, 2048, 768
+    g = np.random.Generator(np.random.PCG64(41))
+
+    def enc(fmt, rows, n_in):
+        w = g.standard_normal(n_exp * rows * n_in, dtype=np.float32) * np.float32(0.02)
+        return encode.encode(fmt, w, threads=threads)
+    raw = {"gate": enc("Q4_K", FF, E), "up": enc("Q4_K", FF, E), "down": enc("Q6_K", E, FF)}
+    dev = torch.device("cuda", 0)
+    per_set = sum(r.size for r in raw.values())
+    nsets = max(2, -(-2 * LLC_BYTES // per_set))
+    base = {n: torch.from_numpy(r).to(dev) for n, r in raw.items()}
+    sets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(nsets - 1)]
+    layers = [experts.Experten(experts.PackedExperts(s["gate"], 12, n_exp, FF, E),
+                               experts.PackedExperts(s["up"], 12, n_exp, FF, E),
+                               experts.PackedExperts(s["down"], 14, n_exp, E, FF)) for s in sets]
+    per_expert = per_set // n_exp
+    for Ltok in (1, 4):
+        logits = torch.from_numpy(_x(42, (Ltok, n_exp))).to(dev)
+        x = torch.from_numpy(_x(43, (Ltok, E))).to(dev)
+        idx, w = experts.auswahl(logits, k)
+        out = {}
+
+        def go(i):
+            out["y"] = layers[i % nsets](x, idx, w)
+        us_eager = _events_us(go, max(50, steps // 10), max(10, warmup // 10))
+        eager = [layers[j](x, idx, w).clone() for j in range(nsets)]
+        # the layer as the reference runs one step: captured in a graph (one per expert set), replayed
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graphs, outs = [], []
+        with torch.cuda.stream(side):
+            for j in range(nsets):
+                layers[j](x, idx, w)
+        torch.cuda.current_stream().wait_stream(side)
+        for j in range(nsets):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                outs.append(layers[j](x, idx, w))
+            graphs.append(gr)
+        us = _events_us(lambda i: graphs[i % nsets].replay(), steps, warmup)
+        torch.cuda.synchronize()
+        for j in range(nsets):           # every replayed graph still gives the eager result
+            graphs[j].replay()
+            torch.cuda.synchronize()
+            if not torch.equal(outs[j], eager[j]):
+                raise SystemExit(f"moe: graph replay of set {j} differs from the eager layer")
+        out["y"] = outs[0]
+        distinct = len(set(idx.cpu().numpy().reshape(-1).tolist()))
+        ab = distinct * per_expert + Ltok * 4 * E * 2
+        # end to end against the oracle chain on the selected experts (dequantised weights, fp64)
+        ids = idx.cpu().numpy()
+        wts = w.cpu().numpy().astype(np.float64)
+        xb = oracle.round_bf16(x.cpu().numpy())
+        ref = np.zeros((Ltok, E))
+
+        def part(name, e):
+            r = raw[name]
+            return r[e * (r.size // n_exp):(e + 1) * (r.size // n_exp)]
+        for t in range(Ltok):
+            for j in range(k):
+                e = int(ids[t, j])
+                gg = oracle.mv_deq("Q4_K", part("gate", e), FF, E, xb[t:t + 1])[0]
+                uu = oracle.mv_deq("Q4_K", part("up", e), FF, E, xb[t:t + 1])[0]
+                a = oracle.round_bf16((gg / (1.0 + np.exp(-gg)) * uu).astype(np.float32)[None])
+                ref[t] += wts[t, j] * oracle.mv_deq("Q6_K", part("down", e), E, FF, a)[0]
+        err = float(oracle.rel_err_rows(out["y"].cpu().numpy(), ref).max())
+        _record("moe", f"128 experts top-8, {Ltok} token(s)", "Q4_K+Q6_K", us, ab, err,
+                distinct_experts=distinct, expert_sets=nsets, us_eager_python=round(us_eager, 3),
+                timing="graph replay of the whole expert layer")
+        del graphs, outs, eager
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,12 +309,19 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
+    ap.add_argument("--config", default="headline",
+                    choices=("headline", "q8_0", "speculative", "lowbit", "moe", "all"),
+                    help="headline (default): the metric line; the others print one record per case of "
+                         "the other workloads (Q8_0 batch 1, speculative verify n=1..8, TQ2_0/IQ2_XXS, MoE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the mat-vec path is single-GPU "
                                    "(multi-GPU sharding by output rows is described in DESIGN.md, not built)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.config != "headline":
+        run_configs(args.config, min(args.steps, 500), min(args.warmup, 50))
+        return
 
     import numpy as np
     import torch

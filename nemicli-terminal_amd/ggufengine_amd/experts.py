@@ -7,10 +7,11 @@ The reference's expert path around the gathered mat-vec, on this library's kerne
   - `auswahl(logits, k)`: the softmax router of `_Schicht._auswahl` (models/baukasten.py:171-190)
     without the grouped and sigmoid variants: p = softmax(logits), the k largest, their p optionally
     renormalised to sum 1 (+1e-20), times the weights scale.
-  - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  One token:
-    gate/up on the shared input, down on each expert's own activation.  Several tokens: every
-    (token, slot) pair on its own, in (token, slot) order, the weighted sum per token in that fixed
-    order; the shared input of a token is read by its k slots (x_group = k) instead of repeated.
+  - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  Every
+    (token, slot) pair on its own, in (token, slot) order (the reference's one-token and graph paths),
+    the weighted sum per token in that fixed order; gate/up read each token's input, quantised once
+    for both, through its k slots (x_group = k) instead of repeating it; down reads each slot's own
+    activation.
 
 Every expert product runs on libnmq's HIP kernels; without the library the constructor raises.
 """
@@ -59,20 +60,23 @@ class PackedExperts:
         return cudakern.mv(self.name, self.raw, ids, a.reshape(ids.numel(), -1), self.n_out, self.n_in,
                            self.adressen)
 
-    def matvec_tokens(self, ids: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        """ids (L, k), x (L, n_in): expert ids[t, j] applied to token t's input -> (L*k, n_out) float32,
-        rows in (token, slot) order (each token's input quantised once, read by its k slots)."""
+    def matvec_tokens(self, ids: torch.Tensor, x) -> torch.Tensor:
+        """ids (L, k), x (L, n_in) or its Eingang: expert ids[t, j] applied to token t's input ->
+        (L*k, n_out) float32, rows in (token, slot) order (each token's input quantised once, read by its
+        k slots).  A tensor x is rounded to bf16 first, as cudakern.mv does."""
         L_, k = ids.shape
-        flat = ids.reshape(-1).to(x.device, torch.int64).contiguous()
-        e = Eingang(x.reshape(L_, self.n_in).to(torch.bfloat16).contiguous())
-        y = torch.empty(L_ * k, self.n_out, dtype=torch.float32, device=x.device)
+        e = x if isinstance(x, Eingang) else Eingang(x.reshape(L_, self.n_in).to(torch.bfloat16).contiguous())
+        if e.n != L_ * self.n_in:
+            raise ValueError(f"matvec_tokens: input of {e.n} values for {L_} tokens of {self.n_in}")
+        flat = ids.reshape(-1).to(e.xq.device, torch.int64).contiguous()
+        y = torch.empty(L_ * k, self.n_out, dtype=torch.float32, device=e.xq.device)
         if self.adressen is None:
             quelle, per = self.raw, self.raw.shape[1]
         else:
-            quelle, per = self.adressen.to(x.device, torch.int64).contiguous(), -1
+            quelle, per = self.adressen.to(e.xq.device, torch.int64).contiguous(), -1
         _starten("mv_experts", _native.lib().nmq_mv_experts, TYPE_ID[self.name], quelle.data_ptr(), flat.data_ptr(),
                  L_ * k, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, y.data_ptr(),
-                 self.n_out, self.n_in, _native.stream_ptr(x.device))
+                 self.n_out, self.n_in, _native.stream_ptr(e.xq.device))
         return y
 
 
@@ -105,13 +109,11 @@ class Experten:
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights."""
         L_, E = x.shape
-        if L_ == 1:
-            ids = idx[0]
-            g = self.gate.matvec(ids, x[0])
-            u = self.up.matvec(ids, x[0])
-            y = self.down.matvec_je(ids, self._gu(g, u))                       # (k, E)
-            return (y * w[0].float().unsqueeze(-1)).sum(0, keepdim=True)
-        g = self.gate.matvec_tokens(idx, x)
-        u = self.up.matvec_tokens(idx, x)
+        # gate and up read the same tokens: their int8 input is made once (x rounded to bf16 first)
+        e = Eingang(x.to(torch.bfloat16).contiguous())
+        g = self.gate.matvec_tokens(idx, e)
+        u = self.up.matvec_tokens(idx, e)
         y = self.down.matvec_je(idx.reshape(-1), self._gu(g, u))              # (L*k, E)
+        if L_ == 1:
+            return (y * w[0].float().unsqueeze(-1)).sum(0, keepdim=True)
         return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)

@@ -250,6 +250,31 @@ struct Fmt<NMQ_Q6_K> {
     }
 };
 
+// Q6_K unit (one token): decode and reduce one 16-value group at a time (the same sums and fp32
+// operations, in the same order, as decode() + unit_dot(), with a quarter of the decoded registers).
+__device__ __forceinline__ float q6k_dot1(const Fmt<NMQ_Q6_K>::Raw& r, const XSlice& x, int u) {
+    const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+    const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+    const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    const float d = h2f(r.d);
+    const u32 sh = 8u * (u32)(u & 1);
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        int s1 = 0, s2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32 lo = (g & 1) ? lb[k] : la[k];
+            const u32 w = sub32x4(((lo >> (4 * (g >> 1))) & 0x0f0f0f0fu) | (((qh[k] >> (2 * g)) & 0x03030303u) << 4));
+            s1 = dot4(w, x.q[4 * g + k], s1);
+            s2 = dot4(w, x.q2[4 * g + k], s2);
+        }
+        const float ws = d * (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
+        acc += ws * x.d[g] * ((float)s1 + FEIN * (float)s2);
+    }
+    return acc;
+}
+
 // Q8_0, 34-byte blocks (quant.py:46-50, cudakern.py:307-313): unit u = blocks 2u and 2u+1 (68
 // bytes).  The second block is absent when the row has an odd number of blocks and u is the last.
 template <>

@@ -295,27 +295,35 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     const int b0 = slice * bpr, last = b0 + bpr - 1;
     const u8* rowp = p.w + (int64_t)min(row0 + n, p.n_out - 1) * p.row_bytes;
 
-    // input reads of the first round, then the weight reads: the first round's stores wait only for
-    // the older input reads while the weights stream in
+    // One staging round: the input reads first, then (once every wave has issued them) the weight
+    // reads, and the stores wait only for the older input reads.  Several rounds: the input is staged
+    // completely before the weight reads (no input read pending where the two paths meet, which would
+    // make the compiler wait for all outstanding reads).  The CU's vector cache returns data in request
+    // order, so input requested after another wave's weights would wait for them; the barrier between
+    // input and weight reads waits for issue only.
     const int rounds = (p.n_in + 4 * (int)blockDim.x - 1) / (4 * (int)blockDim.x);
-    XStage st;
-    stage_load(st, 0, p);
-    const u64 gv = tab_load<F>();
-    // Every wave's input reads are issued before any wave's weight reads: the CU's vector cache
-    // returns data in request order, so input requested after another wave's weights would wait
-    // for them.  (The barrier waits for issue only, not for the data.)
-    lds_barrier();
-
     typename M::Raw buf[NB];
+    if (rounds == 1) {
+        XStage st;
+        stage_load(st, 0, p);
+        const u64 gv = tab_load<F>();
+        lds_barrier();
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
-    __builtin_amdgcn_sched_barrier(0);
-
-    tab_store<F>(tab, gv);
-    stage_store(st, 0, lds, p);
-    for (int r = 1; r < rounds; ++r) {
-        stage_load(st, r, p);
-        stage_store(st, r, lds, p);
+        for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
+        __builtin_amdgcn_sched_barrier(0);
+        tab_store<F>(tab, gv);
+        stage_store(st, 0, lds, p);
+    } else {
+        for (int r = 0; r < rounds; ++r) {
+            XStage st;
+            stage_load(st, r, p);
+            stage_store(st, r, lds, p);
+        }
+        tab_store<F>(tab, tab_load<F>());
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
     }
     lds_barrier();
 

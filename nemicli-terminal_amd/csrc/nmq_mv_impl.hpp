@@ -164,9 +164,11 @@ __device__ __forceinline__ void tab_store(u64* tab, u64 gv) {
     for (int i = threadIdx.x; i < 128; i += blockDim.x) tab[256 + i] = iq2_sign_mask((u32)i);
 }
 
-// Input staging of the one-token kernels around their first weight reads: round 0 of the input and
-// the table entry go out first, the weight reads (issue()) next, and the stores wait only for the
-// older input reads; later rounds (rows longer than 16 values per thread) follow.
+// Input staging of the one-token kernels around their first weight reads.  One round (the input fits
+// one chunk per thread): its reads and the table entry go out first, the weight reads (issue()) next,
+// and the stores wait only for the older input reads.  Several rounds: everything is staged before
+// the weight reads, so that no input read can still be pending where the two paths meet (a pending
+// read there makes the compiler wait for every outstanding read, the weights included).
 template <int F, typename Issue>
 __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
     using FM = Fmt<F>;
@@ -174,18 +176,25 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
     const int8_t* xq2 = p.xq2 + xrow * p.n_in;
     const float* xd = p.xd + xrow * (p.n_in / 32);
     const float* xs = p.xs + xrow * (p.n_in / 32);
-    XRound r;
-    stage1_load(r, 0, xq, xq2, xd, xs, p.n_in);
-    const u64 gv = tab_load<F>();
-    __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
-    issue();
-    __builtin_amdgcn_sched_barrier(0);
-    tab_store<F>(tab, gv);
-    stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp);
     const int rounds = (p.ktp / 16 + (int)blockDim.x - 1) / (int)blockDim.x;
-    for (int k = 1; k < rounds; ++k) {
-        stage1_load(r, k, xq, xq2, xd, xs, p.n_in);
-        stage1_store<FM::STRIDED>(r, k, lds, p.n_in, p.ktp);
+    if (rounds == 1) {
+        XRound r;
+        stage1_load(r, 0, xq, xq2, xd, xs, p.n_in);
+        const u64 gv = tab_load<F>();
+        __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
+        issue();
+        __builtin_amdgcn_sched_barrier(0);
+        tab_store<F>(tab, gv);
+        stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp);
+    } else {
+        for (int k = 0; k < rounds; ++k) {
+            XRound r;
+            stage1_load(r, k, xq, xq2, xd, xs, p.n_in);
+            stage1_store<FM::STRIDED>(r, k, lds, p.n_in, p.ktp);
+        }
+        tab_store<F>(tab, tab_load<F>());
+        __builtin_amdgcn_sched_barrier(0);
+        issue();
     }
     lds_barrier();
 }
@@ -382,6 +391,8 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
     using FM = Fmt<F>;
     if constexpr (F == NMQ_Q4_K) {
         return q4k_dot1(raw, x, lc.hi[it], lc.t0sh[it]);
+    } else if constexpr (F == NMQ_Q6_K) {
+        return q6k_dot1(raw, x, u);
     } else {
         WUnit wu;
         FM::decode(raw, u, tab, wu);
@@ -463,6 +474,121 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
                                             p.nblk, base + off);
             mv1_compute<F, T, RW, NITM>(buf[i], x, base + off, p.n_out, lt, U, tab, y, lc);
             base += stride;
+        }
+    }
+}
+
+// ---- one token, long rows (more than 128 units of 64 values) ---------------------------------------
+// A wave owns whole rows (RW at a time, T = 64 lanes, NIT units per lane): all of a row group's weights
+// are requested at once; the input is staged once per workgroup in LDS and each unit's slice is read
+// from there as it is used (holding NIT slices in registers would not fit beside the weights).
+// PIPE = false: one row group per wave (the launch has at least as many waves as groups).  PIPE: waves
+// with several row groups request the next group's weights before computing the current one.
+// Q6_K unit against the input staged in LDS (stage_tile layout), one 16-value group at a time:
+// q6k_dot1 with the group's 2 x 16 input bytes and its xd read just before use.
+__device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const u8* base, int ktp, int u) {
+    const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+    const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+    const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    const float d = h2f(r.d);
+    const u32 sh = 8u * (u32)(u & 1);
+    const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+    const float4 xd = *(const float4*)((const float*)(base + 2 * ktp) + 8 * b + 4 * h);
+    const float xdg[4] = {xd.x, xd.y, xd.z, xd.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int ph = swz<true>(16 * b + 8 * h + 2 * g + j);
+        const u32x4 a = *(const u32x4*)(base + 16 * ph);
+        const u32x4 c = *(const u32x4*)(base + ktp + 16 * ph);
+        const u32 xa[4] = {a.x, a.y, a.z, a.w};
+        const u32 xc[4] = {c.x, c.y, c.z, c.w};
+        int s1 = 0, s2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32 lo = (g & 1) ? lb[k] : la[k];
+            const u32 w = sub32x4(((lo >> (4 * (g >> 1))) & 0x0f0f0f0fu) | (((qh[k] >> (2 * g)) & 0x03030303u) << 4));
+            s1 = dot4(w, xa[k], s1);
+            s2 = dot4(w, xc[k], s2);
+        }
+        const float ws = d * (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
+        acc += ws * xdg[g] * ((float)s1 + FEIN * (float)s2);
+    }
+    return acc;
+}
+
+template <int F, int RW, int NIT>
+__device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, const u8* lds, int ktp, int r0,
+                                            int n_out, int lane, int U, const u64* tab, float* y,
+                                            const LaneConst& lc) {
+    using FM = Fmt<F>;
+    float acc[RW];
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) acc[rr] = 0.f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int u = lane + it * 64;
+        const int uc = min(u, U - 1);
+        if constexpr (F == NMQ_Q6_K) {
+#pragma unroll
+            for (int rr = 0; rr < RW; ++rr) {
+                const float v = q6k_dot1_lds(st.raw[rr][it], lds, ktp, uc);
+                acc[rr] += u < U ? v : 0.f;
+            }
+        } else {
+            XSlice x;
+            read_slice<FM::STRIDED>(lds, ktp, uc, x);
+#pragma unroll
+            for (int rr = 0; rr < RW; ++rr) {
+                const float v = unit_dot1<F>(st.raw[rr][it], uc, tab, x, lc, it);
+                acc[rr] += u < U ? v : 0.f;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one input slice live at a time
+    }
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) acc[rr] = team_sum<64>(acc[rr]);
+    if (lane == 0) {
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr)
+            if (r0 + rr < n_out) gpw<float>(y)[r0 + rr] = acc[rr];
+    }
+}
+
+template <int F, int RW, int NIT, bool PIPE>
+__global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int m = blockIdx.y;
+    const u8* wbase = p.w;
+    int64_t xrow = 0;
+    if (p.ids) {
+        const int64_t e = gp<int64_t>(p.ids)[m];
+        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
+        xrow = m / p.x_group;
+    }
+    float* y = p.y + (int64_t)m * p.n_out;
+    const int U = (p.n_in + 63) >> 6;
+    const int stride = gridDim.x * W * RW;
+    int base = (blockIdx.x * W + wave) * RW;
+    Mv1Step<F, 64, RW, NIT> a;
+    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(wbase, p.row_bytes, base, p.n_out, lane, U, p.nblk, base); });
+    const LaneConst lc = lane_const<F, 64, NIT>(lane);
+    if constexpr (!PIPE) {
+        // the launch gives every wave at most one row group (grid x W >= groups)
+        if (base < p.n_out) mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+    } else {
+        Mv1Step<F, 64, RW, NIT> b;
+        for (;;) {
+            b.load(wbase, p.row_bytes, base + stride, p.n_out, lane, U, p.nblk, base);
+            mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+            base += stride;
+            if (base >= p.n_out) return;
+            a.load(wbase, p.row_bytes, base + stride, p.n_out, lane, U, p.nblk, base);
+            mvl_compute<F, RW, NIT>(b, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+            base += stride;
+            if (base >= p.n_out) return;
         }
     }
 }
@@ -649,13 +775,53 @@ inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     int64_t waves = (int64_t)wpc * di.cus / n_mats;
     if (waves < 1) waves = 1;
     if (waves > steps) waves = steps;
-    const int wmax = env_int("NMQ_MV1_W", 8);
+    int wmax = env_int("NMQ_MV1_W", 8);
+    wmax = wmax < 1 ? 1 : (wmax > 8 ? 8 : wmax);  // launch bound: 512 threads
     s.W = (int)(waves < wmax ? waves : wmax);
     s.grid_x = (int)((waves + s.W - 1) / s.W);
     s.ktp = (n_in + 127) / 128 * 128;
     s.lds = (size_t)s.ktp * 9 / 4;
     s.ok = s.lds <= (size_t)di.lds_max;
     return s;
+}
+
+// Long rows at one token: T = 64 lanes per row, NIT = 3 or 4 units per lane (129..256 units = up to
+// 16384 values); one row per wave while the rows fit the resident waves (NMQ_MVL_WPC = 16 per CU),
+// otherwise the pipelined variant.  The input (2.25 bytes per value) must fit the workgroup's LDS.
+struct MvlShape {
+    bool ok;
+    int nit, W, grid_x, ktp;
+    bool pipe;
+    size_t lds;
+};
+
+inline MvlShape plan_mvl(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
+    MvlShape s{};
+    const int U = (n_in + 63) / 64;
+    if (U <= 128 || U > 256 || !env_int("NMQ_MVL", 1)) return s;
+    s.nit = U <= 192 ? 3 : 4;
+    int64_t waves_max = (int64_t)env_int("NMQ_MVL_WPC", 16) * di.cus / n_mats;
+    if (waves_max < 1) waves_max = 1;
+    const int64_t groups = n_out;  // RW = 1
+    s.pipe = groups > waves_max;
+    int64_t waves = groups < waves_max ? groups : waves_max;
+    if (waves < 1) waves = 1;
+    const int wcap = s.pipe ? 8 : 16;  // launch bounds: 512 / 1024 threads
+    int wmax = env_int("NMQ_MVL_W", s.pipe ? 8 : 4);  // measured on MI355X: 4-wave workgroups (several
+                                                       // per CU) beat one 16-wave workgroup per CU
+    wmax = wmax < 1 ? 1 : (wmax > wcap ? wcap : wmax);
+    s.W = (int)(waves < wmax ? waves : wmax);
+    s.grid_x = (int)((waves + s.W - 1) / s.W);
+    s.ktp = (n_in + 127) / 128 * 128;
+    s.lds = (size_t)s.ktp * 9 / 4;
+    s.ok = s.lds <= (size_t)di.lds_max;
+    return s;
+}
+
+template <int F>
+inline MvKernel pick_mvl(int nit, bool pipe) {
+    if (nit == 3) return pipe ? mvl_kernel<F, 1, 3, true> : mvl_kernel<F, 1, 3, false>;
+    return pipe ? mvl_kernel<F, 1, 4, true> : mvl_kernel<F, 1, 4, false>;
 }
 
 template <int F, int T>
@@ -691,10 +857,11 @@ inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     if (wgs < 1) wgs = 1;
     const int64_t R = ((int64_t)n_out + wgs - 1) / wgs;  // rows per workgroup
     int rw = env_int("NMQ_MVC_RW", 0);
-    if (rw == 0) {
+    if (rw <= 0) {
         rw = 1;
         while (rw < 8 && R > (int64_t)P * rw * 16) rw *= 2;
     }
+    rw = rw <= 1 ? 1 : (rw <= 2 ? 2 : (rw <= 4 ? 4 : 8));  // the instantiated widths
     const int wmax = rw >= 8 ? 8 : 16;
     int64_t W = (R + P * rw - 1) / (P * rw);
     if (W > wmax) W = wmax;
@@ -739,6 +906,15 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             p.ktp = sc.ktp;
             MvKernel k = pick_mvc<F>(sc.T, sc.rw);
             hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(64 * sc.W), sc.lds, stream, p);
+            return (int)hipGetLastError();
+        }
+    }
+    if (nc == 1) {
+        const MvlShape sl = plan_mvl(p.n_out, p.n_in, n_mats, di);
+        if (sl.ok) {
+            p.ktp = sl.ktp;
+            MvKernel k = pick_mvl<F>(sl.nit, sl.pipe);
+            hipLaunchKernelGGL(k, dim3((unsigned)sl.grid_x, (unsigned)n_mats), dim3(64 * sl.W), sl.lds, stream, p);
             return (int)hipGetLastError();
         }
     }

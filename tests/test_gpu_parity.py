@@ -129,6 +129,28 @@ def test_mv_one_token(nmq, oracle, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("n_in", [10240, 14336, 16384])
+@pytest.mark.parametrize("pipelined", [False, True])
+def test_mv_one_token_long_rows(nmq, oracle, monkeypatch, fmt, n_in, pipelined):
+    """One token on rows of 160..256 units of 64 values (the Llama down projection has 224): one row
+    per wave, and (with fewer resident waves than rows) the variant that cycles two row buffers."""
+    n_out = 300
+    if pipelined:
+        monkeypatch.setenv("NMQ_MVL_WPC", "1")   # 1 wave per CU: fewer waves than rows
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=81)
+    x = np.random.default_rng(82).standard_normal((1, n_in)).astype(np.float32)
+    x[0, 5] = 25.0
+    say("mv long rows", fmt, n_in, pipelined)
+    e = quant_dev(dev(x))
+    y = torch.full((1, n_out), float("nan"), device="cuda")
+    from ggufengine_amd.gguf_types import TYPE_ID
+    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+                               e.xs.data_ptr(), y.data_ptr(), n_out, n_in, 1, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("nc", [2, 3, 4, 5, 8, 9, 16])
 def test_mv_tokens(nmq, oracle, fmt, nc):
     n_out, n_in = (300, 1280) if fmt != "Q8_0" else (300, 1056)

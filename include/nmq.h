@@ -35,7 +35,8 @@ extern "C" {
 /* Tokens handled by one launch of the mat-vec kernels; nmq_mv loops over larger counts. */
 #define NMQ_MAX_COLS 8
 
-/* ABI version of this header (bumped on incompatible changes). */
+/* ABI version of this header, bumped on incompatible changes (2: nmq_quant_q8 mode 2, the fused
+ * expert entry points). */
 int nmq_abi_version(void);
 
 /* Text for a return code of any entry point (static storage). */
@@ -53,13 +54,25 @@ int nmq_device_arch(char* buf, int len);
 
 /*
  * Two-stage int8 activation ("Eingang").  Replaces the `quant_q8` launch of mmvq.Eingang
- * (mmvq.py:62-83, 825-843).  x: n values (fp32 if x_is_f32, else bf16), n % 32 == 0; several token
- * rows may be passed back to back.  Per 32 values g:
+ * (mmvq.py:62-83, 825-843).  x: n values, n % 32 == 0; several token rows may be passed back to
+ * back.  x_is_f32: 0 bf16; 1 fp32; 2 fp32 rounded to bf16 first (nearest even), the input the
+ * reference's cudakern entry points form (cudakern.py:764).  Per 32 values g:
  *   xd[g] = max|x| / 127, xq = rint(x / xd), xq2 = clamp(rint((x - xq*xd) / (xd/254)), +-127),
  *   xs[g] = sum of the 32 values.
  */
 int nmq_quant_q8(const void* x, int x_is_f32, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
                  void* stream);
+
+/*
+ * The gated activation of an expert MLP, made the down projection's two-stage input in one launch:
+ * a = bf16(silu(g) * u) (silu(g) = g / (1 + exp(-g)), fp32, then rounded to bf16 nearest even),
+ * then the two-stage quantisation of nmq_quant_q8.  g, u: fp32[n], n % 32 == 0.  Replaces the
+ * `silu(gate) * up` of Experten._gu (models/moe.py:252-255) followed by cudakern.mv's bf16 cast and
+ * the input quantisation of the down call (the reference's fused one-token path does the same in
+ * mmvq.akt_q8, mmvq.py:959-966).
+ */
+int nmq_silu_mul_quant(const float* g, const float* u, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
+                       void* stream);
 
 /*
  * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of NMQ_MAX_COLS tokens).
@@ -88,6 +101,24 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
 int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_t per_expert,
                    const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int x_group,
                    float* y, int n_out, int n_in, void* stream);
+
+/*
+ * Two expert tensors of the same format and shape (gate and up) on the same ids and inputs in one
+ * launch: y[j] = A_{ids[j]} x_(j / x_group) and y[n_ids + j] = B_{ids[j]} x_(j / x_group) for
+ * j < n_ids (n_ids <= 32767); w_a, w_b, per_expert as in nmq_mv_experts.  y: fp32 (2 n_ids x n_out).
+ * Replaces the gate and up calls of Experten (models/moe.py:270-274, PackedExperts.matvec), two
+ * launches of the gathered kernel, with one.
+ */
+int nmq_mv_experts2(int fmt, const void* w_a, const void* w_b, const int64_t* ids, int n_ids, int64_t per_expert,
+                    const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int x_group,
+                    float* y, int n_out, int n_in, void* stream);
+
+/*
+ * Weighted combine of expert outputs: out[t][e] = sum_{j<k} w[t*k + j] * y[t*k + j][e], the slots j
+ * added in order (fp32 fused multiply-adds).  y: fp32 (L*k x E), w: fp32 (L x k), out: fp32 (L x E).
+ * Replaces the `(y * w).sum(...)` combine of Experten.__call__ (models/moe.py:275-277, 319-320).
+ */
+int nmq_moe_combine(const float* y, const float* w, int L, int k, int E, float* out, void* stream);
 
 /*
  * Diagnostic: the int32 sums the mat-vec kernels form, per 16 weights, for one token:

@@ -33,18 +33,39 @@ DeviceInfo device_info() {
 
 // ---- two-stage int8 activation (reference mmvq.py:59-83) ----------------------------------------
 // One lane per value, 32 lanes (half a wave) per group.  max|x| and the sum use the xor butterfly
-// over offsets 16, 8, 4, 2, 1 (never crossing the 32-lane half), in the order of mmvq.py:42-46.
+// over offsets 16, 8, 4, 2, 1 (never crossing the 32-lane half), in the order of mmvq.py:42-46
+// (half_max / half_sum_xor: one swizzle and four DPP rotations per reduction).
 // d = max / 127 and the quotients are IEEE divisions (the library is built without fast-math);
 // the residual x - q*d is one fused multiply-add (the CPU oracle does the same).
-__global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ x, int f32, int8_t* __restrict__ xq,
-                                                        int8_t* __restrict__ xq2, float* __restrict__ xd,
-                                                        float* __restrict__ xs, int64_t n) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// Input modes: 0 bf16; 1 fp32; 2 fp32 rounded to bf16 first (what the reference's cudakern entry
+// points do to their input, cudakern.py:764); 3 silu(g) * u in fp32 (g = x, u second operand), then
+// rounded to bf16 (the gated activation of a MoE expert fed to the down projection as bf16).
+__device__ __forceinline__ float round_bf16(float f) {
+    const u32 u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);  // NaN
+    return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ x, const float* __restrict__ u2,
+                                                        int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
+                                                        float* __restrict__ xd, float* __restrict__ xs, int64_t n) {
+    // every argument in the first batch of scalar loads (the compiler would otherwise fetch some of
+    // them behind the branches below, one dependent round trip each)
+    asm volatile("" ::"s"(x), "s"(u2), "s"(xq), "s"(xq2), "s"(xd), "s"(xs), "s"(n));
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads
     if ((i & ~(int64_t)31) >= n) return;  // whole 32-lane groups only (n % 32 == 0)
-    const float v = f32 ? ((const float*)x)[i] : __uint_as_float((u32)((const u16*)x)[i] << 16);
-    float a = fabsf(v);
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) a = fmaxf(a, __shfl_xor(a, o));
+    float v;
+    if constexpr (MODE == 0) {
+        v = __uint_as_float((u32)((const u16*)x)[i] << 16);
+    } else if constexpr (MODE == 3) {
+        const float g = ((const float*)x)[i];
+        v = round_bf16(g / (1.0f + expf(-g)) * u2[i]);
+    } else {
+        v = ((const float*)x)[i];
+        if constexpr (MODE == 2) v = round_bf16(v);
+    }
+    const float a = half_max(fabsf(v));
     const float d = a / 127.0f;
     int q = 0, q2 = 0;
     if (d > 0.0f) {
@@ -53,15 +74,26 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ 
         q2 = (int)rintf(r / (d * FEIN));
         q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
     }
-    float s = v;
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    const float s = half_sum_xor(v);
     xq[i] = (int8_t)q;
     xq2[i] = (int8_t)q2;
     if ((threadIdx.x & 31) == 0) {
         xd[i >> 5] = d;
         xs[i >> 5] = s;
     }
+}
+
+// ---- weighted combine of expert outputs (reference models/moe.py:275-277, 319-320) --------------
+// out[t][e] = sum_j w[t*k + j] * y[t*k + j][e], j = 0..k-1 in this order (a fixed order).
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y, const float* __restrict__ w,
+                                                           int L, int k, int E, float* __restrict__ out) {
+    asm volatile("" ::"s"(y), "s"(w), "s"(L), "s"(k), "s"(E), "s"(out));
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)L * E) return;
+    const int t = (int)(i / E), e = (int)(i % E);
+    float acc = 0.f;
+    for (int j = 0; j < k; ++j) acc = fmaf(gp<float>(w)[(int64_t)t * k + j], gp<float>(y)[((int64_t)t * k + j) * E + e], acc);
+    gpw<float>(out)[i] = acc;
 }
 
 // ---- diagnostic: per-16 integer sums, through the same unit decoders as mv_kernel ---------------
@@ -71,10 +103,10 @@ __global__ __launch_bounds__(256) void block_sums_kernel(const u8* __restrict__ 
                                                           int32_t* __restrict__ s2, int n_out, int n_in) {
     using FM = Fmt<F>;
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
-    fill_tables<F>(tab);
+    fill_tables<F>(tab, 256);
     __syncthreads();
     const int units = (n_in + 63) / 64, nblk = n_in / FM::BV;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads
     if (idx >= (int64_t)n_out * units) return;
     const int row = (int)(idx / units), u = (int)(idx % units);
     typename FM::Raw raw;
@@ -122,13 +154,13 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const u8* __restrict_
 #pragma clang fp contract(off)
     using FM = Fmt<F>;
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
-    fill_tables<F>(tab);
+    fill_tables<F>(tab, 256);
     __syncthreads();
     // a "row" of one block; Q8_0 units span two blocks, so Q8_0 rows are two blocks (last may be one)
     constexpr int BPU = FM::BV == 32 ? 2 : 1;  // blocks per row handled here
     constexpr int UPR = FM::BV == 32 ? 1 : 4;  // units per row
     const int64_t rows = (n_blocks + BPU - 1) / BPU;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads
     if (idx >= rows * UPR) return;
     const int64_t row = idx / UPR;
     const int u = (int)(idx % UPR);
@@ -219,7 +251,7 @@ static bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) =
 
 extern "C" {
 
-int nmq_abi_version(void) { return 1; }
+int nmq_abi_version(void) { return 2; }
 
 const char* nmq_strerror(int code) {
     switch (code) {
@@ -260,11 +292,37 @@ int nmq_device_arch(char* buf, int len) {
 int nmq_quant_q8(const void* x, int x_is_f32, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
                  void* stream) {
     if (!x || !xq || !xq2 || !xd || !xs) return NMQ_ERR_ARG;
+    if (x_is_f32 < 0 || x_is_f32 > 2) return NMQ_ERR_ARG;
     if (n <= 0 || n % 32) return NMQ_ERR_SHAPE;
     const int64_t blocks = (n + 255) / 256;
     if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
-    hipLaunchKernelGGL(quant_q8_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, x, x_is_f32, xq,
-                       xq2, xd, xs, n);
+    const dim3 g((unsigned)blocks), b(256);
+    const hipStream_t s = (hipStream_t)stream;
+    if (x_is_f32 == 0) hipLaunchKernelGGL(quant_q8_kernel<0>, g, b, 0, s, x, nullptr, xq, xq2, xd, xs, n);
+    else if (x_is_f32 == 1) hipLaunchKernelGGL(quant_q8_kernel<1>, g, b, 0, s, x, nullptr, xq, xq2, xd, xs, n);
+    else hipLaunchKernelGGL(quant_q8_kernel<2>, g, b, 0, s, x, nullptr, xq, xq2, xd, xs, n);
+    return (int)hipGetLastError();
+}
+
+int nmq_silu_mul_quant(const float* g, const float* u, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
+                       void* stream) {
+    if (!g || !u || !xq || !xq2 || !xd || !xs) return NMQ_ERR_ARG;
+    if (!aligned(g, 4) || !aligned(u, 4)) return NMQ_ERR_ARG;
+    if (n <= 0 || n % 32) return NMQ_ERR_SHAPE;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    hipLaunchKernelGGL(quant_q8_kernel<3>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, g, u, xq, xq2,
+                       xd, xs, n);
+    return (int)hipGetLastError();
+}
+
+int nmq_moe_combine(const float* y, const float* w, int L, int k, int E, float* out, void* stream) {
+    if (!y || !w || !out || !aligned(y, 4) || !aligned(w, 4) || !aligned(out, 4)) return NMQ_ERR_ARG;
+    if (L < 1 || k < 1 || E < 1 || (int64_t)L * k > 65535) return NMQ_ERR_SHAPE;
+    const int64_t blocks = ((int64_t)L * E + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, y, w, L, k, E,
+                       out);
     return (int)hipGetLastError();
 }
 
@@ -307,12 +365,8 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
     return NMQ_OK;
 }
 
-int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_t per_expert, const int8_t* xq,
-                   const int8_t* xq2, const float* xd, const float* xs, int x_group, float* y, int n_out, int n_in,
-                   void* stream) {
-    int e = check_mv(fmt, w, xq, xq2, xd, xs, y, n_out, n_in);
-    if (e) return e;
-    if (!ids || n_ids < 1 || n_ids > 65535 || x_group < 1) return NMQ_ERR_ARG;
+static int check_experts(int fmt, const void* w, int n_ids, int64_t per_expert, int x_group, int n_out, int n_in) {
+    if (n_ids < 1 || n_ids > 65535 || x_group < 1) return NMQ_ERR_ARG;
     if (per_expert >= 0) {
         int bv, bb;
         nmq_format_info(fmt, &bv, &bb);
@@ -322,6 +376,17 @@ int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_
     } else if (!aligned(w, 8)) {
         return NMQ_ERR_ARG;
     }
+    return NMQ_OK;
+}
+
+int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_t per_expert, const int8_t* xq,
+                   const int8_t* xq2, const float* xd, const float* xs, int x_group, float* y, int n_out, int n_in,
+                   void* stream) {
+    int e = check_mv(fmt, w, xq, xq2, xd, xs, y, n_out, n_in);
+    if (e) return e;
+    if (!ids) return NMQ_ERR_ARG;
+    e = check_experts(fmt, w, n_ids, per_expert, x_group, n_out, n_in);
+    if (e) return e;
     MvParams p{};
     p.w = (const u8*)w;
     p.ids = ids;
@@ -334,7 +399,37 @@ int nmq_mv_experts(int fmt, const void* w, const int64_t* ids, int n_ids, int64_
     p.n_out = n_out;
     p.n_in = n_in;
     p.x_group = x_group;
+    p.n_ids = n_ids;
     return launch_any(fmt, p, 1, n_ids, (hipStream_t)stream);
+}
+
+int nmq_mv_experts2(int fmt, const void* w_a, const void* w_b, const int64_t* ids, int n_ids, int64_t per_expert,
+                    const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int x_group, float* y,
+                    int n_out, int n_in, void* stream) {
+    int e = check_mv(fmt, w_a, xq, xq2, xd, xs, y, n_out, n_in);
+    if (e) return e;
+    e = check_mv(fmt, w_b, xq, xq2, xd, xs, y, n_out, n_in);
+    if (e) return e;
+    if (!ids || n_ids > 32767) return NMQ_ERR_ARG;
+    e = check_experts(fmt, w_a, n_ids, per_expert, x_group, n_out, n_in);
+    if (e) return e;
+    e = check_experts(fmt, w_b, n_ids, per_expert, x_group, n_out, n_in);
+    if (e) return e;
+    MvParams p{};
+    p.w = (const u8*)w_a;
+    p.w2 = (const u8*)w_b;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xq = xq;
+    p.xq2 = xq2;
+    p.xd = xd;
+    p.xs = xs;
+    p.y = y;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    p.x_group = x_group;
+    p.n_ids = n_ids;
+    return launch_any(fmt, p, 1, 2 * n_ids, (hipStream_t)stream);
 }
 
 int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2, int n_out,

@@ -42,6 +42,36 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// Xor butterflies over the 32 lanes of each half-wave with offsets 16, 8, 4, 2, 1 (the tree of the
+// reference's warp_sum, mmvq.py:42-46): the xor-16 level by ds_swizzle (bitmask mode, inside 32
+// lanes), the others by DPP rotations of 16-lane rows.  After the xor-16 level a lane's partial
+// depends only on its index modulo 16, after xor 8 modulo 8, and so on, so rotating the row by 8, 4,
+// 2, 1 hands each lane a copy of its xor partner's partial: the same additions (own + partner) as
+// the xor butterfly, hence bit-identical sums.  All 32 lanes of a half-wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
+}
+__device__ __forceinline__ float half_sum_xor(float v) {
+    v += swz_xor16(v);
+    v += dpp_f<0x128>(v);  // row_ror:8
+    v += dpp_f<0x124>(v);  // row_ror:4
+    v += dpp_f<0x122>(v);  // row_ror:2
+    v += dpp_f<0x121>(v);  // row_ror:1
+    return v;
+}
+__device__ __forceinline__ float half_max(float v) {
+    v = fmaxf(v, swz_xor16(v));
+    v = fmaxf(v, dpp_f<0x128>(v));
+    v = fmaxf(v, dpp_f<0x124>(v));
+    v = fmaxf(v, dpp_f<0x122>(v));
+    v = fmaxf(v, dpp_f<0x121>(v));
+    return v;
+}
+
 __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (u16)(bits16 & 0xffffu));
 }

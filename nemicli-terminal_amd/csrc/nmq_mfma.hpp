@@ -193,7 +193,7 @@ struct XStage {
 };
 
 __device__ __forceinline__ void stage_load(XStage& st, int r, const MvmParams& p) {
-    const int T = blockDim.x, S = p.n_in / 32;
+    const int T = 64 * p.ks * p.tpw, S = p.n_in / 32;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = (4 * r + j) * T + (int)threadIdx.x;
@@ -209,7 +209,7 @@ __device__ __forceinline__ void stage_load(XStage& st, int r, const MvmParams& p
 }
 
 __device__ __forceinline__ void stage_store(const XStage& st, int r, u8* lds, const MvmParams& p) {
-    const int T = blockDim.x, S = p.n_in / 32;
+    const int T = 64 * p.ks * p.tpw, S = p.n_in / 32;
     u64* frag = (u64*)lds;
     float2* xsc = (float2*)(lds + (size_t)S * 512);
 #pragma unroll
@@ -280,6 +280,9 @@ __device__ __forceinline__ void mvm_block(const typename Mfma<F>::Raw& cur, int 
 template <int F, int NB, bool RING>
 __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     using M = Mfma<F>;
+    // every argument into the first batch of scalar loads (see args_early)
+    asm volatile("" ::"s"(p.w), "s"(p.xq), "s"(p.xq2), "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in),
+                 "s"(p.nc), "s"(p.ks), "s"(p.tpw), "s"(p.row_bytes), "s"(p.nblk));
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -301,7 +304,8 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     // make the compiler wait for all outstanding reads).  The CU's vector cache returns data in request
     // order, so input requested after another wave's weights would wait for them; the barrier between
     // input and weight reads waits for issue only.
-    const int rounds = (p.n_in + 4 * (int)blockDim.x - 1) / (4 * (int)blockDim.x);
+    const int nt = 64 * p.ks * p.tpw;  // threads of the workgroup, from the arguments (see args_early)
+    const int rounds = (p.n_in + 4 * nt - 1) / (4 * nt);
     typename M::Raw buf[NB];
     if (rounds == 1) {
         XStage st;
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
 #pragma unroll
         for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
         __builtin_amdgcn_sched_barrier(0);
-        tab_store<F>(tab, gv);
+        tab_store<F>(tab, gv, nt);
         stage_store(st, 0, lds, p);
     } else {
         for (int r = 0; r < rounds; ++r) {
@@ -320,7 +324,7 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
             stage_load(st, r, p);
             stage_store(st, r, lds, p);
         }
-        tab_store<F>(tab, tab_load<F>());
+        tab_store<F>(tab, tab_load<F>(), nt);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);

@@ -37,7 +37,38 @@ struct MvParams {
     int n_tiles;
     int groups;    // row groups per workgroup
     int nblk;      // blocks per row
+    int nt;        // threads per workgroup, set by the launcher (the built-in block size is read from the
+                   // launch's hidden arguments by a dependent scalar and vector load at kernel entry)
+    const u8* w2;  // experts: a second expert tensor (same format and shape) for instances n_ids.. 2 n_ids-1
+    int n_ids;     // experts: entries of ids (instances per expert tensor)
 };
+
+// Weights and input row of instance m (blockIdx.y).  One matrix: w, input row 0.  Experts: instance m
+// reads expert ids[m'] of tensor w (m' = m) or, with a second tensor, of w2 (m' = m - n_ids for
+// m >= n_ids), at ids[m'] * per_expert bytes or at the address table entry ids[m']; its input row is
+// m' / x_group.
+__device__ __forceinline__ const u8* instance_weights(const MvParams& p, int m, int64_t& xrow) {
+    if (!p.ids) {
+        xrow = 0;
+        return p.w;
+    }
+    const bool second = p.w2 != nullptr && m >= p.n_ids;
+    const int mm = second ? m - p.n_ids : m;
+    const int64_t e = gp<int64_t>(p.ids)[mm];
+    xrow = mm / p.x_group;
+    const u8* base = second ? p.w2 : p.w;
+    return p.per_expert >= 0 ? base + e * p.per_expert : (const u8*)(gp<int64_t>(base)[e]);
+}
+
+// Every kernel argument (and the launch shape) into the first batch of scalar loads at kernel entry:
+// left alone, the compiler fetches some of them behind branches, one dependent round trip each.
+// The asm statement is empty; it only makes the values live in scalar registers at that point.
+__device__ __forceinline__ void args_early(const MvParams& p) {
+    asm volatile("" ::"s"(p.w), "s"(p.ids), "s"(p.per_expert), "s"(p.row_bytes), "s"(p.xq), "s"(p.xq2),
+                 "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in), "s"(p.x_group), "s"(p.kt),
+                 "s"(p.ktp), "s"(p.n_tiles), "s"(p.groups), "s"(p.nblk), "s"(p.nt), "s"(p.w2), "s"(p.n_ids),
+                 "s"(gridDim.x));
+}
 
 // 16-byte chunk permutations of the LDS input (bijective inside every aligned group of 8 chunks).
 template <bool STRIDED>
@@ -47,8 +78,8 @@ __device__ __forceinline__ int swz(int ch) {
 
 template <bool STRIDED>
 __device__ __forceinline__ void stage_tile(u8* lds, const int8_t* xq, const int8_t* xq2, const float* xd,
-                                           const float* xs, int n_in, int nc, int k0, int kt, int ktp) {
-    const int tid = threadIdx.x, nt = blockDim.x;
+                                           const float* xs, int n_in, int nc, int k0, int kt, int ktp, int nt) {
+    const int tid = threadIdx.x;
     const int tok = (ktp * 9) / 4;
     for (int c = 0; c < nc; ++c) {
         u8* base = lds + c * tok;
@@ -119,8 +150,8 @@ struct XRound {
 };
 
 __device__ __forceinline__ void stage1_load(XRound& r, int rnd, const int8_t* xq, const int8_t* xq2, const float* xd,
-                                            const float* xs, int n_in) {
-    const int i = rnd * (int)blockDim.x + (int)threadIdx.x;
+                                            const float* xs, int n_in, int nt) {
+    const int i = rnd * nt + (int)threadIdx.x;
     const int ch = 16 * i < n_in ? i : 0;
     r.a = *gp<u32x4>(xq + 16 * ch);
     r.b = *gp<u32x4>(xq2 + 16 * ch);
@@ -130,8 +161,8 @@ __device__ __forceinline__ void stage1_load(XRound& r, int rnd, const int8_t* xq
 }
 
 template <bool STRIDED>
-__device__ __forceinline__ void stage1_store(const XRound& r, int rnd, u8* lds, int n_in, int ktp) {
-    const int i = rnd * (int)blockDim.x + (int)threadIdx.x;
+__device__ __forceinline__ void stage1_store(const XRound& r, int rnd, u8* lds, int n_in, int ktp, int nt) {
+    const int i = rnd * nt + (int)threadIdx.x;
     if (i < ktp / 16) {
         const bool ok = 16 * i < n_in;
         const int ph = swz<STRIDED>(i);
@@ -154,14 +185,14 @@ __device__ __forceinline__ u64 tab_load() {
 }
 
 template <int F>
-__device__ __forceinline__ void tab_store(u64* tab, u64 gv) {
+__device__ __forceinline__ void tab_store(u64* tab, u64 gv, int nt) {
     if (F != NMQ_IQ2_XXS) return;
-    if (blockDim.x >= 256) {
+    if (nt >= 256) {
         if (threadIdx.x < 256) tab[threadIdx.x] = gv;
     } else {
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) tab[i] = IQ2XXS_GRID[i];
+        for (int i = threadIdx.x; i < 256; i += nt) tab[i] = IQ2XXS_GRID[i];
     }
-    for (int i = threadIdx.x; i < 128; i += blockDim.x) tab[256 + i] = iq2_sign_mask((u32)i);
+    for (int i = threadIdx.x; i < 128; i += nt) tab[256 + i] = iq2_sign_mask((u32)i);
 }
 
 // Input staging of the one-token kernels around their first weight reads.  One round (the input fits
@@ -176,23 +207,24 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
     const int8_t* xq2 = p.xq2 + xrow * p.n_in;
     const float* xd = p.xd + xrow * (p.n_in / 32);
     const float* xs = p.xs + xrow * (p.n_in / 32);
-    const int rounds = (p.ktp / 16 + (int)blockDim.x - 1) / (int)blockDim.x;
+    const int nt = p.nt;
+    const int rounds = (p.ktp / 16 + nt - 1) / nt;
     if (rounds == 1) {
         XRound r;
-        stage1_load(r, 0, xq, xq2, xd, xs, p.n_in);
+        stage1_load(r, 0, xq, xq2, xd, xs, p.n_in, nt);
         const u64 gv = tab_load<F>();
         __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
         issue();
         __builtin_amdgcn_sched_barrier(0);
-        tab_store<F>(tab, gv);
-        stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp);
+        tab_store<F>(tab, gv, nt);
+        stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp, nt);
     } else {
         for (int k = 0; k < rounds; ++k) {
             XRound r;
-            stage1_load(r, k, xq, xq2, xd, xs, p.n_in);
-            stage1_store<FM::STRIDED>(r, k, lds, p.n_in, p.ktp);
+            stage1_load(r, k, xq, xq2, xd, xs, p.n_in, nt);
+            stage1_store<FM::STRIDED>(r, k, lds, p.n_in, p.ktp, nt);
         }
-        tab_store<F>(tab, tab_load<F>());
+        tab_store<F>(tab, tab_load<F>(), nt);
         __builtin_amdgcn_sched_barrier(0);
         issue();
     }
@@ -200,15 +232,16 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
 }
 
 template <int F>
-__device__ __forceinline__ void fill_tables(u64* tab) {
+__device__ __forceinline__ void fill_tables(u64* tab, int nt) {
     if (F == NMQ_IQ2_XXS) {
-        for (int i = threadIdx.x; i < 384; i += blockDim.x)
+        for (int i = threadIdx.x; i < 384; i += nt)
             tab[i] = i < 256 ? IQ2XXS_GRID[i] : iq2_sign_mask((u32)(i - 256));
     }
 }
 
 template <int F, int NC, int T, int RW>
 __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
+    args_early(p);
     using FM = Fmt<F>;
     constexpr bool S = FM::STRIDED;
     constexpr int TW = T > 64 ? T / 64 : 1;  // waves per team
@@ -218,26 +251,21 @@ __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     __shared__ float red[T > 64 ? 4 * RW * NC : 1];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, W = blockDim.x >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, W = p.nt >> 6;
     const int team = T >= 64 ? wave / TW : wave * P + lane / T;
     const int lt = T >= 64 ? (wave % TW) * 64 + lane : lane % T;
     const int teams = T >= 64 ? W / TW : W * P;
     const int m = blockIdx.y;
 
-    const u8* wbase = p.w;
-    int64_t xrow = 0;
-    if (p.ids) {
-        const int64_t e = gp<int64_t>(p.ids)[m];
-        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
-        xrow = m / p.x_group;
-    }
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, m, xrow);
     const int8_t* xq = p.xq + xrow * p.n_in;
     const int8_t* xq2 = p.xq2 + xrow * p.n_in;
     const float* xd = p.xd + xrow * (p.n_in / 32);
     const float* xs = p.xs + xrow * (p.n_in / 32);
     float* y = p.y + (int64_t)m * NC * p.n_out;
 
-    fill_tables<F>(tab);
+    fill_tables<F>(tab, p.nt);
     const int tok = (p.ktp * 9) / 4;
     const int rows_iter = teams * RW;
     const int row_wg = blockIdx.x * p.groups * rows_iter;
@@ -267,7 +295,7 @@ __global__ __launch_bounds__(256) void mv_kernel(MvParams p) {
             }
             if (p.n_tiles > 1 || g == 0) {
                 __syncthreads();
-                stage_tile<S>(lds, xq, xq2, xd, xs, p.n_in, NC, k0, kt, p.ktp);
+                stage_tile<S>(lds, xq, xq2, xd, xs, p.n_in, NC, k0, kt, p.ktp, p.nt);
                 __syncthreads();
             }
             for (int it = 0; it < nit; ++it) {
@@ -426,20 +454,16 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
 
 template <int F, int T, int RW, int NITM, int NBUF>
 __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
+    args_early(p);
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
     const int team = lane / T, lt = lane % T;
     const int m = blockIdx.y;
-    const u8* wbase = p.w;
-    int64_t xrow = 0;
-    if (p.ids) {
-        const int64_t e = gp<int64_t>(p.ids)[m];
-        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
-        xrow = m / p.x_group;
-    }
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, m, xrow);
     float* y = p.y + (int64_t)m * p.n_out;
     const int U = (p.n_in + 63) >> 6;
     const int gw = blockIdx.x * W + wave, nw = gridDim.x * W;
@@ -557,17 +581,13 @@ __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, c
 
 template <int F, int RW, int NIT, bool PIPE>
 __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
+    args_early(p);
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
     const int m = blockIdx.y;
-    const u8* wbase = p.w;
-    int64_t xrow = 0;
-    if (p.ids) {
-        const int64_t e = gp<int64_t>(p.ids)[m];
-        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
-        xrow = m / p.x_group;
-    }
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, m, xrow);
     float* y = p.y + (int64_t)m * p.n_out;
     const int U = (p.n_in + 63) >> 6;
     const int stride = gridDim.x * W * RW;
@@ -600,21 +620,17 @@ __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
 // weight byte of the matvec is in flight at once, the shape a streaming read needs at this size).
 template <int F, int T, int RW>
 __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
+    args_early(p);
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     // the wave index is uniform across the wave: readfirstlane lets the row addressing run on SALU
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
     const int team = lane / T, lt = lane % T;
     const int m = blockIdx.y;
-    const u8* wbase = p.w;
-    int64_t xrow = 0;
-    if (p.ids) {
-        const int64_t e = gp<int64_t>(p.ids)[m];
-        wbase = p.per_expert >= 0 ? p.w + e * p.per_expert : (const u8*)(gp<int64_t>(p.w)[e]);
-        xrow = m / p.x_group;
-    }
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, m, xrow);
     float* y = p.y + (int64_t)m * p.n_out;
     const int U = (p.n_in + 63) >> 6;
     const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
@@ -905,7 +921,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         if (sc.ok) {
             p.ktp = sc.ktp;
             MvKernel k = pick_mvc<F>(sc.T, sc.rw);
-            hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(64 * sc.W), sc.lds, stream, p);
+            p.nt = 64 * sc.W;
+            hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(p.nt), sc.lds, stream, p);
             return (int)hipGetLastError();
         }
     }
@@ -914,7 +931,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         if (sl.ok) {
             p.ktp = sl.ktp;
             MvKernel k = pick_mvl<F>(sl.nit, sl.pipe);
-            hipLaunchKernelGGL(k, dim3((unsigned)sl.grid_x, (unsigned)n_mats), dim3(64 * sl.W), sl.lds, stream, p);
+            p.nt = 64 * sl.W;
+            hipLaunchKernelGGL(k, dim3((unsigned)sl.grid_x, (unsigned)n_mats), dim3(p.nt), sl.lds, stream, p);
             return (int)hipGetLastError();
         }
     }
@@ -923,7 +941,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         if (s1.ok) {
             p.ktp = s1.ktp;
             MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf);
-            hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(64 * s1.W), s1.lds, stream, p);
+            p.nt = 64 * s1.W;
+            hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(p.nt), s1.lds, stream, p);
             return (int)hipGetLastError();
         }
     }
@@ -933,7 +952,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     p.n_tiles = s.n_tiles;
     p.groups = s.groups;
     MvKernel k = pick_kernel<F>(nc, s.rw, s.T);
-    hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x, (unsigned)n_mats), dim3(64 * s.W), s.lds, stream, p);
+    p.nt = 64 * s.W;
+    hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x, (unsigned)n_mats), dim3(p.nt), s.lds, stream, p);
     return (int)hipGetLastError();
 }
 

@@ -17,6 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.abspath(os.path.join(HERE, "..", "libnmq.so"))
 
 NMQ_OK, NMQ_ERR_FORMAT, NMQ_ERR_SHAPE, NMQ_ERR_ARG, NMQ_ERR_DEVICE = 0, -1, -2, -3, -4
+ABI_VERSION = 2
 MAX_COLS = 8
 
 _lock = threading.Lock()
@@ -40,6 +41,10 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_mv.argtypes, L.nmq_mv.restype = [i, p, p, p, p, p, p, i, i, i, p], i
     L.nmq_mv_experts.argtypes = [i, p, p, i, i64, p, p, p, p, i, p, i, i, p]
     L.nmq_mv_experts.restype = i
+    L.nmq_mv_experts2.argtypes = [i, p, p, p, i, i64, p, p, p, p, i, p, i, i, p]
+    L.nmq_mv_experts2.restype = i
+    L.nmq_silu_mul_quant.argtypes, L.nmq_silu_mul_quant.restype = [p, p, p, p, p, p, i64, p], i
+    L.nmq_moe_combine.argtypes, L.nmq_moe_combine.restype = [p, p, i, i, i, p, p], i
     L.nmq_block_sums.argtypes, L.nmq_block_sums.restype = [i, p, p, p, p, p, i, i, p], i
     L.nmq_dequant_bf16.argtypes, L.nmq_dequant_bf16.restype = [i, p, p, i64, p], i
     L.nmq_encode.argtypes, L.nmq_encode.restype = [i, p, i64, p, i], i64

@@ -17,7 +17,7 @@ import torch
 
 from . import _native
 from .gguf_types import TYPE_ID
-from .mmvq import Eingang, _starten
+from .mmvq import _starten, eingang_bf16
 
 THREADS = 256
 FORMATE = {"Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "IQ2_XXS": (256, 66), "TQ2_0": (256, 66)}
@@ -49,9 +49,8 @@ def mv(fmt: str, raw: torch.Tensor, ids: torch.Tensor, x: torch.Tensor, n_out: i
         raise ValueError(f"cudakern.mv: format {fmt}")
     geraet = x.device
     ids = ids.to(geraet, torch.int64).contiguous()
-    xb = x.to(torch.bfloat16).contiguous()
     k = ids.numel()
-    e = Eingang(xb)
+    e = eingang_bf16(x)
     y = torch.empty(k, n_out, dtype=torch.float32, device=geraet)
     if adressen is None:
         quelle, per = raw, raw.shape[1] if raw.dim() == 2 else raw.numel()
@@ -76,7 +75,7 @@ def mm(fmt: str, raw: torch.Tensor, x: torch.Tensor, n_out: int, n_in: int) -> t
     grenze = mm_bis(geraet)
     if not 2 <= M <= grenze:
         raise ValueError(f"mm: {M} rows (2..{grenze})")
-    e = Eingang(x.to(torch.bfloat16).contiguous())
+    e = eingang_bf16(x)
     y = torch.empty(M, n_out, dtype=torch.float32, device=geraet)
     L = _native.lib()
     _starten("mv", L.nmq_mv, TYPE_ID[fmt], raw.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),

@@ -9,9 +9,10 @@ The reference's expert path around the gathered mat-vec, on this library's kerne
     renormalised to sum 1 (+1e-20), times the weights scale.
   - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  Every
     (token, slot) pair on its own, in (token, slot) order (the reference's one-token and graph paths),
-    the weighted sum per token in that fixed order; gate/up read each token's input, quantised once
-    for both, through its k slots (x_group = k) instead of repeating it; down reads each slot's own
-    activation.
+    the weighted sum per token in slot order.  Five launches: each token's input quantised once (after
+    rounding to bf16, as cudakern.mv does), gate and up in one gathered launch reading that input
+    through the token's k slots (x_group = k), silu(gate) * up rounded to bf16 and quantised in one
+    launch, down on each slot's own activation, the combine.
 
 Every expert product runs on libnmq's HIP kernels; without the library the constructor raises.
 """
@@ -24,7 +25,7 @@ import torch.nn.functional as F
 
 from . import _native, cudakern
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
-from .mmvq import Eingang, _starten
+from .mmvq import Eingang, _starten, eingang_bf16
 
 
 class PackedExperts:
@@ -65,7 +66,7 @@ class PackedExperts:
         (L*k, n_out) float32, rows in (token, slot) order (each token's input quantised once, read by its
         k slots).  A tensor x is rounded to bf16 first, as cudakern.mv does."""
         L_, k = ids.shape
-        e = x if isinstance(x, Eingang) else Eingang(x.reshape(L_, self.n_in).to(torch.bfloat16).contiguous())
+        e = x if isinstance(x, Eingang) else eingang_bf16(x.reshape(L_, self.n_in))
         if e.n != L_ * self.n_in:
             raise ValueError(f"matvec_tokens: input of {e.n} values for {L_} tokens of {self.n_in}")
         flat = ids.reshape(-1).to(e.xq.device, torch.int64).contiguous()
@@ -106,14 +107,49 @@ class Experten:
     def _gu(h_gate: torch.Tensor, h_up: torch.Tensor) -> torch.Tensor:
         return F.silu(h_gate) * h_up
 
+    def _fused(self) -> bool:
+        g, u = self.gate, self.up
+        return (g.ggml_type == u.ggml_type and g.raw.shape == u.raw.shape and (g.adressen is None) == (u.adressen is None))
+
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights."""
+        """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights.
+        Five launches: the tokens' input (rounded to bf16, two-stage int8), gate and up together on every
+        (token, slot), silu(gate) * up made the down input, down on every slot, the weighted combine."""
         L_, E = x.shape
-        # gate and up read the same tokens: their int8 input is made once (x rounded to bf16 first)
-        e = Eingang(x.to(torch.bfloat16).contiguous())
-        g = self.gate.matvec_tokens(idx, e)
-        u = self.up.matvec_tokens(idx, e)
-        y = self.down.matvec_je(idx.reshape(-1), self._gu(g, u))              # (L*k, E)
-        if L_ == 1:
-            return (y * w[0].float().unsqueeze(-1)).sum(0, keepdim=True)
-        return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)
+        k = idx.shape[1]
+        if not self._fused():
+            e = eingang_bf16(x)
+            g = self.gate.matvec_tokens(idx, e)
+            u = self.up.matvec_tokens(idx, e)
+            y = self.down.matvec_je(idx.reshape(-1), self._gu(g, u))
+            return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)
+        L = _native.lib()
+        dev = x.device
+        st = _native.stream_ptr(dev)
+        n = L_ * k
+        FF = self.gate.n_out
+        e = eingang_bf16(x)
+        flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
+        gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
+        if self.gate.adressen is None:
+            wa, wb, per = self.gate.raw, self.up.raw, self.gate.raw.shape[1]
+        else:
+            wa = self.gate.adressen.to(dev, torch.int64).contiguous()
+            wb, per = self.up.adressen.to(dev, torch.int64).contiguous(), -1
+        _starten("mv_experts2", L.nmq_mv_experts2, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
+                 flat.data_ptr(), n, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k,
+                 gu.data_ptr(), FF, E, st)
+        a = Eingang(n=n * FF, device=dev)
+        _starten("silu_mul_quant", L.nmq_silu_mul_quant, gu.data_ptr(), gu[n:].data_ptr(), a.xq.data_ptr(),
+                 a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), n * FF, st)
+        y = torch.empty(n, E, dtype=torch.float32, device=dev)
+        if self.down.adressen is None:
+            wd, perd = self.down.raw, self.down.raw.shape[1]
+        else:
+            wd, perd = self.down.adressen.to(dev, torch.int64).contiguous(), -1
+        _starten("mv_experts", L.nmq_mv_experts, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), n, perd,
+                 a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), 1, y.data_ptr(), E, FF, st)
+        out = torch.empty(L_, E, dtype=torch.float32, device=dev)
+        wf = w.to(dev, torch.float32).contiguous()
+        _starten("moe_combine", L.nmq_moe_combine, y.data_ptr(), wf.data_ptr(), L_, k, E, out.data_ptr(), st)
+        return out

@@ -86,6 +86,19 @@ class Eingang:
         return [_z(self.xq[ab:]), _z(self.xq2[ab:]), _z(self.xd[ab // 32:]), _z(self.xs[ab // 32:])]
 
 
+def eingang_bf16(x: torch.Tensor) -> Eingang:
+    """The Eingang of x rounded to bf16 first (the input convention of the cudakern entry points,
+    reference cudakern.py:764), in one launch: fp32 x is rounded inside the quantisation kernel."""
+    x = x.reshape(-1)
+    if x.dtype == torch.bfloat16:
+        return Eingang(x)
+    xf = x.float().contiguous()
+    e = Eingang(n=xf.numel(), device=xf.device)
+    _starten("quant_q8", _native.lib().nmq_quant_q8, xf.data_ptr(), 2,
+             *[t.data_ptr() for t in (e.xq, e.xq2, e.xd, e.xs)], e.n, _native.stream_ptr(xf.device))
+    return e
+
+
 _TEILEN = threading.local()
 
 

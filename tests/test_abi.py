@@ -37,7 +37,8 @@ def test_format_table(L):
         assert L.nmq_format_info(t, ctypes.byref(bv), ctypes.byref(bb)) == 0, name
         assert (bv.value, bb.value) == (v, b), name
     assert L.nmq_format_info(2, None, None) == -1          # Q4_0: not served
-    assert L.nmq_abi_version() == 1
+    from ggufengine_amd import _native
+    assert L.nmq_abi_version() == _native.ABI_VERSION == 2
 
 
 def test_rejects_bad_arguments_without_launching(L):

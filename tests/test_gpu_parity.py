@@ -121,7 +121,8 @@ def test_mv_one_token(nmq, oracle, fmt, shape):
     e = quant_dev(dev(x))
     y = torch.empty(1, n_out, device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID
-    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+    raw_d = dev(raw)  # kept alive until the launch has run
+    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
                                e.xs.data_ptr(), y.data_ptr(), n_out, n_in, 1, nmq.stream_ptr()))
     torch.cuda.synchronize()
     _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
@@ -144,7 +145,8 @@ def test_mv_one_token_long_rows(nmq, oracle, monkeypatch, fmt, n_in, pipelined):
     e = quant_dev(dev(x))
     y = torch.full((1, n_out), float("nan"), device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID
-    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+    raw_d = dev(raw)  # kept alive until the launch has run
+    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
                                e.xs.data_ptr(), y.data_ptr(), n_out, n_in, 1, nmq.stream_ptr()))
     torch.cuda.synchronize()
     _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
@@ -191,7 +193,8 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
         e = quant_dev(dev(x))
         y = torch.full((nc, n_out), float("nan"), device="cuda")
         say("mv tokens mfma", fmt, split, nc)
-        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+        raw_d = dev(raw)  # kept alive until the launch has run
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
                                    e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
                                    nmq.stream_ptr()))
         torch.cuda.synchronize()
@@ -211,7 +214,8 @@ def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
         e = quant_dev(dev(x))
         y = torch.full((nc, n_out), float("nan"), device="cuda")
         say("mv tokens dot4", fmt, nc)
-        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], dev(raw).data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+        raw_d = dev(raw)  # kept alive until the launch has run
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
                                    e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
                                    nmq.stream_ptr()))
         torch.cuda.synchronize()
@@ -276,7 +280,8 @@ def test_dequant_bf16_exact(nmq, oracle, fmt):
     out = torch.empty(n_blocks * BV[fmt], dtype=torch.bfloat16, device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID
     say("dequant", fmt, n_blocks)
-    nmq.check(nmq.lib().nmq_dequant_bf16(TYPE_ID[fmt], dev(raw).data_ptr(), out.data_ptr(), n_blocks,
+    raw_d = dev(raw)  # kept alive until the launch has run
+    nmq.check(nmq.lib().nmq_dequant_bf16(TYPE_ID[fmt], raw_d.data_ptr(), out.data_ptr(), n_blocks,
                                          nmq.stream_ptr()))
     torch.cuda.synchronize()
     ref = oracle.round_bf16(oracle.dequant(fmt, raw))

@@ -32,7 +32,8 @@ extern "C" {
 #define NMQ_ERR_ARG (-3)    /* NULL pointer where one is required, bad count                       */
 #define NMQ_ERR_DEVICE (-4) /* no usable device / not a gfx950 device                             */
 
-/* Tokens handled by one launch of the mat-vec kernels; nmq_mv loops over larger counts. */
+/* Tokens handled by one launch of the dot4 mat-vec kernels (the matrix-core kernel takes up to twice
+ * as many); nmq_mv loops over larger counts. */
 #define NMQ_MAX_COLS 8
 
 /* ABI version of this header, bumped on incompatible changes (2: nmq_quant_q8 mode 2, the fused
@@ -75,7 +76,8 @@ int nmq_silu_mul_quant(const float* g, const float* u, int8_t* xq, int8_t* xq2, 
                        void* stream);
 
 /*
- * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of NMQ_MAX_COLS tokens).
+ * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of up to 2 * NMQ_MAX_COLS
+ * tokens on the matrix cores, NMQ_MAX_COLS on the dot4 kernels).
  * w: n_out rows of n_in values in GGUF block format, rows back to back.  Token c's two-stage input
  * lies at xq + c*n_in, xq2 + c*n_in, xd + c*n_in/32, xs + c*n_in/32 (the layout of an Eingang of
  * ncols rows).  y: fp32, token-major (ncols x n_out).

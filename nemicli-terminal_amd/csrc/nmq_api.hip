@@ -345,8 +345,9 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
     int e = check_mv(fmt, w, xq, xq2, xd, xs, y, n_out, n_in);
     if (e) return e;
     if (ncols < 1) return NMQ_ERR_ARG;
-    for (int c0 = 0; c0 < ncols; c0 += NMQ_MAX_COLS) {
-        const int nc = ncols - c0 < NMQ_MAX_COLS ? ncols - c0 : NMQ_MAX_COLS;
+    for (int c0 = 0; c0 < ncols; c0 += 2 * NMQ_MAX_COLS) {
+        // up to 16 tokens per call of the launcher (one launch on the matrix cores, else two of 8)
+        const int nc = ncols - c0 < 2 * NMQ_MAX_COLS ? ncols - c0 : 2 * NMQ_MAX_COLS;
         MvParams p{};
         p.w = (const u8*)w;
         p.ids = nullptr;

@@ -18,7 +18,8 @@
 // Work split: a wave owns one 16-row tile and one of KS slices of the row's blocks; a workgroup holds
 // TPW tiles x KS slices (W = TPW*KS waves) and stages the input of all tokens once, as ready-made A
 // fragments ([step][k-block][input row], 512 bytes per 32 values, conflict-free 64-bit reads).  The
-// KS partial sums of a tile are added through LDS.
+// KS partial sums of a tile are added through LDS.  Up to 16 tokens per launch: G = 2 groups of 8
+// share every decoded weight fragment (two MFMAs per fragment).
 #pragma once
 
 #include <algorithm>
@@ -179,96 +180,115 @@ struct Mfma<NMQ_IQ2_XXS> {
     }
 };
 
-// LDS layout of the input: A fragments then (xd, xs) pairs.
-//   frag[s][kb][n] (u64): s = 32-value step of the row; input row n = xq (n even) or xq2 (n odd) of
-//   token n / 2, values 32s + 8kb .. + 8
-//   xsc[s][t] (float2): (xd / 254, xs) of token t, step s
-// Staged in rounds: per round each thread reads 4 16-byte chunks (16 input rows x n_in / 16 chunks in
-// all, 16 rows x 4 chunks per wave access) and one (xd, xs) pair.  Every read is issued (threads with
-// nothing to read re-read the start of xq), so a round's reads can be issued before the weight reads
-// and waited for alone.  Rows of absent tokens (t >= nc) are left unwritten.
+// LDS layout of the input, G groups of 8 tokens (group g = tokens 8g .. 8g + 7): A fragments of every
+// group, then (xd / 254, xs) pairs of every group.
+//   frag_g[s][kb][n] (u64) at g * S * 512 bytes: s = 32-value step of the row; input row n = xq (n even)
+//   or xq2 (n odd) of token 8g + n / 2, values 32s + 8kb .. + 8
+//   xsc_g[s][t] (float2) at G * S * 512 + g * S * 64 bytes: token 8g + t, step s
+// Staged in rounds: per round each thread reads 4 16-byte chunks (16 G input rows x n_in / 16 chunks
+// in all, 16 G rows x 4 / G chunks per wave access) and one (xd, xs) pair.  Every read is issued
+// (threads with nothing to read re-read the start of xq), so a round's reads can be issued before the
+// weight reads and waited for alone.  Rows of absent tokens (t >= nc) are left unwritten.
 struct XStage {
     u32x4 v[4];
     float2 f;
 };
 
+template <int G>
 __device__ __forceinline__ void stage_load(XStage& st, int r, const MvmParams& p) {
     const int T = 64 * p.ks * p.tpw, S = p.n_in / 32;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = (4 * r + j) * T + (int)threadIdx.x;
-        const int n = i & 15, c = i >> 4, t = n >> 1;
-        const bool ok = i < p.n_in && t < p.nc;
-        const int8_t* src = ok ? ((n & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in + 16 * c : p.xq;
+        const int na = i & (16 * G - 1), c = i / (16 * G), t = 8 * (na >> 4) + ((na & 15) >> 1);
+        const bool ok = i < G * p.n_in && t < p.nc;
+        const int8_t* src = ok ? ((na & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in + 16 * c : p.xq;
         st.v[j] = *gp<u32x4>(src);
     }
     const int i = r * T + (int)threadIdx.x;
-    const int t = i & 7, s = i >> 3;
-    const int64_t o = (i < 8 * S && t < p.nc) ? (int64_t)t * S + s : 0;
+    const int t = i & (8 * G - 1), s = i / (8 * G);
+    const int64_t o = (i < 8 * G * S && t < p.nc) ? (int64_t)t * S + s : 0;
     st.f = make_float2(gp<float>(p.xd)[o], gp<float>(p.xs)[o]);
 }
 
+template <int G>
 __device__ __forceinline__ void stage_store(const XStage& st, int r, u8* lds, const MvmParams& p) {
     const int T = 64 * p.ks * p.tpw, S = p.n_in / 32;
-    u64* frag = (u64*)lds;
-    float2* xsc = (float2*)(lds + (size_t)S * 512);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int i = (4 * r + j) * T + (int)threadIdx.x;
-        const int n = i & 15, c = i >> 4, t = n >> 1;
-        if (i < p.n_in && t < p.nc) {
+        const int na = i & (16 * G - 1), c = i / (16 * G), g = na >> 4, n = na & 15, t = 8 * g + (n >> 1);
+        if (i < G * p.n_in && t < p.nc) {
             // values 16c .. 16c + 15: step c / 2, k-blocks 2 (c & 1) and 2 (c & 1) + 1
-            u64* d = frag + ((c >> 1) * 4 + 2 * (c & 1)) * 16 + n;
+            u64* d = (u64*)(lds + (size_t)g * S * 512) + ((c >> 1) * 4 + 2 * (c & 1)) * 16 + n;
             d[0] = (u64)st.v[j].x | ((u64)st.v[j].y << 32);
             d[16] = (u64)st.v[j].z | ((u64)st.v[j].w << 32);
         }
     }
     const int i = r * T + (int)threadIdx.x;
-    if (i < 8 * S && (i & 7) < p.nc) xsc[i] = make_float2(st.f.x * FEIN, st.f.y);
+    const int t = i & (8 * G - 1), s = i / (8 * G);
+    if (i < 8 * G * S && t < p.nc) {
+        float2* xsc = (float2*)(lds + (size_t)G * S * 512 + (size_t)(t >> 3) * S * 64);
+        xsc[s * 8 + (t & 7)] = make_float2(st.f.x * FEIN, st.f.y);
+    }
 }
 
-// One 256-value block of the lane's weight row into its sums of tokens 2kb and 2kb + 1:
+// One 256-value block of the lane's weight row into its sums of tokens 8g + 2kb and 8g + 2kb + 1 of
+// every group g (the weight fragment of a step is decoded once and meets G input fragments):
 //   y += w_g * (xd_g / 254) * (254 S1 + S2) - m_g * xs_g   per 32-value group g (Q6_K: per 16, no m term)
 // (254 S1 + S2 is exact in int32: |S1|, |S2| <= 32 * 127 * 63.)
 // The LDS operands of each step are read one step ahead.
-template <int F>
-__device__ __forceinline__ void mvm_block(const typename Mfma<F>::Raw& cur, int b, const u64* tab, const u64* frag,
-                                          const float2* xsc, int lane, float& acc0, float& acc1) {
+template <int F, int G>
+__device__ __forceinline__ void mvm_block(const typename Mfma<F>::Raw& cur, int b, const u64* tab, const u8* lds, int S,
+                                          int lane, float (&acc)[G][2]) {
     using M = Mfma<F>;
     const int kb = lane >> 4, n = lane & 15;
-    u64 xv[2];
-    float4 xf[2];
-    xv[0] = frag[(b * M::STEPS * 4 + kb) * 16 + n];
-    xf[0] = *(const float4*)(xsc + b * M::STEPS * 8 + 2 * kb);
+    u64 xv[2][G];
+    float4 xf[2][G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const u64* frag = (const u64*)(lds + (size_t)g * S * 512);
+        const float2* xsc = (const float2*)(lds + (size_t)G * S * 512 + (size_t)g * S * 64);
+        xv[0][g] = frag[(b * M::STEPS * 4 + kb) * 16 + n];
+        xf[0][g] = *(const float4*)(xsc + b * M::STEPS * 8 + 2 * kb);
+    }
 #pragma unroll
     for (int s = 0; s < M::STEPS; ++s) {
         if (s + 1 < M::STEPS) {
             const int gn = b * M::STEPS + s + 1;
-            xv[(s + 1) & 1] = frag[(gn * 4 + kb) * 16 + n];
-            xf[(s + 1) & 1] = *(const float4*)(xsc + gn * 8 + 2 * kb);  // (xd, xs) of tokens 2kb, 2kb+1
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                const u64* frag = (const u64*)(lds + (size_t)g * S * 512);
+                const float2* xsc = (const float2*)(lds + (size_t)G * S * 512 + (size_t)g * S * 64);
+                xv[(s + 1) & 1][g] = frag[(gn * 4 + kb) * 16 + n];
+                xf[(s + 1) & 1][g] = *(const float4*)(xsc + gn * 8 + 2 * kb);  // tokens 2kb, 2kb + 1
+            }
         }
         __builtin_amdgcn_sched_barrier(0);  // the next step's reads stay ahead of this step's work
         u64 wv;
         if constexpr (F == NMQ_IQ2_XXS) wv = M::frag_iq(cur, s, kb, tab);
         else wv = M::frag(cur, s);
-        const u64 x = xv[s & 1];
-        const float4 f = xf[s & 1];
-        if constexpr (M::GS == 16) {
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const u64 xm = (kb >> 1) == half ? x : 0ull;
+        for (int g = 0; g < G; ++g) {
+            const u64 x = xv[s & 1][g];
+            const float4 f = xf[s & 1][g];
+            if constexpr (M::GS == 16) {
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const u64 xm = (kb >> 1) == half ? x : 0ull;
+                    i32x4 c = {0, 0, 0, 0};
+                    c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xm, (long)wv, c, 0, 0, 0);
+                    const float w = M::fac(cur, 2 * s + half).x;
+                    acc[g][0] = fmaf(w * f.x, (float)__mul24(c[0], 254) + (float)c[1], acc[g][0]);
+                    acc[g][1] = fmaf(w * f.z, (float)__mul24(c[2], 254) + (float)c[3], acc[g][1]);
+                }
+            } else {
                 i32x4 c = {0, 0, 0, 0};
-                c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xm, (long)wv, c, 0, 0, 0);
-                const float w = M::fac(cur, 2 * s + half).x;
-                acc0 = fmaf(w * f.x, (float)__mul24(c[0], 254) + (float)c[1], acc0);
-                acc1 = fmaf(w * f.z, (float)__mul24(c[2], 254) + (float)c[3], acc1);
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+                const float2 w = M::fac(cur, s);
+                acc[g][0] = fmaf(w.x * f.x, (float)(__mul24(c[0], 254) + c[1]), fmaf(-w.y, f.y, acc[g][0]));
+                acc[g][1] = fmaf(w.x * f.z, (float)(__mul24(c[2], 254) + c[3]), fmaf(-w.y, f.w, acc[g][1]));
             }
-        } else {
-            i32x4 c = {0, 0, 0, 0};
-            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
-            const float2 w = M::fac(cur, s);
-            acc0 = fmaf(w.x * f.x, (float)(__mul24(c[0], 254) + c[1]), fmaf(-w.y, f.y, acc0));
-            acc1 = fmaf(w.x * f.z, (float)(__mul24(c[2], 254) + c[3]), fmaf(-w.y, f.w, acc1));
         }
     }
 }
@@ -276,8 +296,8 @@ __device__ __forceinline__ void mvm_block(const typename Mfma<F>::Raw& cur, int 
 // NB blocks of the wave's slice are held in registers.  RING = false: the slice has exactly NB blocks,
 // all requested before the input is staged.  RING = true: any number of blocks, each buffer refilled
 // NB blocks ahead once used (requests past the slice re-read its last block, so every wave issues the
-// same loads and the waits count exactly).
-template <int F, int NB, bool RING>
+// same loads and the waits count exactly).  G: groups of 8 tokens per launch (1 or 2).
+template <int F, int NB, bool RING, int G>
 __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     using M = Mfma<F>;
     // every argument into the first batch of scalar loads (see args_early)
@@ -287,9 +307,7 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int S = p.n_in / 32;
-    const u64* frag = (const u64*)lds;
-    const float2* xsc = (const float2*)(lds + (size_t)S * 512);
-    float* red = (float*)lds;  // W x 64 x 2 sums, after the blocks
+    float* red = (float*)lds;  // W x 64 x 2G sums, after the blocks
 
     const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
     const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
@@ -305,11 +323,11 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     // order, so input requested after another wave's weights would wait for them; the barrier between
     // input and weight reads waits for issue only.
     const int nt = 64 * p.ks * p.tpw;  // threads of the workgroup, from the arguments (see args_early)
-    const int rounds = (p.n_in + 4 * nt - 1) / (4 * nt);
+    const int rounds = (G * p.n_in + 4 * nt - 1) / (4 * nt);
     typename M::Raw buf[NB];
     if (rounds == 1) {
         XStage st;
-        stage_load(st, 0, p);
+        stage_load<G>(st, 0, p);
         const u64 gv = tab_load<F>();
         lds_barrier();
         __builtin_amdgcn_sched_barrier(0);
@@ -317,12 +335,12 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
         for (int u = 0; u < NB; ++u) M::load(rowp + (int64_t)min(b0 + u, last) * M::BB, kb, buf[u]);
         __builtin_amdgcn_sched_barrier(0);
         tab_store<F>(tab, gv, nt);
-        stage_store(st, 0, lds, p);
+        stage_store<G>(st, 0, lds, p);
     } else {
         for (int r = 0; r < rounds; ++r) {
             XStage st;
-            stage_load(st, r, p);
-            stage_store(st, r, lds, p);
+            stage_load<G>(st, r, p);
+            stage_store<G>(st, r, lds, p);
         }
         tab_store<F>(tab, tab_load<F>(), nt);
         __builtin_amdgcn_sched_barrier(0);
@@ -331,37 +349,46 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     }
     lds_barrier();
 
-    float acc0 = 0.f, acc1 = 0.f;
+    float acc[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g) acc[g][0] = acc[g][1] = 0.f;
     if constexpr (RING) {
         for (int j0 = 0; j0 < bpr; j0 += NB) {
 #pragma unroll
             for (int u = 0; u < NB; ++u) {
-                if (j0 + u < bpr) mvm_block<F>(buf[u], b0 + j0 + u, tab, frag, xsc, lane, acc0, acc1);
+                if (j0 + u < bpr) mvm_block<F, G>(buf[u], b0 + j0 + u, tab, lds, S, lane, acc);
                 M::load(rowp + (int64_t)min(b0 + j0 + u + NB, last) * M::BB, kb, buf[u]);
             }
         }
     } else {
 #pragma unroll
-        for (int u = 0; u < NB; ++u) mvm_block<F>(buf[u], b0 + u, tab, frag, xsc, lane, acc0, acc1);
+        for (int u = 0; u < NB; ++u) mvm_block<F, G>(buf[u], b0 + u, tab, lds, S, lane, acc);
     }
 
-    // add the KS slices of each tile; lane (n, kb) holds weight row row0 + n, tokens 2kb and 2kb + 1
+    // add the KS slices of each tile; lane (n, kb) holds weight row row0 + n, tokens 8g + 2kb, 8g + 2kb + 1
     // (the sums take the place of the staged input, once every wave is done with it)
     lds_barrier();
-    red[(wave * 64 + lane) * 2] = acc0;
-    red[(wave * 64 + lane) * 2 + 1] = acc1;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        red[((wave * 64 + lane) * G + g) * 2] = acc[g][0];
+        red[((wave * 64 + lane) * G + g) * 2 + 1] = acc[g][1];
+    }
     lds_barrier();
     if (slice == 0) {
-        float s0 = 0.f, s1 = 0.f;
-        for (int q = 0; q < p.ks; ++q) {
-            const int ri = ((tile_in_wg * p.ks + q) * 64 + lane) * 2;
-            s0 += red[ri];
-            s1 += red[ri + 1];
-        }
-        const int r = row0 + n, t = 2 * kb;
-        if (r < p.n_out) {
-            if (t < p.nc) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = s0;
-            if (t + 1 < p.nc) gpw<float>(p.y)[(int64_t)(t + 1) * p.n_out + r] = s1;
+        const int r = row0 + n;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            float s0 = 0.f, s1 = 0.f;
+            for (int q = 0; q < p.ks; ++q) {
+                const int ri = (((tile_in_wg * p.ks + q) * 64 + lane) * G + g) * 2;
+                s0 += red[ri];
+                s1 += red[ri + 1];
+            }
+            const int t = 8 * g + 2 * kb;
+            if (r < p.n_out) {
+                if (t < p.nc) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = s0;
+                if (t + 1 < p.nc) gpw<float>(p.y)[(int64_t)(t + 1) * p.n_out + r] = s1;
+            }
         }
     }
 }
@@ -370,19 +397,21 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
 
 struct MvmShape {
     bool ok;
-    int ks, tpw, grid_x, nb;
+    int ks, tpw, grid_x, nb, g;
     bool ring;
     size_t lds;
 };
 
 // Tiles of 16 rows; K slices per tile and tiles per workgroup chosen for about one workgroup of up
 // to 16 waves per CU (the staged input takes most of the LDS).  A slice of up to NBMAX blocks is held
-// in registers whole; longer slices cycle through NBRING buffers.
+// in registers whole; longer slices cycle through NBRING buffers.  9..16 tokens: two groups of 8 in
+// one launch when their input fits the LDS.
 template <int F>
 inline MvmShape plan_mvm(int n_out, int n_in, int nc, int cus, int lds_max) {
     MvmShape s{};
     const int mode = env_int("NMQ_MVM", 1);  // 0: never, 1: from MIN_NC tokens, 2: from 2 tokens
-    if (mode == 0 || nc < (mode == 2 ? 2 : Mfma<F>::MIN_NC) || nc > 8 || n_in % 256) return s;
+    if (mode == 0 || nc < (mode == 2 ? 2 : Mfma<F>::MIN_NC) || nc > 16 || n_in % 256) return s;
+    s.g = nc > 8 ? 2 : 1;
     const int nblk = n_in / 256;
     const int tiles = (n_out + 15) / 16;
     int tpw = env_int("NMQ_MVM_TPW", 0);
@@ -401,22 +430,26 @@ inline MvmShape plan_mvm(int n_out, int n_in, int nc, int cus, int lds_max) {
     s.grid_x = (tiles + tpw - 1) / tpw;
     s.ring = !(bpr <= Mfma<F>::NBMAX && (bpr & (bpr - 1)) == 0);
     s.nb = s.ring ? Mfma<F>::NBRING : bpr;
-    s.lds = std::max((size_t)(n_in / 32) * 576, (size_t)W * 512);
+    s.lds = std::max((size_t)s.g * (n_in / 32) * 576, (size_t)W * 512 * s.g);
     s.ok = s.lds + 4096 <= (size_t)lds_max;
     return s;
+}
+
+template <int F, int G>
+inline void (*pick_mvm(const MvmShape& s))(MvmParams) {
+    constexpr int NBM = Mfma<F>::NBMAX;
+    if (s.ring) return mvm_kernel<F, Mfma<F>::NBRING, true, G>;
+    if (s.nb == 1) return mvm_kernel<F, 1, false, G>;
+    if (s.nb == 2) return mvm_kernel<F, (NBM >= 2 ? 2 : 1), false, G>;
+    if (s.nb == 4) return mvm_kernel<F, (NBM >= 4 ? 4 : 1), false, G>;
+    return mvm_kernel<F, NBM, false, G>;
 }
 
 template <int F>
 int launch_mvm(const MvmShape& s, MvmParams p, hipStream_t stream) {
     p.ks = s.ks;
     p.tpw = s.tpw;
-    constexpr int NBM = Mfma<F>::NBMAX;
-    void (*k)(MvmParams);
-    if (s.ring) k = mvm_kernel<F, Mfma<F>::NBRING, true>;
-    else if (s.nb == 1) k = mvm_kernel<F, 1, false>;
-    else if (s.nb == 2) k = mvm_kernel<F, (NBM >= 2 ? 2 : 1), false>;
-    else if (s.nb == 4) k = mvm_kernel<F, (NBM >= 4 ? 4 : 1), false>;
-    else k = mvm_kernel<F, NBM, false>;
+    void (*k)(MvmParams) = s.g == 2 ? pick_mvm<F, 2>(s) : pick_mvm<F, 1>(s);
     hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
     return (int)hipGetLastError();
 }

@@ -899,7 +899,22 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     const DeviceInfo di = device_info();
     p.nblk = p.n_in / FM::BV;
     p.row_bytes = (int64_t)p.nblk * FM::BB;
-    // 2..8 tokens of one matrix: the matrix cores (see nmq_mfma.hpp)
+    // 2..16 tokens of one matrix: the matrix cores (see nmq_mfma.hpp); more than 8 tokens that cannot
+    // go there in one launch run as two launches of at most 8
+    if (nc > 8) {
+        const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
+        if (!(sm.ok && p.ids == nullptr)) {
+            int e = launch_mv<F>(p, 8, n_mats, stream);
+            if (e) return e;
+            MvParams q = p;
+            q.xq += (int64_t)8 * p.n_in;
+            q.xq2 += (int64_t)8 * p.n_in;
+            q.xd += (int64_t)8 * (p.n_in / 32);
+            q.xs += (int64_t)8 * (p.n_in / 32);
+            q.y += (int64_t)8 * p.n_out;
+            return launch_mv<F>(q, nc - 8, n_mats, stream);
+        }
+    }
     if (nc >= 2 && p.ids == nullptr) {
         const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
         if (sm.ok) {

@@ -177,9 +177,9 @@ def test_mv_tokens(nmq, oracle, fmt, nc):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("split", [(1, 16), (1, 8), (1, 4), (1, 2), (1, 1), (2, 4), (4, 4), (3, 2)])
 def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
-    """2..8 tokens on the matrix cores with every (tiles per workgroup, K slices) split: slices of
-    16, 8, 4, 2 and 1 blocks (held whole or cycled through buffers), a partial last tile, and
-    workgroups whose last tiles lie past the matrix."""
+    """2..16 tokens on the matrix cores (one or two groups of 8 per launch) with every (tiles per
+    workgroup, K slices) split: slices of 16, 8, 4, 2 and 1 blocks (held whole or cycled through
+    buffers), a partial last tile, and workgroups whose last tiles lie past the matrix."""
     tpw, ks = split
     n_out, n_in = 200, 4096
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=61 + ks)
@@ -187,7 +187,7 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
     monkeypatch.setenv("NMQ_MVM", "2")   # the matrix-core path from 2 tokens on, whatever the format
     monkeypatch.setenv("NMQ_MVM_TPW", str(tpw))
     monkeypatch.setenv("NMQ_MVM_KS", str(ks))
-    for nc in (2, 7, 8):
+    for nc in (2, 7, 8, 12, 16):
         x = np.random.default_rng(62 + nc).standard_normal((nc, n_in)).astype(np.float32)
         x[:, 7] = 30.0
         e = quant_dev(dev(x))
@@ -209,7 +209,7 @@ def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=71)
     from ggufengine_amd.gguf_types import TYPE_ID
     monkeypatch.setenv("NMQ_MVM", "0")
-    for nc in (2, 5, 8):
+    for nc in (2, 5, 8, 13):                   # 13: launches of 8 and 5
         x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
         e = quant_dev(dev(x))
         y = torch.full((nc, n_out), float("nan"), device="cuda")

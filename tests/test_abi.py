@@ -59,6 +59,22 @@ def test_rejects_bad_arguments_without_launching(L):
     assert L.nmq_dequant_bf16(12, a16, a16, 0, None) == _native.NMQ_ERR_SHAPE
     assert L.nmq_encode(12, None, 256, a16, 1) == _native.NMQ_ERR_ARG
     assert b"block format" in L.nmq_strerror(-1)
+    # quantisation modes: 0 bf16, 1 fp32, 2 fp32 rounded to bf16; anything else is refused
+    assert L.nmq_quant_q8(a16, 3, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_quant_q8(a16, -1, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    # fused expert entry points
+    assert L.nmq_silu_mul_quant(None, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_silu_mul_quant(a16, a16 + 2, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_silu_mul_quant(a16, a16, a16, a16, a16, a16, 48, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mv_experts2(12, a16, None, a16, 2, 0, a16, a16, a16, a16, 1, a16, 4, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_experts2(12, a16, a16, None, 2, 0, a16, a16, a16, a16, 1, a16, 4, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_experts2(12, a16, a16, a16, 40000, 4 * 144, a16, a16, a16, a16, 1, a16, 4, 256,
+                             None) == _native.NMQ_ERR_ARG      # 2 x 40000 instances exceed the grid
+    assert L.nmq_mv_experts2(12, a16, a16, a16, 2, 144, a16, a16, a16, a16, 1, a16, 4, 256,
+                             None) == _native.NMQ_ERR_SHAPE    # stride smaller than one matrix
+    assert L.nmq_moe_combine(None, a16, 1, 8, 64, a16, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_moe_combine(a16, a16, 0, 8, 64, a16, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_moe_combine(a16, a16, 1, 8, 64, a16 + 1, None) == _native.NMQ_ERR_ARG
 
 
 def test_python_api_without_gpu():

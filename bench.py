@@ -417,6 +417,51 @@ def main():
         cfg["us_per_layer"] = round(us_layer, 3)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
+
+        # The same layer with its inputs formed as the reference's one-token step forms them
+        # (models/baukasten.py:217-241 without rope and attention): RMS norm fused with the q/k/v input,
+        # the attention output quantised, residual add + RMS norm fused with the gate/up input,
+        # silu(gate) * up fused with the down input.  Same launch count, more work per launch.
+        E, FF = 4096, 14336
+        rng_s = np.random.Generator(np.random.PCG64(34))
+        h_s = torch.from_numpy(rng_s.standard_normal(E, dtype=np.float32)).to(dev)
+        nw_s = torch.from_numpy((1 + 0.1 * rng_s.standard_normal(E)).astype(np.float32)).to(dev)
+        xn_s = torch.empty(E, dtype=torch.float32, device=dev)
+        hn_s = torch.empty(E, dtype=torch.float32, device=dev)
+        a_s = torch.empty(FF, dtype=torch.float32, device=dev)
+
+        def ptrs(e):
+            return e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr()
+
+        def mv_named(lw, name, ei):
+            _, f, r, k, _, _ = next(t for t in LAYER if t[0] == name)
+            _native.check(L.nmq_mv(TYPE[f], lw[name].data_ptr(), *ptrs(ei), ys[name].data_ptr(), r, k, 1, stream))
+
+        def step_layer(li):
+            lw = layers[li % nl]
+            _native.check(L.nmq_norm_q8(h_s.data_ptr(), None, 1.0, None, nw_s.data_ptr(), 1e-5, xn_s.data_ptr(),
+                                        *ptrs(eg["x_attn"]), E, stream))
+            for name in ("q", "k", "v"):
+                mv_named(lw, name, eg["x_attn"])
+            _native.check(L.nmq_quant_q8(xin["attn_out"].data_ptr(), 1, *ptrs(eg["attn_out"]), E, stream))
+            mv_named(lw, "o", eg["attn_out"])
+            _native.check(L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(), nw_s.data_ptr(),
+                                        1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E, stream))
+            mv_named(lw, "gate", eg["x_ffn"])
+            mv_named(lw, "up", eg["x_ffn"])
+            _native.check(L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
+                                       *ptrs(eg["act"]), FF, stream))
+            mv_named(lw, "down", eg["act"])
+
+        for i in range(max(5, args.warmup // 10)):
+            step_layer(i)
+        torch.cuda.synchronize()
+        t0.record()
+        for i in range(reps):
+            step_layer(i)
+        t1.record()
+        torch.cuda.synchronize()
+        cfg["us_per_layer_fused_inputs"] = round(t0.elapsed_time(t1) / reps * 1e3, 3)
         del layers
         # per-matrix breakdown: each mat-vec timed alone, rotating over its own copies (> 2x the LLC)
         parts = {}
@@ -454,6 +499,22 @@ def main():
         t1.record()
         torch.cuda.synchronize()
         parts["quant_q8_4096"] = {"us": round(t0.elapsed_time(t1) / reps * 1e3, 3)}
+        small = {
+            "norm_q8_4096": lambda: L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(),
+                                                  nw_s.data_ptr(), 1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E,
+                                                  stream),
+            "akt_q8_14336": lambda: L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
+                                                 *ptrs(eg["act"]), FF, stream)}
+        for pname, fn in small.items():
+            for i in range(20):
+                _native.check(fn())
+            torch.cuda.synchronize()
+            t0.record()
+            for i in range(reps):
+                fn()
+            t1.record()
+            torch.cuda.synchronize()
+            parts[pname] = {"us": round(t0.elapsed_time(t1) / reps * 1e3, 3)}
         cfg["layer_parts"] = parts
         del mats
 

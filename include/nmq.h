@@ -75,6 +75,30 @@ int nmq_quant_q8(const void* x, int x_is_f32, int8_t* xq, int8_t* xq2, float* xd
 int nmq_silu_mul_quant(const float* g, const float* u, int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n,
                        void* stream);
 
+/* Largest row nmq_norm_q8 takes (one workgroup per row). */
+#define NMQ_NORM_MAX 65536
+
+/*
+ * RMS norm of one row fused with its two-stage input.  With r: v = h + rs*r, written to hout
+ * (hout must not overlap h or r); without r (NULL): v = h and hout is not used.  Then
+ *   inv = 1 / sqrt(sum(v^2) / n + eps),  xn = (v * inv) * w,
+ * and (xq, xq2, xd, xs) = the two-stage input of xn, as nmq_quant_q8 forms it from fp32.  Every fp32
+ * operation is rounded on its own (no fused multiply-add) except the sum of squares.  h, r, w, hout,
+ * xn: fp32[n]; n % 32 == 0, n <= NMQ_NORM_MAX.  One workgroup.
+ * Replaces the norm_q8 kernel and wrapper of mmvq (mmvq.py:102-120, 951-961).
+ */
+int nmq_norm_q8(const float* h, const float* r, float rs, float* hout, const float* w, float eps, float* xn,
+                int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n, void* stream);
+
+/*
+ * a = act(g) * u (u NULL: a = act(g)), act(x) = x / (1 + exp(-x)) (gelu == 0) or
+ * 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3))) (gelu == 1), fp32, written to a, and the
+ * two-stage input of a.  g, u, a: fp32[n], n % 32 == 0.
+ * Replaces the akt_q8 kernel and wrapper of mmvq (mmvq.py:122-133, 964-971).
+ */
+int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, int8_t* xq2, float* xd, float* xs,
+               int64_t n, void* stream);
+
 /*
  * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of up to 2 * NMQ_MAX_COLS
  * tokens on the matrix cores, NMQ_MAX_COLS on the dot4 kernels).

@@ -46,6 +46,28 @@ __device__ __forceinline__ float round_bf16(float f) {
     return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
 }
 
+// Two-stage input of the value v held by this lane; value index i (i % 32 == lane % 32).  All 32
+// lanes of the lane's half-wave take part.
+__device__ __forceinline__ void quant32_store(float v, int64_t i, int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
+                                              float* __restrict__ xd, float* __restrict__ xs) {
+    const float a = half_max(fabsf(v));
+    const float d = a / 127.0f;
+    int q = 0, q2 = 0;
+    if (d > 0.0f) {
+        q = (int)rintf(v / d);
+        const float r = fmaf(-(float)q, d, v);
+        q2 = (int)rintf(r / (d * FEIN));
+        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+    }
+    const float s = half_sum_xor(v);
+    xq[i] = (int8_t)q;
+    xq2[i] = (int8_t)q2;
+    if ((threadIdx.x & 31) == 0) {
+        xd[i >> 5] = d;
+        xs[i >> 5] = s;
+    }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ x, const float* __restrict__ u2,
                                                         int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
@@ -65,22 +87,105 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ 
         v = ((const float*)x)[i];
         if constexpr (MODE == 2) v = round_bf16(v);
     }
-    const float a = half_max(fabsf(v));
-    const float d = a / 127.0f;
-    int q = 0, q2 = 0;
-    if (d > 0.0f) {
-        q = (int)rintf(v / d);
-        const float r = fmaf(-(float)q, d, v);
-        q2 = (int)rintf(r / (d * FEIN));
-        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+    quant32_store(v, i, xq, xq2, xd, xs);
+}
+
+// ---- fused producers of the two-stage input (one token) ----------------------------------------
+// RMS norm of one row (reference mmvq.py:102-120, norm_q8): v = h + rs * r (r given: also written to
+// hout), inv = 1 / sqrt(sum(v^2) / n + eps), xn = v * inv * w, and the two-stage input of xn.  One
+// workgroup of 1024 threads; value i belongs to thread i % 1024 in both passes, so the second pass
+// quantises one value per lane.  NV > 0 (rows of at most 1024 NV values): h, r and w are requested
+// together in one round of loads and held in registers across the reduction; NV = 0 (longer rows):
+// the second pass reads them again.  v and xn are rounded after every operation (no contraction),
+// so they are reproducible from h, r, rs, w and inv; only the sum of squares depends on the order.
+template <int NV>
+__global__ __launch_bounds__(1024) void norm_q8_kernel(const float* __restrict__ h, const float* __restrict__ r,
+                                                       float rs, float* __restrict__ hout, const float* __restrict__ w,
+                                                       float eps, float* __restrict__ xn, int8_t* __restrict__ xq,
+                                                       int8_t* __restrict__ xq2, float* __restrict__ xd,
+                                                       float* __restrict__ xs, int n) {
+    asm volatile("" ::"s"(h), "s"(r), "s"(rs), "s"(hout), "s"(w), "s"(eps), "s"(xn), "s"(xq), "s"(xq2), "s"(xd),
+                 "s"(xs), "s"(n));
+    __shared__ float red[16];
+    const int t = threadIdx.x;
+    float ss = 0.f;
+    constexpr int NR = NV > 0 ? NV : 1;
+    float v[NR], wv[NR];
+    if constexpr (NV > 0) {
+        float rv[NR];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {  // clamped indexes: every load is issued unconditionally
+            const int ic = min(t + 1024 * k, n - 1);
+            v[k] = h[ic];
+            wv[k] = w[ic];
+        }
+        if (r) {
+#pragma unroll
+            for (int k = 0; k < NV; ++k) rv[k] = r[min(t + 1024 * k, n - 1)];
+#pragma unroll
+            for (int k = 0; k < NV; ++k) {
+                v[k] = __fadd_rn(v[k], __fmul_rn(rs, rv[k]));
+                if (t + 1024 * k < n) hout[t + 1024 * k] = v[k];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+            if (t + 1024 * k < n) ss = fmaf(v[k], v[k], ss);
+    } else {
+        for (int i = t; i < n; i += 1024) {
+            float x = h[i];
+            if (r) {
+                x = __fadd_rn(x, __fmul_rn(rs, r[i]));
+                hout[i] = x;
+            }
+            ss = fmaf(x, x, ss);
+        }
     }
-    const float s = half_sum_xor(v);
-    xq[i] = (int8_t)q;
-    xq2[i] = (int8_t)q2;
-    if ((threadIdx.x & 31) == 0) {
-        xd[i >> 5] = d;
-        xs[i >> 5] = s;
+    ss = team_sum<64>(ss);
+    if ((t & 63) == 0) red[t >> 6] = ss;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) tot += red[k];
+    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
+    // n % 32 == 0: each 32-lane half of a wave is wholly inside or wholly past the row
+    if constexpr (NV > 0) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            const int i = t + 1024 * k;
+            if (i < n) {
+                const float o = __fmul_rn(__fmul_rn(v[k], inv), wv[k]);
+                xn[i] = o;
+                quant32_store(o, i, xq, xq2, xd, xs);
+            }
+        }
+    } else {
+        for (int i = t; i < n; i += 1024) {
+            const float x = r ? __fadd_rn(h[i], __fmul_rn(rs, r[i])) : h[i];  // recomputed, the same rounding
+            const float o = __fmul_rn(__fmul_rn(x, inv), w[i]);
+            xn[i] = o;
+            quant32_store(o, i, xq, xq2, xd, xs);
+        }
     }
+}
+
+// a = act(g) * u (u == nullptr: act(g)), act = silu (GELU 0) or the tanh form of gelu (GELU 1), fp32,
+// and the two-stage input of a (reference mmvq.py:122-133, akt_q8).
+template <int GELU>
+__global__ __launch_bounds__(256) void akt_q8_kernel(const float* __restrict__ g, const float* __restrict__ u,
+                                                     float* __restrict__ a, int8_t* __restrict__ xq,
+                                                     int8_t* __restrict__ xq2, float* __restrict__ xd,
+                                                     float* __restrict__ xs, int64_t n) {
+    asm volatile("" ::"s"(g), "s"(u), "s"(a), "s"(xq), "s"(xq2), "s"(xd), "s"(xs), "s"(n));
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads
+    if ((i & ~(int64_t)31) >= n) return;
+    const float x = g[i];
+    float v;
+    if constexpr (GELU) v = 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
+    else v = x / (1.0f + expf(-x));
+    if (u) v *= u[i];
+    a[i] = v;
+    quant32_store(v, i, xq, xq2, xd, xs);
 }
 
 // ---- weighted combine of expert outputs (reference models/moe.py:275-277, 319-320) --------------
@@ -313,6 +418,42 @@ int nmq_silu_mul_quant(const float* g, const float* u, int8_t* xq, int8_t* xq2, 
     if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
     hipLaunchKernelGGL(quant_q8_kernel<3>, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, g, u, xq, xq2,
                        xd, xs, n);
+    return (int)hipGetLastError();
+}
+
+int nmq_norm_q8(const float* h, const float* r, float rs, float* hout, const float* w, float eps, float* xn,
+                int8_t* xq, int8_t* xq2, float* xd, float* xs, int64_t n, void* stream) {
+    if (!h || !w || !xn || !xq || !xq2 || !xd || !xs || (r && !hout)) return NMQ_ERR_ARG;
+    if (!aligned(h, 4) || !aligned(w, 4) || !aligned(xn, 4) || (r && (!aligned(r, 4) || !aligned(hout, 4))))
+        return NMQ_ERR_ARG;
+    if (n <= 0 || n % 32 || n > NMQ_NORM_MAX) return NMQ_ERR_SHAPE;
+    if (r) {  // the second pass recomputes v from h and r, so hout must not overlap either
+        const uintptr_t o0 = (uintptr_t)hout, o1 = o0 + (uintptr_t)n * 4;
+        for (const float* in : {h, r})
+            if ((uintptr_t)in < o1 && o0 < (uintptr_t)in + (uintptr_t)n * 4) return NMQ_ERR_ARG;
+    }
+    void (*k)(const float*, const float*, float, float*, const float*, float, float*, int8_t*, int8_t*, float*,
+              float*, int) = n <= 1024   ? norm_q8_kernel<1>
+                             : n <= 2048 ? norm_q8_kernel<2>
+                             : n <= 4096 ? norm_q8_kernel<4>
+                             : n <= 8192 ? norm_q8_kernel<8>
+                             : n <= 16384 ? norm_q8_kernel<16> : norm_q8_kernel<0>;
+    hipLaunchKernelGGL(k, dim3(1), dim3(1024), 0, (hipStream_t)stream, h, r, rs, hout, w, eps, xn, xq, xq2, xd, xs,
+                       (int)n);
+    return (int)hipGetLastError();
+}
+
+int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, int8_t* xq2, float* xd, float* xs,
+               int64_t n, void* stream) {
+    if (!g || !a || !xq || !xq2 || !xd || !xs) return NMQ_ERR_ARG;
+    if (!aligned(g, 4) || !aligned(a, 4) || (u && !aligned(u, 4)) || (gelu != 0 && gelu != 1)) return NMQ_ERR_ARG;
+    if (n <= 0 || n % 32) return NMQ_ERR_SHAPE;
+    const int64_t blocks = (n + 255) / 256;
+    if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
+    const dim3 gr((unsigned)blocks), b(256);
+    const hipStream_t s = (hipStream_t)stream;
+    if (gelu) hipLaunchKernelGGL(akt_q8_kernel<1>, gr, b, 0, s, g, u, a, xq, xq2, xd, xs, n);
+    else hipLaunchKernelGGL(akt_q8_kernel<0>, gr, b, 0, s, g, u, a, xq, xq2, xd, xs, n);
     return (int)hipGetLastError();
 }
 

@@ -45,6 +45,9 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_mv_experts2.restype = i
     L.nmq_silu_mul_quant.argtypes, L.nmq_silu_mul_quant.restype = [p, p, p, p, p, p, i64, p], i
     L.nmq_moe_combine.argtypes, L.nmq_moe_combine.restype = [p, p, i, i, i, p, p], i
+    f = ctypes.c_float
+    L.nmq_norm_q8.argtypes, L.nmq_norm_q8.restype = [p, p, f, p, p, f, p, p, p, p, p, i64, p], i
+    L.nmq_akt_q8.argtypes, L.nmq_akt_q8.restype = [p, p, i, p, p, p, p, p, i64, p], i
     L.nmq_block_sums.argtypes, L.nmq_block_sums.restype = [i, p, p, p, p, p, i, i, p], i
     L.nmq_dequant_bf16.argtypes, L.nmq_dequant_bf16.restype = [i, p, p, i64, p], i
     L.nmq_encode.argtypes, L.nmq_encode.restype = [i, p, i64, p, i], i64

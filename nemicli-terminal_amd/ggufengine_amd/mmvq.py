@@ -3,7 +3,7 @@ Drop-in for the reference's ggufengine/mmvq.py (int8 mat-vec on Q4_K / Q6_K bloc
 
 Same names, arguments and return shapes as the reference module (mmvq.py:25-37, 808-938):
 `FORMATE`, `SPALTEN`, `MMVQ_BIS`, `MMQ_BIS`, `ZEILEN_JE_WARP`, `verfuegbar`, `Eingang`, `mv`,
-`eingang_teilen`, `mm`, `entpacken`, `schritt_moeglich`.  The arithmetic is the reference's: the
+`eingang_teilen`, `mm`, `entpacken`, `norm_q8`, `akt_q8`, `schritt_moeglich`.  The arithmetic is the reference's: the
 input is quantised per 32 values in two int8 stages (about 15 bits, fp32 scale and sum), every
 weight byte is read once and multiplied with v_dot4_i32_i8, and the per-sub-block scales are applied
 in fp32.  Launches go through libnmq.so (include/nmq.h) on torch's current stream, so they can be
@@ -11,11 +11,12 @@ captured in a HIP graph.  No torch or CPU fallback: `verfuegbar` is False withou
 gfx950 device, and calls raise.
 
 Differences from the reference (documented, same results within the parity tolerance):
-  - up to SPALTEN = 8 tokens per launch (the reference compiles 1..9);
-  - `mm` (the reference's tensor-core MMQ tiles for 17..112 tokens) runs the same int8 mat-vec
-    kernels in groups of SPALTEN tokens;
-  - the fused one-token steps (norm_q8, akt_q8, rope_kv, attention1) are not provided here;
-    `schritt_moeglich` returns False, and callers then take their unfused path
+  - up to 16 tokens per launch on the int8 matrix cores, SPALTEN = 8 on the dot4 kernels (the
+    reference compiles 1..9 per launch);
+  - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs the same int8
+    kernels in groups of 16 tokens, on the two-stage input (more precise than fp16);
+  - of the fused one-token steps, norm_q8 and akt_q8 are provided; rope_kv and attention1 are not,
+    so `schritt_moeglich` returns False and callers take their unfused layer path
     (models/baukasten.py:205).
 """
 from __future__ import annotations
@@ -168,7 +169,54 @@ def entpacken(fmt: str, raw: torch.Tensor, n_out: int, n_in: int) -> torch.Tenso
     return out
 
 
+def _f32(t: torch.Tensor) -> torch.Tensor:
+    """t as a contiguous float32 vector (t itself when it already is one)."""
+    if t.dim() == 1 and t.dtype == torch.float32 and t.is_contiguous():
+        return t
+    return t.reshape(-1).to(torch.float32).contiguous()
+
+
+def norm_q8(h: torch.Tensor, w: torch.Tensor, eps: float, rest: Optional[torch.Tensor] = None,
+            rs: float = 1.0):
+    """RMS norm of one row, fused with its Eingang (reference mmvq.py:951-961).  With `rest`, first
+    h = h + rs * rest.  -> (normalised float32, Eingang, new h) in one launch."""
+    h = _f32(h)
+    n = h.numel()
+    w = _f32(w)
+    if w.numel() != n:
+        raise ValueError(f"norm_q8: weight of {w.numel()} values for a row of {n}")
+    e = Eingang(n=n, device=h.device)
+    xn = torch.empty(n, dtype=torch.float32, device=h.device)
+    hn = None
+    if rest is not None:
+        rest = _f32(rest)
+        if rest.numel() != n:
+            raise ValueError(f"norm_q8: rest of {rest.numel()} values for a row of {n}")
+        hn = torch.empty(n, dtype=torch.float32, device=h.device)
+    _starten("norm_q8", _native.lib().nmq_norm_q8, h.data_ptr(), None if rest is None else rest.data_ptr(),
+             float(rs), None if hn is None else hn.data_ptr(), w.data_ptr(), float(eps), xn.data_ptr(),
+             *[t.data_ptr() for t in (e.xq, e.xq2, e.xd, e.xs)], n, _native.stream_ptr(h.device))
+    return xn, e, (h if hn is None else hn)
+
+
+def akt_q8(g: torch.Tensor, u: Optional[torch.Tensor], gelu: bool):
+    """act(g) * u (without u: act(g)), act = silu or tanh-gelu -> (float32, Eingang) in one launch
+    (reference mmvq.py:964-971)."""
+    g = _f32(g)
+    n = g.numel()
+    if u is not None:
+        u = _f32(u)
+        if u.numel() != n:
+            raise ValueError(f"akt_q8: up of {u.numel()} values for a gate of {n}")
+    e = Eingang(n=n, device=g.device)
+    a = torch.empty(n, dtype=torch.float32, device=g.device)
+    _starten("akt_q8", _native.lib().nmq_akt_q8, g.data_ptr(), None if u is None else u.data_ptr(), int(bool(gelu)),
+             a.data_ptr(), *[t.data_ptr() for t in (e.xq, e.xq2, e.xd, e.xs)], n, _native.stream_ptr(g.device))
+    return a, e
+
+
 def schritt_moeglich(device, H: int, Hkv: int, D: int) -> bool:
-    """The fused one-token step kernels are not part of this library: always False, so callers run
-    their general layer path (reference mmvq.py:1009-1014, models/baukasten.py:205)."""
+    """The whole fused one-token step also needs rope_kv and attention1, which are not part of this
+    library: always False, so callers run their general layer path (reference mmvq.py:1009-1014,
+    models/baukasten.py:205).  norm_q8 and akt_q8 are available on their own."""
     return False

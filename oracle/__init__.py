@@ -103,6 +103,35 @@ def quant_q8(x: np.ndarray):
     return xq, xq2, xd, xs
 
 
+def norm_row(h: np.ndarray, w: np.ndarray, eps: float, r=None, rs: float = 1.0):
+    """mmvq.py:102-120 norm_q8 without its quantisation: v = h + rs*r in fp32 (product and sum each
+    rounded, numpy float32 semantics), then the RMS norm in fp64, xn = v / sqrt(mean(v^2) + eps) * w.
+    -> (v float32, xn float64).  Pinned by closed forms in tests/test_oracle.py."""
+    h = np.ascontiguousarray(h, dtype=np.float32).ravel()
+    v = h if r is None else h + np.float32(rs) * np.ascontiguousarray(r, dtype=np.float32).ravel()
+    v64 = v.astype(np.float64)
+    inv = 1.0 / np.sqrt(np.mean(v64 * v64) + float(eps))
+    return v, v64 * inv * np.asarray(w, np.float64).ravel()
+
+
+GELU_C = 0.7978845608      # sqrt(2/pi) as written in mmvq.py:127
+GELU_A = 0.044715
+
+
+def akt(g: np.ndarray, u=None, gelu: bool = False) -> np.ndarray:
+    """mmvq.py:122-133 akt_q8 without its quantisation, in fp64: silu(g) = g / (1 + exp(-g)) or the tanh
+    form of gelu, 0.5 g (1 + tanh(GELU_C (g + GELU_A g^3))), times u if given.  Pinned by the odd-part
+    identities act(x) - act(-x) = x, by silu = x * expit(x) and by the erf form of gelu
+    (tests/test_oracle.py)."""
+    x = np.asarray(g, np.float64).ravel()
+    if gelu:
+        a = 0.5 * x * (1.0 + np.tanh(GELU_C * (x + GELU_A * x * x * x)))
+    else:
+        with np.errstate(over="ignore"):
+            a = x / (1.0 + np.exp(-x))
+    return a if u is None else a * np.asarray(u, np.float64).ravel()
+
+
 def block_sums(fmt, raw: np.ndarray, n_out: int, n_in: int, xq: np.ndarray, xq2: np.ndarray):
     """int32 sums per 16 weights: (s1, s2), each (n_out, n_in/16)."""
     raw = np.ascontiguousarray(raw, dtype=np.uint8).ravel()

@@ -75,6 +75,20 @@ def test_rejects_bad_arguments_without_launching(L):
     assert L.nmq_moe_combine(None, a16, 1, 8, 64, a16, None) == _native.NMQ_ERR_ARG
     assert L.nmq_moe_combine(a16, a16, 0, 8, 64, a16, None) == _native.NMQ_ERR_SHAPE
     assert L.nmq_moe_combine(a16, a16, 1, 8, 64, a16 + 1, None) == _native.NMQ_ERR_ARG
+    # fused producers of the one-token step
+    h, r, o = a16, a16 + 1024, a16 + 2048
+    assert L.nmq_norm_q8(None, None, 1.0, None, a16, 1e-6, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_norm_q8(h, r, 1.0, None, a16, 1e-6, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_norm_q8(h, r, 1.0, h + 64, a16, 1e-6, a16, a16, a16, a16, a16, 32,
+                         None) == _native.NMQ_ERR_ARG          # hout overlaps h
+    assert L.nmq_norm_q8(h, r, 1.0, r, a16, 1e-6, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_norm_q8(h, r, 1.0, o, a16, 1e-6, a16, a16, a16, a16, a16, 48, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_norm_q8(h, None, 1.0, None, a16, 1e-6, a16, a16, a16, a16, a16, 65536 + 32,
+                         None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_akt_q8(None, None, 0, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_akt_q8(a16, None, 2, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_akt_q8(a16, a16 + 2, 1, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_akt_q8(a16, None, 1, a16, a16, a16, a16, a16, 40, None) == _native.NMQ_ERR_SHAPE
 
 
 def test_python_api_without_gpu():

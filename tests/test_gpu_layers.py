@@ -189,6 +189,84 @@ def test_silu_mul_quant(nmq, oracle):
     assert np.all(xq[:32] == 0) and xd[0] == 0.0
 
 
+def _quant_matches(oracle, e, v):
+    """The Eingang e is, bit for bit, the two-stage input of the fp32 values v."""
+    got = [t.cpu().numpy() for t in (e.xq, e.xq2, e.xd, e.xs)]
+    for a, b in zip(got, oracle.quant_q8(v)):
+        assert np.array_equal(a, b)
+
+
+# (n, with rest, rs): n % 4096 == 0 takes the four-values-per-lane first pass
+NORM = [(4096, False, 1.0), (4096, True, 1.0), (14336, True, 0.5), (2112, False, 1.0), (2112, True, 0.25),
+        (65536, True, 1.0), (32, False, 1.0)]
+
+
+@pytest.mark.parametrize("n,with_rest,rs", NORM)
+def test_norm_q8(nmq, oracle, n, with_rest, rs):
+    """mmvq.norm_q8 (reference mmvq.py:102-120, 951-961): the new h bit for bit, xn within 2e-6 of the
+    fp64 RMS norm (per row, max |err| / max |xn|), its Eingang bit for bit the quantisation of xn."""
+    from ggufengine_amd import mmvq
+    rng = np.random.default_rng(120 + n)
+    h = (rng.standard_normal(n) * 3).astype(np.float32)
+    w = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32)
+    r = rng.standard_normal(n).astype(np.float32) if with_rest else None
+    eps = 1e-5
+    say("norm_q8", n, with_rest, rs)
+    h_d, w_d = dev(h), dev(w)
+    r_d = dev(r) if with_rest else None
+    xn, e, hn = mmvq.norm_q8(h_d, w_d, eps, rest=r_d, rs=rs)
+    torch.cuda.synchronize()
+    v, ref = oracle.norm_row(h, w, eps, r=r, rs=rs)
+    if with_rest:
+        assert hn.data_ptr() != h_d.data_ptr()
+        assert np.array_equal(hn.cpu().numpy(), v)
+    else:
+        assert hn is h_d
+    xn_np = xn.cpu().numpy()
+    assert oracle.rel_err_rows(xn_np, ref).max() <= 2e-6
+    _quant_matches(oracle, e, xn_np)
+
+
+def test_norm_q8_feeds_mv(nmq, oracle):
+    """The Eingang of norm_q8 read by a mat-vec: equal to quantising the returned xn separately."""
+    from ggufengine_amd import mmvq
+    n_out, n = 256, 4096
+    rng = np.random.default_rng(130)
+    raw_d = dev(random_blocks("Q4_K", n_out * n // 256, seed=131))
+    h_d = dev(rng.standard_normal(n).astype(np.float32))
+    w_d = dev(np.ones(n, np.float32))
+    say("norm_q8 -> mv")
+    xn, e, _ = mmvq.norm_q8(h_d, w_d, 1e-6)
+    y1 = mmvq.mv("Q4_K", raw_d, e, n_out, n)
+    y2 = mmvq.mv("Q4_K", raw_d, xn, n_out, n)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+# (n, gelu, with u)
+AKT = [(14336, False, True), (14336, True, True), (2048, False, False), (2048, True, False), (96, True, True)]
+
+
+@pytest.mark.parametrize("n,gelu,with_u", AKT)
+def test_akt_q8(nmq, oracle, n, gelu, with_u):
+    """mmvq.akt_q8 (reference mmvq.py:122-133, 964-971): a within 1e-6 of the fp64 activation (per row,
+    max |err| / max |a|), its Eingang bit for bit the quantisation of a; zero groups stay zero."""
+    from ggufengine_amd import mmvq
+    rng = np.random.default_rng(140 + n + gelu)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    g[:32] = 0.0
+    u = (rng.standard_normal(n) * 2).astype(np.float32) if with_u else None
+    say("akt_q8", n, gelu, with_u)
+    g_d = dev(g)
+    u_d = dev(u) if with_u else None
+    a, e = mmvq.akt_q8(g_d, u_d, gelu)
+    torch.cuda.synchronize()
+    a_np = a.cpu().numpy()
+    assert oracle.rel_err_rows(a_np, oracle.akt(g, u, gelu)).max() <= 1e-6
+    assert np.all(a_np[:32] == 0.0)
+    _quant_matches(oracle, e, a_np)
+
+
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "IQ2_XXS"])
 def test_mv_experts2_matches_two_launches(nmq, fmt):
     from ggufengine_amd.gguf_types import TYPE_ID

@@ -252,3 +252,46 @@ def test_cpu_baseline_gemv(oracle):
     raw = random_blocks("TQ2_0", 300 * 1280 // 256, seed=3)
     y2 = oracle.deq_gemv_f32("TQ2_0", raw, 300, 1280, x, threads=2)
     assert np.allclose(y2, oracle.mv_deq("TQ2_0", raw, 300, 1280, x)[0], rtol=1e-4, atol=1e-5)
+
+
+def test_norm_row_closed_forms(oracle):
+    """RMS norm of mmvq.py:102-120: a constant row normalises to its sign (w = 1, eps = 0), the result
+    does not change when the row is scaled, its mean square is 1, eps shrinks it as sqrt(m/(m+eps)),
+    and the residual add is two fp32 roundings (product, then sum)."""
+    n = 4096
+    for c in (3.0, -0.25):
+        _, xn = oracle.norm_row(np.full(n, c, np.float32), np.ones(n, np.float32), 0.0)
+        assert np.array_equal(xn, np.full(n, np.sign(c)))
+    rng = np.random.default_rng(5)
+    h = rng.standard_normal(n).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    _, a = oracle.norm_row(h, w, 0.0)
+    _, b = oracle.norm_row(h * np.float32(8.0), w, 0.0)           # exact power-of-two scaling
+    assert np.allclose(a, b, rtol=1e-14, atol=0)
+    _, u = oracle.norm_row(h, np.ones(n, np.float32), 0.0)
+    assert abs(np.mean(u * u) - 1.0) < 1e-12
+    m = float(np.mean(h.astype(np.float64) ** 2))
+    _, e = oracle.norm_row(h, np.ones(n, np.float32), 0.5)
+    assert np.allclose(e, u * np.sqrt(m / (m + 0.5)), rtol=1e-12)
+    r = rng.standard_normal(n).astype(np.float32)
+    v, _ = oracle.norm_row(h, w, 1e-6, r=r, rs=0.5)
+    prod = (np.float64(np.float32(0.5)) * r.astype(np.float64)).astype(np.float32)
+    assert np.array_equal(v, (h.astype(np.float64) + prod.astype(np.float64)).astype(np.float32))
+
+
+def test_akt_identities(oracle):
+    """silu and tanh-gelu of mmvq.py:122-133: act(x) - act(-x) = x for both (their even parts cancel),
+    silu = x * logistic(x), the tanh form of gelu within 1e-3 of the erf form x * Phi(x), act(0) = 0,
+    and the product with u."""
+    import math
+    from scipy.special import expit
+    x = np.linspace(-12, 12, 2401)
+    for gelu in (False, True):
+        assert np.allclose(oracle.akt(x, gelu=gelu) - oracle.akt(-x, gelu=gelu), x, rtol=0, atol=1e-12)
+        assert oracle.akt(np.zeros(1), gelu=gelu)[0] == 0.0
+    assert np.allclose(oracle.akt(x), x * expit(x), rtol=1e-13, atol=1e-300)
+    erf_gelu = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in x])
+    assert np.abs(oracle.akt(x, gelu=True) - erf_gelu).max() < 1e-3
+    u = np.linspace(-2, 2, x.size)
+    assert np.array_equal(oracle.akt(x, u, gelu=True), oracle.akt(x, gelu=True) * u)
+    assert oracle.akt(np.array([-1000.0]))[0] == 0.0              # exp overflow: -0 / inf

@@ -28,8 +28,8 @@ for p in (ROOT, os.path.join(ROOT, "nemicli-terminal_amd")):
 METRIC = "Q4_K matvec GB/s (% of HBM peak) + µs/layer, Llama-3-8B shapes, batch 1"
 HBM_PEAK_GBS = 8000.0
 LLC_BYTES = 256 << 20
-BLOCK = {"Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "TQ2_0": (256, 66), "IQ2_XXS": (256, 66)}
-TYPE = {"Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "IQ2_XXS": 16, "TQ2_0": 35}
+BLOCK = {"Q4_0": (32, 18), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "TQ2_0": (256, 66), "IQ2_XXS": (256, 66)}
+TYPE = {"Q4_0": 2, "Q8_0": 8, "Q4_K": 12, "Q6_K": 14, "IQ2_XXS": 16, "TQ2_0": 35}
 # Llama-3-8B decoder layer (Q4_K_M mix): name, format, rows, n_in, weight seed, input
 LAYER = [("q", "Q4_K", 4096, 4096, 21, "x_attn"), ("k", "Q4_K", 1024, 4096, 22, "x_attn"),
          ("v", "Q4_K", 1024, 4096, 23, "x_attn"), ("o", "Q4_K", 4096, 4096, 24, "attn_out"),

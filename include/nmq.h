@@ -20,6 +20,7 @@
 extern "C" {
 #endif
 
+#define NMQ_Q4_0 2     /* 32 values, 18 bytes: fp16 d, qs[16] (lo nibbles 0..15, hi 16..31), d*(q-8) */
 #define NMQ_Q8_0 8     /* 32 values, 34 bytes: fp16 d, int8 qs[32]                             */
 #define NMQ_Q4_K 12    /* 256 values, 144 bytes: fp16 d, dmin, scales[12], qs[128]              */
 #define NMQ_Q6_K 14    /* 256 values, 210 bytes: ql[128], qh[64], int8 sc[16], fp16 d           */

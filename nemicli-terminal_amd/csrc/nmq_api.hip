@@ -261,7 +261,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const u8* __restrict_
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     fill_tables<F>(tab, 256);
     __syncthreads();
-    // a "row" of one block; Q8_0 units span two blocks, so Q8_0 rows are two blocks (last may be one)
+    // a "row" of one block; Q4_0 / Q8_0 units span two blocks, so their rows are two blocks (last may be one)
     constexpr int BPU = FM::BV == 32 ? 2 : 1;  // blocks per row handled here
     constexpr int UPR = FM::BV == 32 ? 1 : 4;  // units per row
     const int64_t rows = (n_blocks + BPU - 1) / BPU;
@@ -310,6 +310,7 @@ __global__ __launch_bounds__(256) void dequant_bf16_kernel(const u8* __restrict_
 // ---- per-format launch tables -----------------------------------------------------------------
 template <int F>
 int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream);
+extern template int launch_mv<NMQ_Q4_0>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_Q8_0>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_Q4_K>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_Q6_K>(MvParams, int, int, hipStream_t);
@@ -318,6 +319,7 @@ extern template int launch_mv<NMQ_TQ2_0>(MvParams, int, int, hipStream_t);
 
 static int launch_any(int fmt, const MvParams& p, int nc, int n_mats, hipStream_t s) {
     switch (fmt) {
+        case NMQ_Q4_0: return launch_mv<NMQ_Q4_0>(p, nc, n_mats, s);
         case NMQ_Q8_0: return launch_mv<NMQ_Q8_0>(p, nc, n_mats, s);
         case NMQ_Q4_K: return launch_mv<NMQ_Q4_K>(p, nc, n_mats, s);
         case NMQ_Q6_K: return launch_mv<NMQ_Q6_K>(p, nc, n_mats, s);
@@ -330,6 +332,7 @@ static int launch_any(int fmt, const MvParams& p, int nc, int n_mats, hipStream_
 template <template <int> class K, typename... A>
 static int launch_fmt_kernel(int fmt, dim3 grid, hipStream_t s, A... a) {
     switch (fmt) {
+        case NMQ_Q4_0: hipLaunchKernelGGL(K<NMQ_Q4_0>::fn, grid, dim3(256), 0, s, a...); break;
         case NMQ_Q8_0: hipLaunchKernelGGL(K<NMQ_Q8_0>::fn, grid, dim3(256), 0, s, a...); break;
         case NMQ_Q4_K: hipLaunchKernelGGL(K<NMQ_Q4_K>::fn, grid, dim3(256), 0, s, a...); break;
         case NMQ_Q6_K: hipLaunchKernelGGL(K<NMQ_Q6_K>::fn, grid, dim3(256), 0, s, a...); break;
@@ -372,6 +375,7 @@ const char* nmq_strerror(int code) {
 int nmq_format_info(int fmt, int* block_values, int* block_bytes) {
     int bv, bb;
     switch (fmt) {
+        case NMQ_Q4_0: bv = 32; bb = 18; break;
         case NMQ_Q8_0: bv = 32; bb = 34; break;
         case NMQ_Q4_K: bv = 256; bb = 144; break;
         case NMQ_Q6_K: bv = 256; bb = 210; break;

@@ -104,6 +104,8 @@ __device__ __forceinline__ u32 ld16(const u8* p) { return *gp<u16>(p); }
 __device__ __forceinline__ u32 sub32x4(u32 v) { return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
 // code - 1 per byte for codes 0..3 (TQ2_0): (c + 0x7f) ^ 0x80 never carries across bytes.
 __device__ __forceinline__ u32 sub1x4(u32 v) { return (v + 0x7f7f7f7fu) ^ 0x80808080u; }
+// q - 8 per byte for nibbles 0..15 (Q4_0): (q + 0x78) ^ 0x80 never carries across bytes.
+__device__ __forceinline__ u32 sub8x4(u32 v) { return (v + 0x78787878u) ^ 0x80808080u; }
 
 // The two-stage input of one unit for one token (read from LDS).
 struct XSlice {
@@ -337,6 +339,45 @@ struct Fmt<NMQ_Q8_0> {
         for (int k = 0; k < 8; ++k) o.w[8 + k] = r.v[9 + k];
         o.ws[0] = o.ws[1] = h2f(r.v[0]);
         o.ws[2] = o.ws[3] = h2f(r.v[8] >> 16);
+        o.wm[0] = o.wm[1] = 0.f;
+    }
+};
+
+// Q4_0, 18-byte blocks (quant.py:60-64, cudakern.py:315-321): fp16 d, then qs[16] whose low
+// nibbles are values 0..15 and high nibbles values 16..31; value = d * (nibble - 8).  Unit u = blocks
+// 2u and 2u+1 (36 bytes); the second is absent when the row has an odd number of blocks and u is the
+// last (then block 0 is read again, its copy's weights set to 0 and its factor to 0).
+template <>
+struct Fmt<NMQ_Q4_0> {
+    static constexpr int BV = 32, BB = 18;
+    static constexpr bool STRIDED = false, HAS_MIN = false;
+    struct Raw {
+        u32x4 q0, q1;
+        u32 d0, d1;
+    };
+    __device__ static void load(const u8* row, int u, int nblk, Raw& r) {
+        const u8* p = row + 36 * u;
+        const bool two = 2 * u + 1 < nblk;
+        const u8* p1 = two ? p + 18 : p;
+        r.q0 = ld4(p + 2);
+        r.d0 = ld16(p);
+        const u32x4 c = ld4(p1 + 2);
+        const u32 d1 = ld16(p1);
+        r.q1 = two ? c : u32x4{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};  // nibbles 8: weight 0
+        r.d1 = two ? d1 : 0u;
+    }
+    __device__ static void decode(const Raw& r, int /*u*/, const u64* /*tab*/, WUnit& o) {
+        const u32 a[4] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w};
+        const u32 b[4] = {r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            o.w[k] = sub8x4(a[k] & 0x0f0f0f0fu);
+            o.w[4 + k] = sub8x4((a[k] >> 4) & 0x0f0f0f0fu);
+            o.w[8 + k] = sub8x4(b[k] & 0x0f0f0f0fu);
+            o.w[12 + k] = sub8x4((b[k] >> 4) & 0x0f0f0f0fu);
+        }
+        o.ws[0] = o.ws[1] = h2f(r.d0);
+        o.ws[2] = o.ws[3] = h2f(r.d1);
         o.wm[0] = o.wm[1] = 0.f;
     }
 };

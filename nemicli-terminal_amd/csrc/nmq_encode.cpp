@@ -5,6 +5,8 @@
 // (tests/test_gguf_ternaer.py:143-154).  These encoders write the block layouts the reference's
 // dequantisers read (ggufengine/quant.py), with this library's own choice of scales:
 //   Q8_0    d = max|x| / 127, q = round(x / d)                     (as quantize_row_q8_0 in ggml)
+//   Q4_0    d = -m / 8 with m the value of largest magnitude, q = min(15, trunc(x / d + 8.5))
+//           (as quantize_row_q4_0 in ggml: m itself maps to nibble 0)
 //   Q4_K    per 32: least-squares scale and min over a few step candidates, then 6-bit sub-scales
 //           relative to fp16 d / dmin
 //   Q6_K    per 16: the largest-magnitude value maps to -32; int8 sub-scales relative to fp16 d
@@ -80,6 +82,19 @@ void enc_q8_0(const float* x, u8* b) {
     const float d = amax / 127.f, id = d > 0.f ? 1.f / d : 0.f;
     put16(b, f2h(d));
     for (int j = 0; j < 32; ++j) b[2 + j] = (u8)(int8_t)clampi((int)roundf(x[j] * id), -127, 127);
+}
+
+// ---- Q4_0 ----
+void enc_q4_0(const float* x, u8* b) {
+    float amax = 0.f, m = 0.f;
+    for (int j = 0; j < 32; ++j)
+        if (fabsf(x[j]) > amax) { amax = fabsf(x[j]); m = x[j]; }
+    const float d = m / -8.f, id = d != 0.f ? 1.f / d : 0.f;
+    put16(b, f2h(d));
+    for (int j = 0; j < 16; ++j) {
+        const int lo = std::min(15, (int)(x[j] * id + 8.5f)), hi = std::min(15, (int)(x[j + 16] * id + 8.5f));
+        b[2 + j] = (u8)(lo | (hi << 4));
+    }
 }
 
 // ---- Q4_K ----
@@ -318,6 +333,7 @@ extern "C" int64_t nmq_encode(int fmt, const float* w, int64_t n, uint8_t* out, 
     int bv, bb;
     EncFn fn;
     switch (fmt) {
+        case NMQ_Q4_0: bv = 32; bb = 18; fn = enc_q4_0; break;
         case NMQ_Q8_0: bv = 32; bb = 34; fn = enc_q8_0; break;
         case NMQ_Q4_K: bv = 256; bb = 144; fn = enc_q4_k; break;
         case NMQ_Q6_K: bv = 256; bb = 210; fn = enc_q6_k; break;

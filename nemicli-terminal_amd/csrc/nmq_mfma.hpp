@@ -136,6 +136,31 @@ struct Mfma<NMQ_Q8_0> {
 };
 
 template <>
+struct Mfma<NMQ_Q4_0> {
+    // a 256-value block of this path is 8 GGUF blocks, one step each; k-block kb of a step is nibble
+    // half kb >> 1 of qs[8 (kb & 1) .. + 8]
+    static constexpr int BB = 8 * 18, STEPS = 8, GS = 32, NBMAX = 2, NBRING = 2, MIN_NC = 3;
+    struct Raw {
+        u32x2 q[8];
+        u32 d[8];
+        u32 sh;  // 0: low nibbles, 4: high nibbles
+    };
+    __device__ static void load(const u8* blk, int kb, Raw& r) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            r.q[s] = ld2(blk + 18 * s + 2 + 8 * (kb & 1));
+            r.d[s] = ld16(blk + 18 * s);
+        }
+        r.sh = 4u * (u32)(kb >> 1);
+    }
+    __device__ static u64 frag(const Raw& r, int s) {
+        const u32x2 v = r.q[s];
+        return (u64)sub8x4((v.x >> r.sh) & 0x0f0f0f0fu) | ((u64)sub8x4((v.y >> r.sh) & 0x0f0f0f0fu) << 32);
+    }
+    __device__ static float2 fac(const Raw& r, int g) { return make_float2(h2f(r.d[g]), 0.f); }
+};
+
+template <>
 struct Mfma<NMQ_TQ2_0> {
     static constexpr int BB = 66, STEPS = 8, GS = 32, NBMAX = 8, NBRING = 8, MIN_NC = 2;
     struct Raw {

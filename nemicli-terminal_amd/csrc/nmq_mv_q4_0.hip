@@ -1,0 +1,6 @@
+// Mat-vec kernels of format Q4_0: every (tokens, team width) variant of mv_kernel.
+#include "nmq_mv_impl.hpp"
+
+namespace nmq {
+template int launch_mv<NMQ_Q4_0>(MvParams, int, int, hipStream_t);
+}  // namespace nmq

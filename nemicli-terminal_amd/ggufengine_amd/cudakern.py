@@ -1,6 +1,6 @@
 """
 Drop-in for the reference's ggufengine/cudakern.py, for the block formats of this path
-(Q8_0, Q4_K, Q6_K, TQ2_0, IQ2_XXS), on gfx950.
+(Q4_0, Q8_0, Q4_K, Q6_K, TQ2_0, IQ2_XXS), on gfx950.
 
 Same names, arguments and return shapes as the reference (cudakern.py:31-54, 733-790):
 `FORMATE`, `IMMER_GEPACKT`, `MM_ZEILEN`, `MM_GROESSEN`, `verfuegbar`, `mm_bis`, `mv`, `mm`.  As in
@@ -20,7 +20,7 @@ from .gguf_types import TYPE_ID
 from .mmvq import _starten, eingang_bf16
 
 THREADS = 256
-FORMATE = {"Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "IQ2_XXS": (256, 66), "TQ2_0": (256, 66)}
+FORMATE = {"Q4_0": (32, 18), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "IQ2_XXS": (256, 66), "TQ2_0": (256, 66)}
 # formats without an int4 path in the reference (qlinear): they always stay in block format
 IMMER_GEPACKT = frozenset(("IQ2_XXS", "TQ2_0"))
 MM_ZEILEN = 16

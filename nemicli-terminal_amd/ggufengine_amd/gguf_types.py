@@ -3,6 +3,7 @@ block).  Same ids and sizes as the reference table ggufengine/gguf.py:64-78 (GGM
 follows ggml; the other formats of that table are outside this path."""
 
 GGML_TYPES = {
+    2: ("Q4_0", 32, 18),
     8: ("Q8_0", 32, 34),
     12: ("Q4_K", 256, 144),
     14: ("Q6_K", 256, 210),

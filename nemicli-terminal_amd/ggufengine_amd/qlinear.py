@@ -24,7 +24,7 @@ from .mmvq import Eingang, _starten
 
 G = 32                 # sub-block size of the GGUF formats (the reference's tinygemm group size)
 UNPACK_FROM = 256      # from this many rows: unpack to bf16 + GEMM instead of the mat-vec kernels
-_FORMATS = ("Q8_0", "Q4_K", "Q6_K")
+_FORMATS = ("Q4_0", "Q8_0", "Q4_K", "Q6_K")
 
 
 def kernel_available(device: torch.device) -> bool:

@@ -18,8 +18,8 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
-Q8_0, Q4_K, Q6_K, IQ2_XXS, TQ2_0 = 8, 12, 14, 16, 35
-FORMATS = {"Q8_0": (Q8_0, 32, 34), "Q4_K": (Q4_K, 256, 144), "Q6_K": (Q6_K, 256, 210),
+Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, TQ2_0 = 2, 8, 12, 14, 16, 35
+FORMATS = {"Q4_0": (Q4_0, 32, 18), "Q8_0": (Q8_0, 32, 34), "Q4_K": (Q4_K, 256, 144), "Q6_K": (Q6_K, 256, 210),
            "IQ2_XXS": (IQ2_XXS, 256, 66), "TQ2_0": (TQ2_0, 256, 66)}
 
 _lib = None

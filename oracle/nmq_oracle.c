@@ -6,7 +6,7 @@
  *
  * It restates, in plain C with IEEE fp32 semantics (built with -ffp-contract=off, no fast-math),
  * the arithmetic of the reference's CPU path:
- *   - the block layouts and dequantisers of ggufengine/quant.py (Q8_0, Q4_K, Q6_K, IQ2_XXS, TQ2_0),
+ *   - the block layouts and dequantisers of ggufengine/quant.py (Q4_0, Q8_0, Q4_K, Q6_K, IQ2_XXS, TQ2_0),
  *   - the two-stage int8 activation quantiser of ggufengine/mmvq.py (quant32 / quant_q8),
  *   - the integer decomposition used by the int8 kernels (per-16-value int32 sums) and the
  *     fp combine of mmvq.py / cudakern.py, accumulated in fp64,
@@ -23,6 +23,7 @@
 
 #include "iq2xxs_grid.h"
 
+#define OR_Q4_0 2
 #define OR_Q8_0 8
 #define OR_Q4_K 12
 #define OR_Q6_K 14
@@ -85,6 +86,7 @@ static int popcount7(uint32_t s) {
 
 int or_format_info(int fmt, int* block_values, int* block_bytes) {
     switch (fmt) {
+        case OR_Q4_0: *block_values = 32; *block_bytes = 18; return 0;
         case OR_Q8_0: *block_values = 32; *block_bytes = 34; return 0;
         case OR_Q4_K: *block_values = 256; *block_bytes = 144; return 0;
         case OR_Q6_K: *block_values = 256; *block_bytes = 210; return 0;
@@ -95,6 +97,16 @@ int or_format_info(int fmt, int* block_values, int* block_bytes) {
 }
 
 /* ---- dequantisers (quant.py) ------------------------------------------------------------------ */
+
+/* quant.py:60-64 deq_q4_0 with _nibbles (:53-57): the 16 low nibbles of qs are values 0..15, the
+ * high nibbles values 16..31; d * (q - 8). */
+static void deq_q4_0(const uint8_t* b, float* out) {
+    const float d = or_half_to_float(rd16(b));
+    for (int j = 0; j < 16; ++j) {
+        out[j] = d * (float)((b[2 + j] & 15) - 8);
+        out[16 + j] = d * (float)((b[2 + j] >> 4) - 8);
+    }
+}
 
 /* quant.py:46-50 deq_q8_0: d * q. */
 static void deq_q8_0(const uint8_t* b, float* out) {
@@ -179,6 +191,7 @@ int or_dequant(int fmt, const uint8_t* raw, int64_t n_blocks, float* out) {
         const uint8_t* b = raw + i * bb;
         float* o = out + i * bv;
         switch (fmt) {
+            case OR_Q4_0: deq_q4_0(b, o); break;
             case OR_Q8_0: deq_q8_0(b, o); break;
             case OR_Q4_K: deq_q4_k(b, o); break;
             case OR_Q6_K: deq_q6_k(b, o); break;
@@ -230,6 +243,7 @@ void or_quant_q8(const float* x, int64_t n, int8_t* xq, int8_t* xq2, float* xd, 
  * int8 kernels) and the fp32 factors applied per 16 values.
  *   Q4_K  w = nibble 0..15, scale d*sc_s per sub-block s, min term dmin*m_s*xs_s  (mmvq.py:341-419)
  *   Q6_K  w = q - 32, scale d*sc16                                                (mmvq.py:421-482)
+ *   Q4_0  w = nibble - 8, scale d                                                 (cudakern.py:315-321)
  *   Q8_0  w = qs, scale d                                                         (cudakern.py:307-313)
  *   TQ2_0 w = code - 1, scale d                                                   (cudakern.py:432-439)
  *   IQ2_XXS w = +-grid byte, scale d*(0.125+0.25*ls) per 32                        (cudakern.py:187-195)
@@ -237,6 +251,16 @@ void or_quant_q8(const float* x, int64_t n, int8_t* xq, int8_t* xq2, float* xd, 
  * wmin[s] is the Q4_K min factor dmin*m_s for sub-block s (0 for other formats). */
 static void decode_int(int fmt, const uint8_t* b, int8_t* w, double* wscale, double* wmin) {
     switch (fmt) {
+        case OR_Q4_0: {
+            const double d = or_half_to_float(rd16(b));
+            for (int j = 0; j < 16; ++j) {
+                w[j] = (int8_t)((b[2 + j] & 15) - 8);
+                w[16 + j] = (int8_t)((b[2 + j] >> 4) - 8);
+            }
+            wscale[0] = wscale[1] = d;
+            wmin[0] = 0.0;
+            break;
+        }
         case OR_Q8_0: {
             const double d = or_half_to_float(rd16(b));
             for (int j = 0; j < 32; ++j) w[j] = (int8_t)b[2 + j];

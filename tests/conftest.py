@@ -34,8 +34,8 @@ def random_blocks(fmt: str, n_blocks: int, seed: int) -> np.ndarray:
     """Random block bytes with small finite fp16 scales (the reference's `zufallsbloecke`,
     tests/test_gguf_iq.py:81-101 and tests/test_mmvq.py:34-45): every byte random, then the scale
     fields set to fp16 values in [0.001, 0.011)."""
-    sizes = {"Q8_0": 34, "Q4_K": 144, "Q6_K": 210, "IQ2_XXS": 66, "TQ2_0": 66}
-    fields = {"Q8_0": (0,), "Q4_K": (0, 2), "Q6_K": (208,), "IQ2_XXS": (0,), "TQ2_0": (64,)}
+    sizes = {"Q4_0": 18, "Q8_0": 34, "Q4_K": 144, "Q6_K": 210, "IQ2_XXS": 66, "TQ2_0": 66}
+    fields = {"Q4_0": (0,), "Q8_0": (0,), "Q4_K": (0, 2), "Q6_K": (208,), "IQ2_XXS": (0,), "TQ2_0": (64,)}
     rng = np.random.default_rng(seed)
     raw = rng.integers(0, 256, size=(n_blocks, sizes[fmt]), dtype=np.uint8)
     for o in fields[fmt]:

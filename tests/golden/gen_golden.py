@@ -4,9 +4,9 @@ Run in the build container:  python tests/golden/gen_golden.py
 It reads the reference's IQ2_XXS grid as text (ggufengine/iqtabellen.py:11-77, hex literals only).
 Nothing here imports or executes reference code; every expected value below comes from one of:
 
-  known_<FMT>   Q8_0 / Q4_K / Q6_K blocks built value by value following the *kernel* indexing of
-                the reference's cudakern.py (dot_Q8_0 :307-313, dot_Q4_K with skala_k4 :360-377,
-                dot_Q6_K :394-407) with scales chosen as powers of two, so that every expected
+  known_<FMT>   Q4_0 / Q8_0 / Q4_K / Q6_K blocks built value by value following the *kernel* indexing
+                of the reference's cudakern.py (dot_Q4_0 :315-321, dot_Q8_0 :307-313, dot_Q4_K with
+                skala_k4 :360-377, dot_Q6_K :394-407) with scales chosen as powers of two, so that every expected
                 value d*sc*q - dmin*m is exact.  The oracle follows quant.py (the vectorised
                 dequantiser); agreement pins both readings of the layout against each other.
   iq2_xxs       random blocks (the reference's `zufallsbloecke`, tests/test_gguf_iq.py:81-101) and
@@ -47,6 +47,17 @@ def known_q8_0(rng, nb):
         q = rng.integers(-128, 128, 32)
         raw += struct.pack("<e", d) + bytes(int(v) & 255 for v in q)
         vals += [d * int(v) for v in q]                     # dot_Q8_0: h2f(d) * (float)qs[j]
+    return np.frombuffer(bytes(raw), np.uint8), np.array(vals, np.float32)
+
+
+def known_q4_0(rng, nb):
+    raw, vals = bytearray(), []
+    for _ in range(nb):
+        d = 2.0 ** int(rng.integers(-12, -4))
+        q = rng.integers(0, 16, 32)                     # nibble of value j
+        qs = bytes(int(q[j]) | (int(q[j + 16]) << 4) for j in range(16))
+        raw += struct.pack("<e", d) + qs
+        vals += [d * (int(v) - 8) for v in q]           # dot_Q4_0: (q[j] & 15) - 8 at j, (q[j] >> 4) - 8 at j + 16
     return np.frombuffer(bytes(raw), np.uint8), np.array(vals, np.float32)
 
 
@@ -194,6 +205,9 @@ def main() -> None:
     out["tq2_0_ternary_w"] = w.reshape(-1)
     out["tq2_0_ternary_raw"] = np.frombuffer(pack_tq2_0(w.reshape(-1).tolist()), np.uint8)
     out["iq2xxs_grid"] = np.array(grid, dtype=np.uint64)
+    # added later with a generator of its own, so the fixtures above stay as they were
+    raw, vals = known_q4_0(np.random.default_rng(20261202), 24)
+    out["known_q4_0_raw"], out["known_q4_0_vals"] = raw, vals
     path = os.path.join(HERE, "formats.npz")
     np.savez_compressed(path, **out)
     print("wrote", path, {k: v.shape for k, v in out.items()})

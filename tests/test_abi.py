@@ -36,7 +36,7 @@ def test_format_table(L):
     for t, (name, v, b) in GGML_TYPES.items():
         assert L.nmq_format_info(t, ctypes.byref(bv), ctypes.byref(bb)) == 0, name
         assert (bv.value, bb.value) == (v, b), name
-    assert L.nmq_format_info(2, None, None) == -1          # Q4_0: not served
+    assert L.nmq_format_info(3, None, None) == -1          # Q4_1: not served
     from ggufengine_amd import _native
     assert L.nmq_abi_version() == _native.ABI_VERSION == 2
 

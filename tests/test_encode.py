@@ -10,7 +10,7 @@ def _w(n, seed=0):
     return (np.random.default_rng(seed).standard_normal(n) * 0.02).astype(np.float32)
 
 
-@pytest.mark.parametrize("fmt,rel", [("Q8_0", 0.01), ("Q4_K", 0.12), ("Q6_K", 0.03), ("IQ2_XXS", 0.45)])
+@pytest.mark.parametrize("fmt,rel", [("Q4_0", 0.12), ("Q8_0", 0.01), ("Q4_K", 0.12), ("Q6_K", 0.03), ("IQ2_XXS", 0.45)])
 def test_encode_dequant_close(oracle, fmt, rel):
     w = _w(256 * 64)
     raw = E.encode(fmt, w, threads=4)
@@ -26,6 +26,21 @@ def test_q8_0_follows_the_config_rule(oracle):
     assert np.array_equal(raw[:, :2].copy().view(np.float16).ravel(), d.astype(np.float16))
     q = raw[:, 2:].view(np.int8).astype(np.int32)
     assert np.all(np.abs(q - np.round(w.reshape(-1, 32) / d[:, None])) <= 1)
+
+
+def test_q4_0_follows_ggml_rule(oracle):
+    """d = -m / 8 for the value m of largest magnitude (which lands on nibble 0); every nibble within one
+    step of x / d + 8."""
+    w = _w(32 * 50, seed=5)
+    raw = E.encode("Q4_0", w).reshape(-1, 18)
+    blk = w.reshape(-1, 32)
+    m = blk[np.arange(blk.shape[0]), np.abs(blk).argmax(1)]
+    d = m / np.float32(-8)
+    assert np.array_equal(raw[:, :2].copy().view(np.float16).ravel(), d.astype(np.float16))
+    qs = raw[:, 2:].astype(np.int32)
+    q = np.concatenate([qs & 15, qs >> 4], axis=1)
+    assert np.all(q[np.arange(blk.shape[0]), np.abs(blk).argmax(1)] == 0)
+    assert np.all(np.abs(q - (blk / d[:, None] + 8)) <= 1)
 
 
 def test_tq2_0_ternary_lossless(oracle):

@@ -12,7 +12,7 @@ from conftest import random_blocks
 
 pytestmark = pytest.mark.gpu
 
-BV = {"Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "TQ2_0": 256, "IQ2_XXS": 256}
+BV = {"Q4_0": 32, "Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "TQ2_0": 256, "IQ2_XXS": 256}
 
 
 def say(*a):
@@ -37,7 +37,8 @@ DISPATCH = [("Q4_K", 1, "mmvq.mv"), ("Q4_K", 9, "mmvq.mv"), ("Q4_K", 16, "mmvq.m
             ("Q4_K", 120, "unpack"), ("Q6_K", 3, "mmvq.mv"), ("Q6_K", 17, "mmvq.mm"),
             ("TQ2_0", 1, "cudakern.mv"), ("TQ2_0", 5, "cudakern.mm"), ("TQ2_0", 17, "unpack"),
             ("IQ2_XXS", 1, "cudakern.mv"), ("IQ2_XXS", 16, "cudakern.mm"), ("Q8_0", 1, "cudakern.mv"),
-            ("Q8_0", 8, "cudakern.mm"), ("Q8_0", 24, "unpack")]
+            ("Q8_0", 8, "cudakern.mm"), ("Q8_0", 24, "unpack"), ("Q4_0", 1, "cudakern.mv"),
+            ("Q4_0", 3, "cudakern.mm"), ("Q4_0", 20, "unpack")]
 
 
 @pytest.mark.parametrize("fmt,M,branch", DISPATCH)

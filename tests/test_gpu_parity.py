@@ -18,8 +18,8 @@ from conftest import random_blocks
 
 pytestmark = pytest.mark.gpu
 
-FMTS = ["Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"]
-BV = {"Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "TQ2_0": 256, "IQ2_XXS": 256}
+FMTS = ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"]
+BV = {"Q4_0": 32, "Q8_0": 32, "Q4_K": 256, "Q6_K": 256, "TQ2_0": 256, "IQ2_XXS": 256}
 TOL_DEQ = 1e-3
 TOL_INT = 2e-5
 
@@ -75,7 +75,7 @@ def test_quant_q8_bitexact(nmq, oracle, dtype):
 @pytest.mark.parametrize("fmt", FMTS)
 def test_block_sums_bitexact(nmq, oracle, fmt):
     n_out = 37
-    n_in = 1056 if fmt == "Q8_0" else 1280      # Q8_0: 33 blocks, the last unit half full
+    n_in = 1056 if BV[fmt] == 32 else 1280      # Q4_0 / Q8_0: 33 blocks, the last unit half full
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=21)
     rng = np.random.default_rng(22)
     xq = rng.integers(-127, 128, n_in).astype(np.int8)
@@ -155,7 +155,7 @@ def test_mv_one_token_long_rows(nmq, oracle, monkeypatch, fmt, n_in, pipelined):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("nc", [2, 3, 4, 5, 8, 9, 16])
 def test_mv_tokens(nmq, oracle, fmt, nc):
-    n_out, n_in = (300, 1280) if fmt != "Q8_0" else (300, 1056)
+    n_out, n_in = (300, 1280) if BV[fmt] != 32 else (300, 1056)
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=41 + nc)
     x = np.random.default_rng(42 + nc).standard_normal((nc, n_in)).astype(np.float32)
     x[:, 7] = 30.0   # an outlier column (test_mmvq.py:71)
@@ -222,7 +222,7 @@ def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "Q8_0", "Q4_0"])
 def test_mv_long_rows_several_tiles(nmq, oracle, fmt):
     """8 tokens of 14336 values exceed the LDS budget: the input goes through in K tiles."""
     n_out, n_in, nc = 96, 14336, 8
@@ -274,9 +274,9 @@ def test_experts_shared_and_own_input(nmq, oracle, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 def test_dequant_bf16_exact(nmq, oracle, fmt):
-    nb = 3 if fmt == "Q8_0" else 5                    # odd Q8_0 count: last pair half
-    raw = random_blocks(fmt, nb * (8 if fmt == "Q8_0" else 1) + (1 if fmt == "Q8_0" else 0), seed=71)
-    n_blocks = raw.size // {"Q8_0": 34, "Q4_K": 144, "Q6_K": 210}.get(fmt, 66)
+    small = BV[fmt] == 32                             # odd Q4_0 / Q8_0 count: last pair half
+    n_blocks = 25 if small else 5
+    raw = random_blocks(fmt, n_blocks, seed=71)
     out = torch.empty(n_blocks * BV[fmt], dtype=torch.bfloat16, device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID
     say("dequant", fmt, n_blocks)

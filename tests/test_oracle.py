@@ -42,7 +42,7 @@ def test_round_bf16_matches_torch(oracle):
 
 # ---- block formats --------------------------------------------------------------------------------------
 
-@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K"])
 def test_dequant_known_answer_blocks(oracle, gold, fmt):
     """Blocks laid out by the reference's kernel indexing (cudakern.py) with exact expected values;
     the oracle follows quant.py -- both readings of the layout must agree bit for bit."""
@@ -155,12 +155,12 @@ def test_quant_q8_matches_numpy_and_bound(oracle):
 
 # ---- integer decomposition and the two mat-vec oracles -----------------------------------------------
 
-@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
 def test_block_sums_brute_force(oracle, fmt):
     """s1/s2 per 16 values equal sums over integer weights recovered from the exact dequantised
     values (value / per-group factor, + min for Q4_K): exact integer arithmetic."""
     n_out, n_in = 3, 512
-    bv, bb = {"Q8_0": (32, 34)}.get(fmt, (256, {"Q4_K": 144, "Q6_K": 210}.get(fmt, 66)))
+    bv, bb = {"Q4_0": (32, 18), "Q8_0": (32, 34)}.get(fmt, (256, {"Q4_K": 144, "Q6_K": 210}.get(fmt, 66)))
     raw = random_blocks(fmt, n_out * n_in // bv, seed=5)
     rng = np.random.default_rng(6)
     xq = rng.integers(-127, 128, n_in).astype(np.int8)
@@ -176,6 +176,9 @@ def _int_weights(oracle, fmt, raw, n_out, n_in):
     """Integer weights from the dequantised values of blocks whose factors are rebuilt here from
     the raw bytes in the layout of the reference's quant.py (Q4_K scales via get_scale_min_k4)."""
     deq = oracle.dequant(fmt, raw).astype(np.float64).reshape(n_out, n_in)
+    if fmt == "Q4_0":   # the nibbles themselves (quant.py _nibbles order: 16 low, then 16 high), minus 8
+        qs = raw.reshape(-1, 18)[:, 2:].astype(np.int64)
+        return (np.concatenate([qs & 15, qs >> 4], axis=1) - 8).reshape(n_out, n_in)
     if fmt == "Q8_0":
         b = raw.reshape(-1, 34)
         d = b[:, :2].copy().view(np.float16).astype(np.float64)
@@ -225,13 +228,13 @@ def _q6_from_bits(b):
     return out
 
 
-@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
 def test_mv_int_agrees_with_dequant_matmul(oracle, fmt):
     """The integer-decomposition mat-vec (what the kernels compute, combined in fp64) and the
     dequantise+matmul path agree to the two-stage input's precision; a wrong factor, sign or
     dropped min term would show as an O(1) relative error."""
     n_out, n_in = 64, 1024
-    bv = 32 if fmt == "Q8_0" else 256
+    bv = 32 if fmt in ("Q4_0", "Q8_0") else 256
     raw = random_blocks(fmt, n_out * n_in // bv, seed=9)
     x = np.random.default_rng(10).standard_normal((2, n_in)).astype(np.float32)
     xq, xq2, xd, xs = oracle.quant_q8(x)

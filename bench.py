@@ -200,6 +200,23 @@ def run_configs(which, steps, warmup):
                         **extra)
             del ws
 
+    if which in ("q4_0", "all"):
+        # Q4_0 (no workload of its own among the headline configurations): W ~N(0,0.02) (seed 61),
+        # 4096x4096 and 14336x4096, x ~N(0,1) (seed 62), n in 1, 2, 4, 8 with both small-batch kernels
+        for rows in (4096, 14336):
+            raw = make_weights("Q4_0", rows, 4096, 61)
+            ws = _copies(torch.from_numpy(raw).cuda())
+            X = _x(62, (8, 4096))
+            for n in (1, 2, 4, 8):
+                us, err = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup)
+                extra = {}
+                if n > 1:
+                    us4, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "0"})
+                    usm, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "2"})
+                    extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
+                _record("q4_0", f"Q4_0 {rows}x4096 n={n}", "Q4_0", us, alg_bytes("Q4_0", rows, 4096, n), err, **extra)
+            del ws
+
     if which in ("lowbit", "all"):
         # TQ2_0: codes i.i.d. P(0)=0.4, P(+-1)=0.3, d = fp16(|N(0,0.02)|) (seed 51); IQ2_XXS from N(0,0.02)
         # (seed 52); x seed 53
@@ -310,9 +327,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
     ap.add_argument("--config", default="headline",
-                    choices=("headline", "q8_0", "speculative", "lowbit", "moe", "all"),
+                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "moe", "all"),
                     help="headline (default): the metric line; the others print one record per case of "
-                         "the other workloads (Q8_0 batch 1, speculative verify n=1..8, TQ2_0/IQ2_XXS, MoE)")
+                         "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, MoE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the mat-vec path is single-GPU "

@@ -138,8 +138,9 @@ struct Mfma<NMQ_Q8_0> {
 template <>
 struct Mfma<NMQ_Q4_0> {
     // a 256-value block of this path is 8 GGUF blocks, one step each; k-block kb of a step is nibble
-    // half kb >> 1 of qs[8 (kb & 1) .. + 8]
-    static constexpr int BB = 8 * 18, STEPS = 8, GS = 32, NBMAX = 2, NBRING = 2, MIN_NC = 3;
+    // half kb >> 1 of qs[8 (kb & 1) .. + 8].  Sixteen small loads per lane and 256 values (the blocks
+    // are 2-byte aligned): measured on MI355X, this path beats the dot4 kernel only from 8 tokens.
+    static constexpr int BB = 8 * 18, STEPS = 8, GS = 32, NBMAX = 4, NBRING = 4, MIN_NC = 8;
     struct Raw {
         u32x2 q[8];
         u32 d[8];

@@ -3,7 +3,9 @@
 
 Headline (one JSON line on stdout): Q4_K 14336x4096 mat-vec at batch 1 (the gate/up projection of a
 Llama-3-8B decoder layer) -- GB/s of algorithmic bytes, % of the 8 TB/s HBM peak, us per mat-vec --
-plus us per Llama-3-8B layer (7 mat-vecs + 4 activation quantisations).
+plus us per Llama-3-8B layer: 4 activation quantisations and the 7 mat-vecs in 4 launches (q, k, v in one
+nmq_mv_multi launch, gate and up in another, o, down), checked against the oracle; the same layer with
+one launch per matrix is reported beside it.
 
 A "step" is one launch of the mat-vec kernel over one token whose two-stage int8 input (Eingang) is
 already resident in HBM.  The weight matrix of each step is one of several identical copies whose
@@ -15,6 +17,7 @@ x ~N(0, 1).  The CPU baseline (reported, not the target) times the oracle's rest
 reference's CPU path on this host: the matrix dequantised once, then an fp32 GEMV per call.
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -394,9 +397,10 @@ def main():
 
     # ---- one Llama-3-8B layer: 4 activation quantisations + 7 mat-vecs ----
     if not args.no_layer:
-        mats = {}
+        mats, raws_np = {}, {}
         for name, f, r, k, s, _ in LAYER:
-            mats[name] = torch.from_numpy(make_weights(f, r, k, s) if name != "gate" else raw).to(dev)
+            raws_np[name] = make_weights(f, r, k, s) if name != "gate" else raw
+            mats[name] = torch.from_numpy(raws_np[name]).to(dev)
         layer_bytes = sum(weight_bytes(f, r, k) for _, f, r, k, _, _ in LAYER)
         nl = max(2, -(-2 * LLC_BYTES // layer_bytes))
         layers = [mats] + [{k: v.clone() for k, v in mats.items()} for _ in range(nl - 1)]
@@ -405,40 +409,63 @@ def main():
         eg = {n: mmvq.Eingang(n=k, device=dev) for n, (k, _) in INPUTS.items()}
         ys = {name: torch.empty(r, dtype=torch.float32, device=dev) for name, _, r, _, _, _ in LAYER}
 
-        def one_layer(li):
+        order = [("x_attn", ("q", "k", "v")), ("attn_out", ("o",)), ("x_ffn", ("gate", "up")), ("act", ("down",))]
+        spec = {t[0]: t for t in LAYER}
+
+        def mats_of(lw, names):
+            """(format, n_in, weight pointers, rows, output pointers) of matrices sharing one input."""
+            f, k = spec[names[0]][1], spec[names[0]][3]
+            return (f, k, [lw[n].data_ptr() for n in names], [spec[n][2] for n in names],
+                    [ys[n].data_ptr() for n in names])
+
+        def one_layer(li, multi=True):
+            """4 input quantisations + 7 mat-vecs; multi: the matrices of one input (q, k, v and gate, up)
+            in one nmq_mv_multi launch each, else one nmq_mv launch per matrix."""
             lw = layers[li % nl]
-            order = [("x_attn", ("q", "k", "v")), ("attn_out", ("o",)), ("x_ffn", ("gate", "up")), ("act", ("down",))]
             for inp, names in order:
                 ei = eg[inp]
-                rc = L.nmq_quant_q8(xin[inp].data_ptr(), 1, ei.xq.data_ptr(), ei.xq2.data_ptr(), ei.xd.data_ptr(),
-                                    ei.xs.data_ptr(), ei.n, stream)
-                if rc:
-                    _native.check(rc)
-                for name in names:
-                    _, f, r, k, _, _ = next(t for t in LAYER if t[0] == name)
-                    rc = L.nmq_mv(TYPE[f], lw[name].data_ptr(), ei.xq.data_ptr(), ei.xq2.data_ptr(), ei.xd.data_ptr(),
-                                  ei.xs.data_ptr(), ys[name].data_ptr(), r, k, 1, stream)
-                    if rc:
-                        _native.check(rc)
+                ep = (ei.xq.data_ptr(), ei.xq2.data_ptr(), ei.xd.data_ptr(), ei.xs.data_ptr())
+                _native.check(L.nmq_quant_q8(xin[inp].data_ptr(), 1, *ep, ei.n, stream))
+                f, k, wp, rows_, yp = mats_of(lw, names)
+                if multi and len(names) > 1:
+                    m = len(names)
+                    _native.check(L.nmq_mv_multi(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
+                                                 (ctypes.c_void_p * m)(*yp), *ep, k, stream))
+                else:
+                    for w_, r_, y_ in zip(wp, rows_, yp):
+                        _native.check(L.nmq_mv(TYPE[f], w_, *ep, y_, r_, k, 1, stream))
 
         reps = max(20, args.steps // 10)
-        for i in range(max(5, args.warmup // 10)):
-            one_layer(i)
-        torch.cuda.synchronize()
-        t0.record()
-        for i in range(reps):
-            one_layer(i)
-        t1.record()
-        torch.cuda.synchronize()
-        us_layer = t0.elapsed_time(t1) / reps * 1e3
+        for multi in (False, True):
+            for i in range(max(5, args.warmup // 10)):
+                one_layer(i, multi)
+            torch.cuda.synchronize()
+            t0.record()
+            for i in range(reps):
+                one_layer(i, multi)
+            t1.record()
+            torch.cuda.synchronize()
+            us_layer = t0.elapsed_time(t1) / reps * 1e3
+            if not multi:
+                cfg["us_per_layer_one_launch_per_matrix"] = round(us_layer, 3)
         cfg["us_per_layer"] = round(us_layer, 3)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
+        # the layer's outputs (last multi-launch step, weights of copy 0 ... nl-1 are identical) against
+        # the oracle: every matrix of the layer, max relative error per output row-vector
+        errs = []
+        for inp, names in order:
+            xv = xin[inp].cpu().numpy()[None]
+            for n in names:
+                f, r, k = spec[n][1], spec[n][2], spec[n][3]
+                errs.append(float(oracle.rel_err_rows(ys[n].cpu().numpy()[None],
+                                                      oracle.mv_deq(f, raws_np[n], r, k, xv)).max()))
+        cfg["layer_max_rel_err_vs_oracle"] = max(errs)
 
         # The same layer with its inputs formed as the reference's one-token step forms them
         # (models/baukasten.py:217-241 without rope and attention): RMS norm fused with the q/k/v input,
         # the attention output quantised, residual add + RMS norm fused with the gate/up input,
-        # silu(gate) * up fused with the down input.  Same launch count, more work per launch.
+        # silu(gate) * up fused with the down input.  Same launches, more work in the input producers.
         E, FF = 4096, 14336
         rng_s = np.random.Generator(np.random.PCG64(34))
         h_s = torch.from_numpy(rng_s.standard_normal(E, dtype=np.float32)).to(dev)
@@ -454,18 +481,22 @@ def main():
             _, f, r, k, _, _ = next(t for t in LAYER if t[0] == name)
             _native.check(L.nmq_mv(TYPE[f], lw[name].data_ptr(), *ptrs(ei), ys[name].data_ptr(), r, k, 1, stream))
 
+        def mv_shared(lw, names, ei):
+            f, k, wp, rows_, yp = mats_of(lw, names)
+            m = len(names)
+            _native.check(L.nmq_mv_multi(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
+                                         (ctypes.c_void_p * m)(*yp), *ptrs(ei), k, stream))
+
         def step_layer(li):
             lw = layers[li % nl]
             _native.check(L.nmq_norm_q8(h_s.data_ptr(), None, 1.0, None, nw_s.data_ptr(), 1e-5, xn_s.data_ptr(),
                                         *ptrs(eg["x_attn"]), E, stream))
-            for name in ("q", "k", "v"):
-                mv_named(lw, name, eg["x_attn"])
+            mv_shared(lw, ("q", "k", "v"), eg["x_attn"])
             _native.check(L.nmq_quant_q8(xin["attn_out"].data_ptr(), 1, *ptrs(eg["attn_out"]), E, stream))
             mv_named(lw, "o", eg["attn_out"])
             _native.check(L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(), nw_s.data_ptr(),
                                         1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E, stream))
-            mv_named(lw, "gate", eg["x_ffn"])
-            mv_named(lw, "up", eg["x_ffn"])
+            mv_shared(lw, ("gate", "up"), eg["x_ffn"])
             _native.check(L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
                                        *ptrs(eg["act"]), FF, stream))
             mv_named(lw, "down", eg["act"])

@@ -113,6 +113,22 @@ int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, i
 int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
            float* y, int n_out, int n_in, int ncols, void* stream);
 
+/* Most matrices one nmq_mv_multi call takes. */
+#define NMQ_MAX_MATS 4
+
+/*
+ * Several matrices of one format and row length applied to one token's input in one launch:
+ *   y_i[r] = W_i[r,:] . x   for i < n_mats, r < n_outs[i],
+ * ws[i]: matrix i's rows (GGUF block format, rows back to back), ys[i]: its fp32 outputs; ws, n_outs
+ * and ys are host arrays of n_mats (1..NMQ_MAX_MATS) entries.  The input as for nmq_mv (one token).
+ * The rows of all matrices are scheduled as one matrix, so small matrices share the launch and its
+ * fixed cost.  Replaces consecutive mmvq.mv / PackedLinear calls on one shared Eingang (q, k, v and
+ * gate, up inside mmvq.eingang_teilen, models/baukasten.py:140-143, 259-260); each output equals what
+ * nmq_mv gives for that matrix alone.
+ */
+int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys,
+                 const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int n_in, void* stream);
+
 /*
  * Expert-id-gathered mat-vec (MoE): for j < n_ids,
  *   y[j][r] = W_{ids[j]}[r,:] . x_(j / x_group)

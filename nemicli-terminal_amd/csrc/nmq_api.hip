@@ -511,6 +511,38 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
     return NMQ_OK;
 }
 
+int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys,
+                 const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int n_in, void* stream) {
+    if (n_mats < 1 || n_mats > NMQ_MAX_MATS || !ws || !n_outs || !ys) return NMQ_ERR_ARG;
+    int64_t total = 0;
+    for (int i = 0; i < n_mats; ++i) {
+        const int e = check_mv(fmt, ws[i], xq, xq2, xd, xs, ys[i], n_outs[i], n_in);
+        if (e) return e;
+        total += n_outs[i];
+    }
+    if (total > (1 << 30)) return NMQ_ERR_SHAPE;
+    MvParams p{};
+    p.w = (const u8*)ws[0];
+    p.y = ys[0];
+    p.xq = xq;
+    p.xq2 = xq2;
+    p.xd = xd;
+    p.xs = xs;
+    p.n_out = (int)total;
+    p.n_in = n_in;
+    p.x_group = 1;
+    p.n_seg = n_mats == 1 ? 0 : n_mats;
+    int end = 0;
+    for (int i = 0; i < 4; ++i) {
+        const bool used = i < n_mats;
+        p.seg_w[i] = (const u8*)(used ? ws[i] : ws[0]);
+        p.seg_y[i] = used ? ys[i] : ys[0];
+        if (used) end += n_outs[i];
+        if (i < 3) p.seg_end[i] = i + 1 < n_mats ? end : 0x7fffffff;
+    }
+    return launch_any(fmt, p, 1, 1, (hipStream_t)stream);
+}
+
 static int check_experts(int fmt, const void* w, int n_ids, int64_t per_expert, int x_group, int n_out, int n_in) {
     if (n_ids < 1 || n_ids > 65535 || x_group < 1) return NMQ_ERR_ARG;
     if (per_expert >= 0) {

@@ -41,6 +41,13 @@ struct MvParams {
                    // launch's hidden arguments by a dependent scalar and vector load at kernel entry)
     const u8* w2;  // experts: a second expert tensor (same format and shape) for instances n_ids.. 2 n_ids-1
     int n_ids;     // experts: entries of ids (instances per expert tensor)
+    // One token over up to four matrices of one format and row length whose rows are concatenated
+    // (segments): rows [seg_end[i-1], seg_end[i]) belong to matrix i (seg_end[-1] = 0; entries past
+    // the last matrix are INT_MAX), read from seg_w[i] and written to seg_y[i].  n_seg = 0: one matrix.
+    int n_seg;
+    int seg_end[3];
+    const u8* seg_w[4];
+    float* seg_y[4];
 };
 
 // Weights and input row of instance m (blockIdx.y).  One matrix: w, input row 0.  Experts: instance m
@@ -60,6 +67,55 @@ __device__ __forceinline__ const u8* instance_weights(const MvParams& p, int m, 
     return p.per_expert >= 0 ? base + e * p.per_expert : (const u8*)(gp<int64_t>(base)[e]);
 }
 
+// Row addressing of the one-token kernels: one matrix (rows back to back from w, outputs from y) or
+// segments.  Copied out of the kernel arguments at entry: the helpers below take it by reference, and
+// a reference to the argument block itself would make the compiler copy the whole block to scratch.
+struct RowMap {
+    const u8* w[4];
+    float* y[4];
+    int64_t row_bytes;
+    int n_out, nblk, n_seg;
+    int end[3];
+    __device__ __forceinline__ int seg(int r) const { return (r >= end[0]) + (r >= end[1]) + (r >= end[2]); }
+    __device__ __forceinline__ int start(int i) const {
+        return i == 0 ? 0 : (i == 1 ? end[0] : (i == 2 ? end[1] : end[2]));
+    }
+    __device__ __forceinline__ const u8* row(int r) const {
+        if (n_seg == 0) return w[0] + (int64_t)r * row_bytes;
+        const int i = seg(r);
+        const u8* b = i == 0 ? w[0] : (i == 1 ? w[1] : (i == 2 ? w[2] : w[3]));
+        return b + (int64_t)(r - start(i)) * row_bytes;
+    }
+    __device__ __forceinline__ float* out(int r) const {
+        if (n_seg == 0) return y[0] + r;
+        const int i = seg(r);
+        float* o = i == 0 ? y[0] : (i == 1 ? y[1] : (i == 2 ? y[2] : y[3]));
+        return o + (r - start(i));
+    }
+};
+
+__device__ __forceinline__ RowMap row_map(const MvParams& p, const u8* wbase, float* y) {
+    RowMap m;
+    m.row_bytes = p.row_bytes;
+    m.n_out = p.n_out;
+    m.nblk = p.nblk;
+    m.n_seg = p.n_seg;
+    if (p.n_seg == 0) {
+        m.w[0] = m.w[1] = m.w[2] = m.w[3] = wbase;
+        m.y[0] = m.y[1] = m.y[2] = m.y[3] = y;
+        m.end[0] = m.end[1] = m.end[2] = 0x7fffffff;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            m.w[i] = p.seg_w[i];
+            m.y[i] = p.seg_y[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) m.end[i] = p.seg_end[i];
+    }
+    return m;
+}
+
 // Every kernel argument (and the launch shape) into the first batch of scalar loads at kernel entry:
 // left alone, the compiler fetches some of them behind branches, one dependent round trip each.
 // The asm statement is empty; it only makes the values live in scalar registers at that point.
@@ -67,7 +123,7 @@ __device__ __forceinline__ void args_early(const MvParams& p) {
     asm volatile("" ::"s"(p.w), "s"(p.ids), "s"(p.per_expert), "s"(p.row_bytes), "s"(p.xq), "s"(p.xq2),
                  "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in), "s"(p.x_group), "s"(p.kt),
                  "s"(p.ktp), "s"(p.n_tiles), "s"(p.groups), "s"(p.nblk), "s"(p.nt), "s"(p.w2), "s"(p.n_ids),
-                 "s"(gridDim.x));
+                 "s"(p.n_seg), "s"(gridDim.x));
 }
 
 // 16-byte chunk permutations of the LDS input (bijective inside every aligned group of 8 chunks).
@@ -383,14 +439,13 @@ struct Mv1Step {
     typename FM::Raw raw[RW][NITM];
     // Rows at or past n_out are replaced by row fb + rr (a row this wave has just read, so the
     // surplus loads of the last steps hit cache lines nearby instead of all waves' one last row).
-    __device__ __forceinline__ void load(const u8* wbase, int64_t row_bytes, int r0, int n_out, int lt, int U,
-                                         int nblk, int fb) {
+    __device__ __forceinline__ void load(const RowMap& rm, int r0, int lt, int U, int fb) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr) {
-            const int r = r0 + rr < n_out ? r0 + rr : min(fb + rr, n_out - 1);
-            const u8* rp = wbase + (int64_t)r * row_bytes;
+            const int r = r0 + rr < rm.n_out ? r0 + rr : min(fb + rr, rm.n_out - 1);
+            const u8* rp = rm.row(r);
 #pragma unroll
-            for (int it = 0; it < NITM; ++it) FM::load(rp, min(lt + it * T, U - 1), nblk, raw[rr][it]);
+            for (int it = 0; it < NITM; ++it) FM::load(rp, min(lt + it * T, U - 1), rm.nblk, raw[rr][it]);
         }
     }
 };
@@ -430,7 +485,7 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
 
 template <int F, int T, int RW, int NITM>
 __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, const XSlice (&x)[NITM], int r0,
-                                            int n_out, int lt, int U, const u64* tab, float* y,
+                                            const RowMap& rm, int lt, int U, const u64* tab,
                                             const LaneConst& lc) {
     float acc[RW];
 #pragma unroll
@@ -448,7 +503,7 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
     if (lt == 0) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
-            if (r0 + rr < n_out) gpw<float>(y)[r0 + rr] = acc[rr];
+            if (r0 + rr < rm.n_out) *gpw<float>(rm.out(r0 + rr)) = acc[rr];
     }
 }
 
@@ -464,7 +519,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    float* y = p.y + (int64_t)m * p.n_out;
+    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int gw = blockIdx.x * W + wave, nw = gridDim.x * W;
     constexpr int SR = P * RW;  // rows per step
@@ -480,7 +535,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     stage1_around<F>(lds, tab, p, xrow, [&] {
 #pragma unroll
         for (int i = 0; i < NBUF - 1; ++i)
-            buf[i].load(wbase, p.row_bytes, base + i * stride + off, p.n_out, lt, U, p.nblk, base + off);
+            buf[i].load(rm, base + i * stride + off, lt, U, base + off);
     });
     XSlice x[NITM];
 #pragma unroll
@@ -494,9 +549,8 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
             if (base >= p.n_out) return;  // wave-uniform
-            buf[(i + NBUF - 1) % NBUF].load(wbase, p.row_bytes, base + (NBUF - 1) * stride + off, p.n_out, lt, U,
-                                            p.nblk, base + off);
-            mv1_compute<F, T, RW, NITM>(buf[i], x, base + off, p.n_out, lt, U, tab, y, lc);
+            buf[(i + NBUF - 1) % NBUF].load(rm, base + (NBUF - 1) * stride + off, lt, U, base + off);
+            mv1_compute<F, T, RW, NITM>(buf[i], x, base + off, rm, lt, U, tab, lc);
             base += stride;
         }
     }
@@ -543,7 +597,7 @@ __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const
 
 template <int F, int RW, int NIT>
 __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, const u8* lds, int ktp, int r0,
-                                            int n_out, int lane, int U, const u64* tab, float* y,
+                                            const RowMap& rm, int lane, int U, const u64* tab,
                                             const LaneConst& lc) {
     using FM = Fmt<F>;
     float acc[RW];
@@ -575,7 +629,7 @@ __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, c
     if (lane == 0) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
-            if (r0 + rr < n_out) gpw<float>(y)[r0 + rr] = acc[rr];
+            if (r0 + rr < rm.n_out) *gpw<float>(rm.out(r0 + rr)) = acc[rr];
     }
 }
 
@@ -588,25 +642,25 @@ __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    float* y = p.y + (int64_t)m * p.n_out;
+    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int stride = gridDim.x * W * RW;
     int base = (blockIdx.x * W + wave) * RW;
     Mv1Step<F, 64, RW, NIT> a;
-    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(wbase, p.row_bytes, base, p.n_out, lane, U, p.nblk, base); });
+    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(rm, base, lane, U, base); });
     const LaneConst lc = lane_const<F, 64, NIT>(lane);
     if constexpr (!PIPE) {
         // the launch gives every wave at most one row group (grid x W >= groups)
-        if (base < p.n_out) mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+        if (base < p.n_out) mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, rm, lane, U, tab, lc);
     } else {
         Mv1Step<F, 64, RW, NIT> b;
         for (;;) {
-            b.load(wbase, p.row_bytes, base + stride, p.n_out, lane, U, p.nblk, base);
-            mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+            b.load(rm, base + stride, lane, U, base);
+            mvl_compute<F, RW, NIT>(a, lds, p.ktp, base, rm, lane, U, tab, lc);
             base += stride;
             if (base >= p.n_out) return;
-            a.load(wbase, p.row_bytes, base + stride, p.n_out, lane, U, p.nblk, base);
-            mvl_compute<F, RW, NIT>(b, lds, p.ktp, base, p.n_out, lane, U, tab, y, lc);
+            a.load(rm, base + stride, lane, U, base);
+            mvl_compute<F, RW, NIT>(b, lds, p.ktp, base, rm, lane, U, tab, lc);
             base += stride;
             if (base >= p.n_out) return;
         }
@@ -631,15 +685,15 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    float* y = p.y + (int64_t)m * p.n_out;
+    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
     Mv1Step<F, T, RW, 1> a;
-    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(wbase, p.row_bytes, r0, p.n_out, lt, U, p.nblk, r0); });
+    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
     const LaneConst lc = lane_const<F, T, 1>(lt);
-    mv1_compute<F, T, RW, 1>(a, x, r0, p.n_out, lt, U, tab, y, lc);
+    mv1_compute<F, T, RW, 1>(a, x, r0, rm, lt, U, tab, lc);
 }
 
 // ---- host side --------------------------------------------------------------------------------
@@ -892,6 +946,8 @@ inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     return s;
 }
 
+inline int seg_start_host(const MvParams& p, int i) { return i == 0 ? 0 : p.seg_end[i - 1]; }
+
 // One launch of NC <= NMQ_MAX_COLS tokens (n_mats instances along blockIdx.y).
 template <int F>
 int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
@@ -960,6 +1016,18 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(p.nt), s1.lds, stream, p);
             return (int)hipGetLastError();
         }
+    }
+    if (p.n_seg > 0) {  // the general kernel reads one matrix: one launch per segment
+        for (int i = 0; i < p.n_seg; ++i) {
+            MvParams q = p;
+            q.n_seg = 0;
+            q.w = p.seg_w[i];
+            q.y = p.seg_y[i];
+            q.n_out = (i + 1 < p.n_seg ? p.seg_end[i] : p.n_out) - seg_start_host(p, i);
+            const int e = launch_mv<F>(q, nc, n_mats, stream);
+            if (e) return e;
+        }
+        return 0;
     }
     const MvShape s = plan_mv<F>(p.n_out, p.n_in, nc, n_mats, di);
     p.kt = s.kt;

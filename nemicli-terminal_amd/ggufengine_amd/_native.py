@@ -45,6 +45,8 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_mv_experts2.restype = i
     L.nmq_silu_mul_quant.argtypes, L.nmq_silu_mul_quant.restype = [p, p, p, p, p, p, i64, p], i
     L.nmq_moe_combine.argtypes, L.nmq_moe_combine.restype = [p, p, i, i, i, p, p], i
+    L.nmq_mv_multi.argtypes = [i, i, p, p, p, p, p, p, p, i, p]
+    L.nmq_mv_multi.restype = i
     f = ctypes.c_float
     L.nmq_norm_q8.argtypes, L.nmq_norm_q8.restype = [p, p, f, p, p, f, p, p, p, p, p, i64, p], i
     L.nmq_akt_q8.argtypes, L.nmq_akt_q8.restype = [p, p, i, p, p, p, p, p, i64, p], i

@@ -149,6 +149,35 @@ def mv(fmt: str, raw: torch.Tensor, x, n_out: int, n_in: int) -> torch.Tensor:
     return y[0] if vektor else y
 
 
+MAX_MATRIZEN = 4   # matrices per mv_mehrere launch (include/nmq.h NMQ_MAX_MATS)
+
+
+def mv_mehrere(fmt: str, raws, x, n_outs, n_in: int) -> list:
+    """Several matrices of one format on one token's input in one launch (q/k/v or gate/up sharing an
+    Eingang): raws[i] (n_outs[i], n_in) in block format, x (n_in,) or an Eingang of one row ->
+    [(n_outs[i],) float32].  Each result equals `mv(fmt, raws[i], x, n_outs[i], n_in)`; the rows of all
+    matrices share the launch.  More than MAX_MATRIZEN matrices go in several launches."""
+    if fmt not in FORMATE:
+        raise ValueError(f"mmvq.mv_mehrere: format {fmt} (this module serves {tuple(FORMATE)})")
+    if len(raws) != len(n_outs) or not raws:
+        raise ValueError("mv_mehrere: one n_out per matrix")
+    e = x if isinstance(x, Eingang) else _eingang(x.reshape(-1))
+    if e.n != n_in:
+        raise ValueError(f"mv_mehrere: one token of {n_in} values expected, the input holds {e.n}")
+    dev = raws[0].device
+    ys = [torch.empty(n, dtype=torch.float32, device=dev) for n in n_outs]
+    L = _native.lib()
+    for a in range(0, len(raws), MAX_MATRIZEN):
+        part = range(a, min(a + MAX_MATRIZEN, len(raws)))
+        k = len(part)
+        ws = (ctypes.c_void_p * k)(*[raws[i].data_ptr() for i in part])
+        ns = (ctypes.c_int * k)(*[int(n_outs[i]) for i in part])
+        yp = (ctypes.c_void_p * k)(*[ys[i].data_ptr() for i in part])
+        _starten("mv", L.nmq_mv_multi, TYPE_ID[fmt], k, ws, ns, yp, e.xq.data_ptr(), e.xq2.data_ptr(),
+                 e.xd.data_ptr(), e.xs.data_ptr(), n_in, _native.stream_ptr(dev))
+    return ys
+
+
 def mm(fmt: str, raw: torch.Tensor, x: torch.Tensor, n_out: int, n_in: int) -> torch.Tensor:
     """Several tokens: x (M, n_in) -> (M, n_out) float32 (reference mmvq.py:902-920).  Runs the int8
     mat-vec kernels in groups of SPALTEN tokens."""

@@ -75,6 +75,16 @@ def test_rejects_bad_arguments_without_launching(L):
     assert L.nmq_moe_combine(None, a16, 1, 8, 64, a16, None) == _native.NMQ_ERR_ARG
     assert L.nmq_moe_combine(a16, a16, 0, 8, 64, a16, None) == _native.NMQ_ERR_SHAPE
     assert L.nmq_moe_combine(a16, a16, 1, 8, 64, a16 + 1, None) == _native.NMQ_ERR_ARG
+    # several matrices in one launch: 1..4 matrices, host arrays present, sizes in range
+    W = (ctypes.c_void_p * 5)(*([a16] * 5))
+    N = (ctypes.c_int * 5)(*([4] * 5))
+    Y = (ctypes.c_void_p * 5)(*([a16] * 5))
+    assert L.nmq_mv_multi(12, 0, W, N, Y, a16, a16, a16, a16, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_multi(12, 5, W, N, Y, a16, a16, a16, a16, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_multi(12, 2, None, N, Y, a16, a16, a16, a16, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_multi(12, 2, W, N, Y, a16, a16, a16, a16, 300, None) == _native.NMQ_ERR_SHAPE
+    N0 = (ctypes.c_int * 2)(4, 0)
+    assert L.nmq_mv_multi(12, 2, W, N0, Y, a16, a16, a16, a16, 256, None) == _native.NMQ_ERR_SHAPE
     # fused producers of the one-token step
     h, r, o = a16, a16 + 1024, a16 + 2048
     assert L.nmq_norm_q8(None, None, 1.0, None, a16, 1e-6, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG

@@ -329,3 +329,58 @@ def test_graph_capture_replays(nmq, oracle):
         assert torch.equal(y, eager), rep
         assert torch.equal(ye, eager_e), rep
         _check_mv(oracle, "Q4_K", raw, n_out, n_in, xv[None], y[None])
+
+
+# ---- several matrices on one input in one launch ---------------------------------------------------------
+
+# (format, n_in, rows of each matrix): chunk kernel, persistent kernel, long rows, a half Q8_0 unit,
+# four matrices, and rows too long for the one-token kernels (one launch per matrix then)
+MULTI = [("Q4_K", 4096, (4096, 1024, 1024)), ("Q4_K", 4096, (7000, 7000)), ("Q6_K", 14336, (300, 200)),
+         ("Q8_0", 1056, (37, 100, 5, 64)), ("IQ2_XXS", 2048, (500, 700, 900)), ("Q4_0", 4096, (1000, 3000)),
+         ("Q4_K", 32768, (50, 70))]
+
+
+@pytest.mark.parametrize("fmt,n_in,rows", MULTI)
+def test_mv_multi_equals_single_launches(nmq, oracle, fmt, n_in, rows):
+    """nmq_mv_multi: every matrix's output bit for bit what nmq_mv gives for it alone, and within the
+    parity bar of the oracle."""
+    import ctypes
+    from ggufengine_amd.gguf_types import TYPE_ID
+    raws = [random_blocks(fmt, r * n_in // BV[fmt], seed=90 + i) for i, r in enumerate(rows)]
+    x = np.random.default_rng(95).standard_normal((1, n_in)).astype(np.float32)
+    e = quant_dev(dev(x))
+    ws = [dev(r) for r in raws]
+    ys = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    alone = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    k = len(rows)
+    say("mv multi", fmt, n_in, rows)
+    L = nmq.lib()
+    args = (e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr())
+    nmq.check(L.nmq_mv_multi(TYPE_ID[fmt], k, (ctypes.c_void_p * k)(*[w.data_ptr() for w in ws]),
+                             (ctypes.c_int * k)(*rows), (ctypes.c_void_p * k)(*[y.data_ptr() for y in ys]),
+                             *args, n_in, nmq.stream_ptr()))
+    for w, y, r in zip(ws, alone, rows):
+        nmq.check(L.nmq_mv(TYPE_ID[fmt], w.data_ptr(), *args, y.data_ptr(), r, n_in, 1, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    for y, ya in zip(ys, alone):
+        assert torch.equal(y, ya)
+    _check_mv(oracle, fmt, raws[-1], rows[-1], n_in, x, ys[-1])
+
+
+def test_mv_mehrere_mirror(nmq, oracle):
+    """mmvq.mv_mehrere: q, k, v of one Eingang, and more matrices than one launch takes."""
+    from ggufengine_amd import mmvq
+    n_in = 1024
+    rows = (256, 64, 64, 128, 32)
+    raws = [random_blocks("Q4_K", r * n_in // 256, seed=97 + i) for i, r in enumerate(rows)]
+    x = np.random.default_rng(98).standard_normal(n_in).astype(np.float32)
+    say("mv_mehrere")
+    ws = [dev(r) for r in raws]
+    xt = dev(x)
+    ys = mmvq.mv_mehrere("Q4_K", ws, xt, rows, n_in)
+    single = [mmvq.mv("Q4_K", w, xt, r, n_in) for w, r in zip(ws, rows)]
+    torch.cuda.synchronize()
+    for y, s in zip(ys, single):
+        assert torch.equal(y, s)
+    with pytest.raises(ValueError):
+        mmvq.mv_mehrere("Q4_K", ws[:2], xt, rows[:1], n_in)

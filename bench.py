@@ -3,9 +3,10 @@
 
 Headline (one JSON line on stdout): Q4_K 14336x4096 mat-vec at batch 1 (the gate/up projection of a
 Llama-3-8B decoder layer) -- GB/s of algorithmic bytes, % of the 8 TB/s HBM peak, us per mat-vec --
-plus us per Llama-3-8B layer: 4 activation quantisations and the 7 mat-vecs in 4 launches (q, k, v in one
-nmq_mv_multi launch, gate and up in another, o, down), checked against the oracle; the same layer with
-one launch per matrix is reported beside it.
+plus us per Llama-3-8B layer: the 7 mat-vecs on their 4 fp32 inputs in 5 launches (q, k, v in one
+nmq_mv_x launch, gate and up in another, o, each quantising its 4096-value input itself; the down
+input quantised by its own launch), checked against the oracle.  Beside it: the same layer with 4 quantisation launches and nmq_mv_multi
+(us_per_layer_multi), and with one launch per matrix (us_per_layer_separate).
 
 A "step" is one launch of the mat-vec kernel over one token whose two-stage int8 input (Eingang) is
 already resident in HBM.  The weight matrix of each step is one of several identical copies whose
@@ -39,6 +40,9 @@ LAYER = [("q", "Q4_K", 4096, 4096, 21, "x_attn"), ("k", "Q4_K", 1024, 4096, 22, 
          ("gate", "Q4_K", 14336, 4096, 25, "x_ffn"), ("up", "Q4_K", 14336, 4096, 26, "x_ffn"),
          ("down", "Q6_K", 4096, 14336, 27, "act")]
 INPUTS = {"x_attn": (4096, 28), "attn_out": (4096, 30), "x_ffn": (4096, 31), "act": (14336, 29)}
+# longest input a layer launch takes as fp32 values (measured: staging 14336 fp32 values in the long-row
+# kernel costs more than a separate quantisation launch)
+VALUES_MAX_N_IN = 8192
 
 
 def weight_bytes(fmt, rows, n_in):
@@ -418,17 +422,25 @@ def main():
             return (f, k, [lw[n].data_ptr() for n in names], [spec[n][2] for n in names],
                     [ys[n].data_ptr() for n in names])
 
-        def one_layer(li, multi=True):
-            """4 input quantisations + 7 mat-vecs; multi: the matrices of one input (q, k, v and gate, up)
-            in one nmq_mv_multi launch each, else one nmq_mv launch per matrix."""
+        def one_layer(li, how):
+            """The 7 mat-vecs and their 4 inputs.  how = "separate": each input quantised by nmq_quant_q8,
+            one nmq_mv launch per matrix; "multi": the matrices of one input (q, k, v and gate, up) in
+            one nmq_mv_multi launch; "values": the launches on 4096-value inputs take the fp32 input
+            directly (nmq_mv_x: each launch quantises it itself), the down projection (14336 values,
+            where staging fp32 values costs more than a quantisation launch) as in "multi"."""
             lw = layers[li % nl]
             for inp, names in order:
+                f, k, wp, rows_, yp = mats_of(lw, names)
+                m = len(names)
+                if how == "values" and k <= VALUES_MAX_N_IN:
+                    _native.check(L.nmq_mv_x(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
+                                             (ctypes.c_void_p * m)(*yp), xin[inp].data_ptr(), _native.X_F32, None,
+                                             k, stream))
+                    continue
                 ei = eg[inp]
                 ep = (ei.xq.data_ptr(), ei.xq2.data_ptr(), ei.xd.data_ptr(), ei.xs.data_ptr())
                 _native.check(L.nmq_quant_q8(xin[inp].data_ptr(), 1, *ep, ei.n, stream))
-                f, k, wp, rows_, yp = mats_of(lw, names)
-                if multi and len(names) > 1:
-                    m = len(names)
+                if how != "separate" and m > 1:
                     _native.check(L.nmq_mv_multi(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
                                                  (ctypes.c_void_p * m)(*yp), *ep, k, stream))
                 else:
@@ -436,22 +448,22 @@ def main():
                         _native.check(L.nmq_mv(TYPE[f], w_, *ep, y_, r_, k, 1, stream))
 
         reps = max(20, args.steps // 10)
-        for multi in (False, True):
+        for how in ("separate", "multi", "values"):
             for i in range(max(5, args.warmup // 10)):
-                one_layer(i, multi)
+                one_layer(i, how)
             torch.cuda.synchronize()
             t0.record()
             for i in range(reps):
-                one_layer(i, multi)
+                one_layer(i, how)
             t1.record()
             torch.cuda.synchronize()
             us_layer = t0.elapsed_time(t1) / reps * 1e3
-            if not multi:
-                cfg["us_per_layer_one_launch_per_matrix"] = round(us_layer, 3)
+            if how != "values":
+                cfg[f"us_per_layer_{how}"] = round(us_layer, 3)
         cfg["us_per_layer"] = round(us_layer, 3)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
-        # the layer's outputs (last multi-launch step, weights of copy 0 ... nl-1 are identical) against
+        # the layer's outputs (last step, value input; the weight copies are identical) against
         # the oracle: every matrix of the layer, max relative error per output row-vector
         errs = []
         for inp, names in order:

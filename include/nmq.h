@@ -130,6 +130,38 @@ int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, 
                  const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int n_in, void* stream);
 
 /*
+ * Input given as values instead of an Eingang (nmq_mv_x, nmq_mv_experts_x): each launch forms the
+ * two-stage input itself, bit for bit what nmq_quant_q8 (or nmq_silu_mul_quant) writes, and saves
+ * that launch.  x_mode:
+ */
+#define NMQ_X_BF16 0          /* bf16 values                                                     */
+#define NMQ_X_F32 1           /* fp32 values                                                     */
+#define NMQ_X_F32_BF16 2      /* fp32 values rounded to bf16 first (the cudakern input convention)*/
+#define NMQ_X_SILU_MUL_BF16 3 /* bf16(silu(x) * x2), x and x2 fp32 (the down input of an expert)  */
+#define NMQ_X_MAX_N_IN 16384  /* longest row (values) of a launch with value input                */
+
+/*
+ * nmq_mv_multi with the token given as values: x (n_in values, mode x_mode; x2 the second operand of
+ * NMQ_X_SILU_MUL_BF16, else NULL), 16-byte aligned (8 for bf16).  n_in % 32 == 0, n_in <=
+ * NMQ_X_MAX_N_IN.  Replaces the quant_q8 launch of mmvq.Eingang plus the mat-vec launch(es) of
+ * mmvq.mv on a tensor (mmvq.py:852-865) with one launch.
+ */
+int nmq_mv_x(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys, const void* x,
+             int x_mode, const void* x2, int n_in, void* stream);
+
+/*
+ * Expert-id-gathered mat-vec with the input given as values: y[j] = A_{ids[j]} x_(j / x_group) for
+ * j < n_ids, and with a second tensor w_b (else NULL) also y[n_ids + j] = B_{ids[j]} x_(j / x_group)
+ * (n_ids <= 32767 then).  x: rows of n_in values (mode x_mode; x2 likewise for NMQ_X_SILU_MUL_BF16).
+ * Otherwise as nmq_mv_experts / nmq_mv_experts2.  Replaces the input quantisation plus the gathered
+ * launch(es) of cudakern.mv with ids (cudakern.py:756-774) and, with NMQ_X_SILU_MUL_BF16, the
+ * silu(gate) * up of Experten (models/moe.py:252-255) in front of the down call.
+ */
+int nmq_mv_experts_x(int fmt, const void* w_a, const void* w_b, const int64_t* ids, int n_ids, int64_t per_expert,
+                     const void* x, int x_mode, const void* x2, int x_group, float* y, int n_out, int n_in,
+                     void* stream);
+
+/*
  * Expert-id-gathered mat-vec (MoE): for j < n_ids,
  *   y[j][r] = W_{ids[j]}[r,:] . x_(j / x_group)
  * Weights of expert e start at w + e*per_expert (per_expert >= 0, bytes), or, with per_expert < 0,

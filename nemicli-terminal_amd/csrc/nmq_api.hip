@@ -40,12 +40,6 @@ DeviceInfo device_info() {
 // Input modes: 0 bf16; 1 fp32; 2 fp32 rounded to bf16 first (what the reference's cudakern entry
 // points do to their input, cudakern.py:764); 3 silu(g) * u in fp32 (g = x, u second operand), then
 // rounded to bf16 (the gated activation of a MoE expert fed to the down projection as bf16).
-__device__ __forceinline__ float round_bf16(float f) {
-    const u32 u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);  // NaN
-    return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
-}
-
 // Two-stage input of the value v held by this lane; value index i (i % 32 == lane % 32).  All 32
 // lanes of the lane's half-wave take part.
 __device__ __forceinline__ void quant32_store(float v, int64_t i, int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
@@ -471,17 +465,32 @@ int nmq_moe_combine(const float* y, const float* w, int L, int k, int E, float* 
     return (int)hipGetLastError();
 }
 
-static int check_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
-                    const float* y, int n_out, int n_in) {
+static int check_w(int fmt, const void* w, const float* y, int n_out, int n_in) {
     int bv, bb;
     if (nmq_format_info(fmt, &bv, &bb)) return NMQ_ERR_FORMAT;
-    if (!w || !xq || !xq2 || !xd || !xs || !y) return NMQ_ERR_ARG;
-    if (!aligned(xq, 16) || !aligned(xq2, 16) || !aligned(xd, 4) || !aligned(xs, 4) || !aligned(y, 4))
-        return NMQ_ERR_ARG;
+    if (!w || !y || !aligned(y, 4)) return NMQ_ERR_ARG;
     if (n_out < 1 || n_in < bv || n_in % bv || n_in > (1 << 20)) return NMQ_ERR_SHAPE;
     // Q4_K reads its 16-byte block header and quant groups with aligned 16-byte loads
     if (fmt == NMQ_Q4_K && !aligned(w, 16)) return NMQ_ERR_ARG;
     if (!aligned(w, 2)) return NMQ_ERR_ARG;
+    return NMQ_OK;
+}
+
+static int check_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
+                    const float* y, int n_out, int n_in) {
+    const int e = check_w(fmt, w, y, n_out, n_in);
+    if (e) return e;
+    if (!xq || !xq2 || !xd || !xs) return NMQ_ERR_ARG;
+    if (!aligned(xq, 16) || !aligned(xq2, 16) || !aligned(xd, 4) || !aligned(xs, 4)) return NMQ_ERR_ARG;
+    return NMQ_OK;
+}
+
+// Input given as values: the one-token kernels stage it (rows of at most NMQ_X_MAX_N_IN values).
+static int check_values(const void* x, int x_mode, const void* x2, int n_in) {
+    if (!x || x_mode < NMQ_X_BF16 || x_mode > NMQ_X_SILU_MUL_BF16) return NMQ_ERR_ARG;
+    if (!aligned(x, x_mode == NMQ_X_BF16 ? 8 : 16)) return NMQ_ERR_ARG;
+    if (x_mode == NMQ_X_SILU_MUL_BF16 && (!x2 || !aligned(x2, 16))) return NMQ_ERR_ARG;
+    if (n_in % 32 || n_in > NMQ_X_MAX_N_IN) return NMQ_ERR_SHAPE;
     return NMQ_OK;
 }
 
@@ -511,14 +520,21 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
     return NMQ_OK;
 }
 
-int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys,
-                 const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int n_in, void* stream) {
+// One token over 1..NMQ_MAX_MATS matrices (segments), input as the two-stage arrays or as values.
+static int mv_segments(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys,
+                       const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, const void* xv,
+                       const void* xv2, int x_mode, int n_in, void* stream) {
     if (n_mats < 1 || n_mats > NMQ_MAX_MATS || !ws || !n_outs || !ys) return NMQ_ERR_ARG;
     int64_t total = 0;
     for (int i = 0; i < n_mats; ++i) {
-        const int e = check_mv(fmt, ws[i], xq, xq2, xd, xs, ys[i], n_outs[i], n_in);
+        const int e = xv ? check_w(fmt, ws[i], ys[i], n_outs[i], n_in)
+                         : check_mv(fmt, ws[i], xq, xq2, xd, xs, ys[i], n_outs[i], n_in);
         if (e) return e;
         total += n_outs[i];
+    }
+    if (xv) {
+        const int e = check_values(xv, x_mode, xv2, n_in);
+        if (e) return e;
     }
     if (total > (1 << 30)) return NMQ_ERR_SHAPE;
     MvParams p{};
@@ -528,6 +544,9 @@ int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, 
     p.xq2 = xq2;
     p.xd = xd;
     p.xs = xs;
+    p.xv = xv;
+    p.xv2 = xv2;
+    p.x_mode = x_mode;
     p.n_out = (int)total;
     p.n_in = n_in;
     p.x_group = 1;
@@ -541,6 +560,17 @@ int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, 
         if (i < 3) p.seg_end[i] = i + 1 < n_mats ? end : 0x7fffffff;
     }
     return launch_any(fmt, p, 1, 1, (hipStream_t)stream);
+}
+
+int nmq_mv_multi(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys,
+                 const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int n_in, void* stream) {
+    return mv_segments(fmt, n_mats, ws, n_outs, ys, xq, xq2, xd, xs, nullptr, nullptr, 0, n_in, stream);
+}
+
+int nmq_mv_x(int fmt, int n_mats, const void* const* ws, const int* n_outs, float* const* ys, const void* x,
+             int x_mode, const void* x2, int n_in, void* stream) {
+    if (!x) return NMQ_ERR_ARG;
+    return mv_segments(fmt, n_mats, ws, n_outs, ys, nullptr, nullptr, nullptr, nullptr, x, x2, x_mode, n_in, stream);
 }
 
 static int check_experts(int fmt, const void* w, int n_ids, int64_t per_expert, int x_group, int n_out, int n_in) {
@@ -608,6 +638,32 @@ int nmq_mv_experts2(int fmt, const void* w_a, const void* w_b, const int64_t* id
     p.x_group = x_group;
     p.n_ids = n_ids;
     return launch_any(fmt, p, 1, 2 * n_ids, (hipStream_t)stream);
+}
+
+int nmq_mv_experts_x(int fmt, const void* w_a, const void* w_b, const int64_t* ids, int n_ids, int64_t per_expert,
+                     const void* x, int x_mode, const void* x2, int x_group, float* y, int n_out, int n_in,
+                     void* stream) {
+    int e = check_w(fmt, w_a, y, n_out, n_in);
+    if (e) return e;
+    if (w_b && (e = check_w(fmt, w_b, y, n_out, n_in))) return e;
+    if ((e = check_values(x, x_mode, x2, n_in))) return e;
+    if (!ids || n_ids > (w_b ? 32767 : 65535)) return NMQ_ERR_ARG;
+    if ((e = check_experts(fmt, w_a, n_ids, per_expert, x_group, n_out, n_in))) return e;
+    if (w_b && (e = check_experts(fmt, w_b, n_ids, per_expert, x_group, n_out, n_in))) return e;
+    MvParams p{};
+    p.w = (const u8*)w_a;
+    p.w2 = (const u8*)w_b;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xv = x;
+    p.xv2 = x2;
+    p.x_mode = x_mode;
+    p.y = y;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    p.x_group = x_group;
+    p.n_ids = n_ids;
+    return launch_any(fmt, p, 1, w_b ? 2 * n_ids : n_ids, (hipStream_t)stream);
 }
 
 int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2, int n_out,

@@ -55,6 +55,10 @@ __device__ __forceinline__ float dpp_f(float v) {
 __device__ __forceinline__ float swz_xor16(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
 }
+__device__ __forceinline__ float swz_xor4(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x101f));
+}
+
 __device__ __forceinline__ float half_sum_xor(float v) {
     v += swz_xor16(v);
     v += dpp_f<0x128>(v);  // row_ror:8
@@ -70,6 +74,13 @@ __device__ __forceinline__ float half_max(float v) {
     v = fmaxf(v, dpp_f<0x122>(v));
     v = fmaxf(v, dpp_f<0x121>(v));
     return v;
+}
+
+// fp32 -> bf16 (returned as fp32), round to nearest even; NaN stays NaN (torch's .to(torch.bfloat16)).
+__device__ __forceinline__ float round_bf16(float f) {
+    const u32 u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float((u | 0x00400000u) & 0xffff0000u);  // NaN
+    return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
 }
 
 __device__ __forceinline__ float h2f(u32 bits16) {

@@ -48,6 +48,12 @@ struct MvParams {
     int seg_end[3];
     const u8* seg_w[4];
     float* seg_y[4];
+    // One-token kernels: the input given as values (row m / x_group of n_in values each) instead of
+    // xq, xq2, xd, xs; the staging forms the two-stage input from them (x_mode: NMQ_X_*, xv2 the second
+    // operand of NMQ_X_SILU_MUL_BF16).  xv = nullptr: the two-stage arrays.
+    const void* xv;
+    const void* xv2;
+    int x_mode;
 };
 
 // Weights and input row of instance m (blockIdx.y).  One matrix: w, input row 0.  Experts: instance m
@@ -94,13 +100,15 @@ struct RowMap {
     }
 };
 
+// EXT = false: the kernel variant without segments (the compiler drops their addressing).
+template <bool EXT>
 __device__ __forceinline__ RowMap row_map(const MvParams& p, const u8* wbase, float* y) {
     RowMap m;
     m.row_bytes = p.row_bytes;
     m.n_out = p.n_out;
     m.nblk = p.nblk;
-    m.n_seg = p.n_seg;
-    if (p.n_seg == 0) {
+    m.n_seg = EXT ? p.n_seg : 0;
+    if (m.n_seg == 0) {
         m.w[0] = m.w[1] = m.w[2] = m.w[3] = wbase;
         m.y[0] = m.y[1] = m.y[2] = m.y[3] = y;
         m.end[0] = m.end[1] = m.end[2] = 0x7fffffff;
@@ -119,11 +127,13 @@ __device__ __forceinline__ RowMap row_map(const MvParams& p, const u8* wbase, fl
 // Every kernel argument (and the launch shape) into the first batch of scalar loads at kernel entry:
 // left alone, the compiler fetches some of them behind branches, one dependent round trip each.
 // The asm statement is empty; it only makes the values live in scalar registers at that point.
+template <bool EXT = false>
 __device__ __forceinline__ void args_early(const MvParams& p) {
     asm volatile("" ::"s"(p.w), "s"(p.ids), "s"(p.per_expert), "s"(p.row_bytes), "s"(p.xq), "s"(p.xq2),
                  "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in), "s"(p.x_group), "s"(p.kt),
                  "s"(p.ktp), "s"(p.n_tiles), "s"(p.groups), "s"(p.nblk), "s"(p.nt), "s"(p.w2), "s"(p.n_ids),
-                 "s"(p.n_seg), "s"(gridDim.x));
+                 "s"(gridDim.x));
+    if constexpr (EXT) asm volatile("" ::"s"(p.n_seg), "s"(p.xv), "s"(p.xv2), "s"(p.x_mode));
 }
 
 // 16-byte chunk permutations of the LDS input (bijective inside every aligned group of 8 chunks).
@@ -251,19 +261,133 @@ __device__ __forceinline__ void tab_store(u64* tab, u64 gv, int nt) {
     for (int i = threadIdx.x; i < 128; i += nt) tab[256 + i] = iq2_sign_mask((u32)i);
 }
 
+// ---- input staging from values ---------------------------------------------------------------
+// A workgroup forms the token's two-stage input itself, with the arithmetic of quant_q8_kernel (the
+// same results bit for bit), straight into stage1_store's LDS layout.  Four values per lane: a
+// 32-value group spans 8 aligned lanes.  For value j = 4l + e of a group, the partners of the
+// butterfly levels j ^ 16, ^ 8, ^ 4, ^ 2, ^ 1 are element e of lanes l ^ 4, ^ 2, ^ 1 and then elements
+// e ^ 2, e ^ 1 of the lane itself, so max and sum make the additions of the 32-lane butterfly.
+struct VRound {
+    float v[4];
+    float u[4];  // second operand (NMQ_X_SILU_MUL_BF16)
+};
+
+__device__ __forceinline__ void stagev_load(VRound& r, int rnd, const void* x, const void* x2, int mode, int n_in,
+                                            int nt) {
+    const int j = rnd * nt + (int)threadIdx.x;  // values 4j .. 4j + 3
+    const int o = 4 * j < n_in ? 4 * j : 0;     // past the row: re-read its start (discarded)
+    if (mode == NMQ_X_BF16) {
+        const u32x2 b = *gp<u32x2>((const u16*)x + o);
+        r.v[0] = __uint_as_float(b.x << 16);
+        r.v[1] = __uint_as_float(b.x & 0xffff0000u);
+        r.v[2] = __uint_as_float(b.y << 16);
+        r.v[3] = __uint_as_float(b.y & 0xffff0000u);
+    } else {
+        const u32x4 a = *gp<u32x4>((const float*)x + o);
+        r.v[0] = __uint_as_float(a.x); r.v[1] = __uint_as_float(a.y);
+        r.v[2] = __uint_as_float(a.z); r.v[3] = __uint_as_float(a.w);
+    }
+    if (mode == NMQ_X_SILU_MUL_BF16) {
+        const u32x4 c = *gp<u32x4>((const float*)x2 + o);
+        r.u[0] = __uint_as_float(c.x); r.u[1] = __uint_as_float(c.y);
+        r.u[2] = __uint_as_float(c.z); r.u[3] = __uint_as_float(c.w);
+    }
+}
+
+template <bool STRIDED>
+__device__ __forceinline__ void stagev_store(const VRound& r, int rnd, u8* lds, int mode, int n_in, int ktp, int nt) {
+    const int j = rnd * nt + (int)threadIdx.x;
+    const int idx = 4 * j;
+    if (idx >= ktp) return;  // whole groups of 8 lanes (ktp % 32 == 0)
+    const bool in = idx < n_in;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float t = r.v[e];
+        if (mode == NMQ_X_F32_BF16) t = round_bf16(t);
+        else if (mode == NMQ_X_SILU_MUL_BF16) t = round_bf16(t / (1.0f + expf(-t)) * r.u[e]);
+        v[e] = in ? t : 0.f;
+    }
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    m = fmaxf(m, swz_xor4(m));
+    m = fmaxf(m, dpp_f<0x4E>(m));  // quad_perm 2,3,0,1: lane ^ 2
+    m = fmaxf(m, dpp_f<0xB1>(m));  // quad_perm 1,0,3,2: lane ^ 1
+    const float d = m / 127.0f;
+    u32 pq = 0u, pq2 = 0u;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        int q = 0, q2 = 0;
+        if (d > 0.0f) {
+            q = (int)rintf(v[e] / d);
+            const float rr = fmaf(-(float)q, d, v[e]);
+            q2 = (int)rintf(rr / (d * FEIN));
+            q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+        }
+        pq |= ((u32)q & 0xffu) << (8 * e);
+        pq2 |= ((u32)q2 & 0xffu) << (8 * e);
+    }
+    float a[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = v[e] + swz_xor4(v[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = a[e] + dpp_f<0x4E>(a[e]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) a[e] = a[e] + dpp_f<0xB1>(a[e]);
+    const float sum = (a[0] + a[2]) + (a[1] + a[3]);
+    u8* qb = lds + 16 * swz<STRIDED>(idx >> 4) + (idx & 15);
+    *(u32*)qb = pq;
+    *(u32*)(qb + ktp) = pq2;
+    if ((threadIdx.x & 7) == 0) {
+        float* dd = (float*)(lds + 2 * ktp);
+        dd[idx >> 5] = d;
+        dd[ktp / 32 + (idx >> 5)] = sum;
+    }
+}
+
 // Input staging of the one-token kernels around their first weight reads.  One round (the input fits
 // one chunk per thread): its reads and the table entry go out first, the weight reads (issue()) next,
 // and the stores wait only for the older input reads.  Several rounds: everything is staged before
 // the weight reads, so that no input read can still be pending where the two paths meet (a pending
 // read there makes the compiler wait for every outstanding read, the weights included).
-template <int F, typename Issue>
+template <int F, bool EXT, typename Issue>
 __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
     using FM = Fmt<F>;
+    const int nt = p.nt;
+    if (EXT && p.xv) {
+        const int esz = p.x_mode == NMQ_X_BF16 ? 2 : 4;
+        const void* xv = (const u8*)p.xv + xrow * p.n_in * esz;
+        const void* xv2 = p.xv2 ? (const u8*)p.xv2 + xrow * p.n_in * 4 : p.xv;
+        const int rounds = (p.ktp / 4 + nt - 1) / nt;
+        if (rounds <= 2) {  // the value reads first, the weight reads next, then the quantisation
+            VRound r[2];
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                if (k < rounds) stagev_load(r[k], k, xv, xv2, p.x_mode, p.n_in, nt);
+            const u64 gv = tab_load<F>();
+            __builtin_amdgcn_sched_barrier(0);
+            issue();
+            __builtin_amdgcn_sched_barrier(0);
+            tab_store<F>(tab, gv, nt);
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                if (k < rounds) stagev_store<FM::STRIDED>(r[k], k, lds, p.x_mode, p.n_in, p.ktp, nt);
+        } else {
+            for (int k = 0; k < rounds; ++k) {
+                VRound r;
+                stagev_load(r, k, xv, xv2, p.x_mode, p.n_in, nt);
+                stagev_store<FM::STRIDED>(r, k, lds, p.x_mode, p.n_in, p.ktp, nt);
+            }
+            tab_store<F>(tab, tab_load<F>(), nt);
+            __builtin_amdgcn_sched_barrier(0);
+            issue();
+        }
+        lds_barrier();
+        return;
+    }
     const int8_t* xq = p.xq + xrow * p.n_in;
     const int8_t* xq2 = p.xq2 + xrow * p.n_in;
     const float* xd = p.xd + xrow * (p.n_in / 32);
     const float* xs = p.xs + xrow * (p.n_in / 32);
-    const int nt = p.nt;
     const int rounds = (p.ktp / 16 + nt - 1) / nt;
     if (rounds == 1) {
         XRound r;
@@ -507,9 +631,10 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
     }
 }
 
-template <int F, int T, int RW, int NITM, int NBUF>
+// EXT: the variant that also takes segments and value input (the plain one keeps the shorter code).
+template <int F, int T, int RW, int NITM, int NBUF, bool EXT>
 __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
-    args_early(p);
+    args_early<EXT>(p);
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
@@ -519,7 +644,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
+    const RowMap rm = row_map<EXT>(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int gw = blockIdx.x * W + wave, nw = gridDim.x * W;
     constexpr int SR = P * RW;  // rows per step
@@ -532,7 +657,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     Mv1Step<F, T, RW, NITM> buf[NBUF];
     const int stride = nw * SR;
     int base = gw * SR;
-    stage1_around<F>(lds, tab, p, xrow, [&] {
+    stage1_around<F, EXT>(lds, tab, p, xrow, [&] {
 #pragma unroll
         for (int i = 0; i < NBUF - 1; ++i)
             buf[i].load(rm, base + i * stride + off, lt, U, base + off);
@@ -633,21 +758,21 @@ __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, c
     }
 }
 
-template <int F, int RW, int NIT, bool PIPE>
+template <int F, int RW, int NIT, bool PIPE, bool EXT>
 __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
-    args_early(p);
+    args_early<EXT>(p);
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
+    const RowMap rm = row_map<EXT>(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int stride = gridDim.x * W * RW;
     int base = (blockIdx.x * W + wave) * RW;
     Mv1Step<F, 64, RW, NIT> a;
-    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(rm, base, lane, U, base); });
+    stage1_around<F, EXT>(lds, tab, p, xrow, [&] { a.load(rm, base, lane, U, base); });
     const LaneConst lc = lane_const<F, 64, NIT>(lane);
     if constexpr (!PIPE) {
         // the launch gives every wave at most one row group (grid x W >= groups)
@@ -672,9 +797,9 @@ __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
 // staged (the HBM latency overlaps the staging), then computes the rows in order as their data
 // arrives.  Used when the matrix fits in the resident waves of one launch (then every
 // weight byte of the matvec is in flight at once, the shape a streaming read needs at this size).
-template <int F, int T, int RW>
+template <int F, int T, int RW, bool EXT>
 __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
-    args_early(p);
+    args_early<EXT>(p);
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
@@ -685,11 +810,11 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
     const int m = blockIdx.y;
     int64_t xrow;
     const u8* wbase = instance_weights(p, m, xrow);
-    const RowMap rm = row_map(p, wbase, p.y + (int64_t)m * p.n_out);
+    const RowMap rm = row_map<EXT>(p, wbase, p.y + (int64_t)m * p.n_out);
     const int U = (p.n_in + 63) >> 6;
     const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
     Mv1Step<F, T, RW, 1> a;
-    stage1_around<F>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
+    stage1_around<F, EXT>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
     const LaneConst lc = lane_const<F, T, 1>(lt);
@@ -793,17 +918,24 @@ inline MvShape plan_mv(int n_out, int n_in, int nc, int n_mats, const DeviceInfo
 template <int F, int T, int RW>
 inline MvKernel pick_mv1_nit(int nitm, int nbuf) {
     switch (nitm) {
-        case 1: return nbuf == 4 ? mv1_kernel<F, T, RW, 1, 4> : mv1_kernel<F, T, RW, 1, 3>;
-        case 2: return nbuf == 4 ? mv1_kernel<F, T, RW, 2, 4> : mv1_kernel<F, T, RW, 2, 3>;
-        default: return mv1_kernel<F, T, RW, 4, 3>;
+        case 1: return nbuf == 4 ? mv1_kernel<F, T, RW, 1, 4, false> : mv1_kernel<F, T, RW, 1, 3, false>;
+        case 2: return nbuf == 4 ? mv1_kernel<F, T, RW, 2, 4, false> : mv1_kernel<F, T, RW, 2, 3, false>;
+        default: return mv1_kernel<F, T, RW, 4, 3, false>;
     }
 }
 template <int F, int T>
 inline MvKernel pick_mv1_rw(int rw, int nitm, int nbuf) {
     return rw == 1 ? pick_mv1_nit<F, T, 1>(nitm, nbuf) : pick_mv1_nit<F, T, 2>(nitm, nbuf);
 }
+// ext: segments or value input, one row per team and 3 buffers (the default shape) only
+template <int F, int T>
+inline MvKernel pick_mv1_ext(int nitm) {
+    return nitm == 1 ? mv1_kernel<F, T, 1, 1, 3, true> : (nitm == 2 ? mv1_kernel<F, T, 1, 2, 3, true>
+                                                                     : mv1_kernel<F, T, 1, 4, 3, true>);
+}
 template <int F>
-inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf) {
+inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf, bool ext) {
+    if (ext) return T == 16 ? pick_mv1_ext<F, 16>(nitm) : (T == 32 ? pick_mv1_ext<F, 32>(nitm) : pick_mv1_ext<F, 64>(nitm));
     switch (T) {
         case 16: return pick_mv1_rw<F, 16>(rw, nitm, nbuf);
         case 32: return pick_mv1_rw<F, 32>(rw, nitm, nbuf);
@@ -888,28 +1020,36 @@ inline MvlShape plan_mvl(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     return s;
 }
 
+template <int F, bool EXT>
+inline MvKernel pick_mvl_e(int nit, bool pipe) {
+    if (nit == 3) return pipe ? mvl_kernel<F, 1, 3, true, EXT> : mvl_kernel<F, 1, 3, false, EXT>;
+    return pipe ? mvl_kernel<F, 1, 4, true, EXT> : mvl_kernel<F, 1, 4, false, EXT>;
+}
 template <int F>
-inline MvKernel pick_mvl(int nit, bool pipe) {
-    if (nit == 3) return pipe ? mvl_kernel<F, 1, 3, true> : mvl_kernel<F, 1, 3, false>;
-    return pipe ? mvl_kernel<F, 1, 4, true> : mvl_kernel<F, 1, 4, false>;
+inline MvKernel pick_mvl(int nit, bool pipe, bool ext) {
+    return ext ? pick_mvl_e<F, true>(nit, pipe) : pick_mvl_e<F, false>(nit, pipe);
 }
 
-template <int F, int T>
+template <int F, int T, bool EXT>
 inline MvKernel pick_mvc_rw(int rw) {
     switch (rw) {
-        case 1: return mvc_kernel<F, T, 1>;
-        case 2: return mvc_kernel<F, T, 2>;
-        case 4: return mvc_kernel<F, T, 4>;
-        default: return mvc_kernel<F, T, 8>;
+        case 1: return mvc_kernel<F, T, 1, EXT>;
+        case 2: return mvc_kernel<F, T, 2, EXT>;
+        case 4: return mvc_kernel<F, T, 4, EXT>;
+        default: return mvc_kernel<F, T, 8, EXT>;
+    }
+}
+template <int F, bool EXT>
+inline MvKernel pick_mvc_e(int T, int rw) {
+    switch (T) {
+        case 16: return pick_mvc_rw<F, 16, EXT>(rw);
+        case 32: return pick_mvc_rw<F, 32, EXT>(rw);
+        default: return pick_mvc_rw<F, 64, EXT>(rw);
     }
 }
 template <int F>
-inline MvKernel pick_mvc(int T, int rw) {
-    switch (T) {
-        case 16: return pick_mvc_rw<F, 16>(rw);
-        case 32: return pick_mvc_rw<F, 32>(rw);
-        default: return pick_mvc_rw<F, 64>(rw);
-    }
+inline MvKernel pick_mvc(int T, int rw, bool ext) {
+    return ext ? pick_mvc_e<F, true>(T, rw) : pick_mvc_e<F, false>(T, rw);
 }
 
 // Chunk mode (mvc_kernel) for one token.  The rows are spread evenly over about one workgroup per
@@ -985,13 +1125,14 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     // One token: chunk mode while the rows per CU are few (every weight in flight at once), the
     // persistent prefetching kernel for larger matrices (measured on MI355X: chunk mode is faster up
     // to 4096 rows of 4096 values, the persistent kernel from 12288 rows).
+    const bool ext = p.n_seg > 0 || p.xv != nullptr;  // the kernel variant with segments / value input
     const int64_t rows_per_cu = ((int64_t)p.n_out * n_mats + di.cus - 1) / di.cus;
     const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > 24 ? 2 : 1);
     if (nc == 1 && mode == 1) {
         const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di);
         if (sc.ok) {
             p.ktp = sc.ktp;
-            MvKernel k = pick_mvc<F>(sc.T, sc.rw);
+            MvKernel k = pick_mvc<F>(sc.T, sc.rw, ext);
             p.nt = 64 * sc.W;
             hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(p.nt), sc.lds, stream, p);
             return (int)hipGetLastError();
@@ -1001,7 +1142,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const MvlShape sl = plan_mvl(p.n_out, p.n_in, n_mats, di);
         if (sl.ok) {
             p.ktp = sl.ktp;
-            MvKernel k = pick_mvl<F>(sl.nit, sl.pipe);
+            MvKernel k = pick_mvl<F>(sl.nit, sl.pipe, ext);
             p.nt = 64 * sl.W;
             hipLaunchKernelGGL(k, dim3((unsigned)sl.grid_x, (unsigned)n_mats), dim3(p.nt), sl.lds, stream, p);
             return (int)hipGetLastError();
@@ -1011,7 +1152,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
         if (s1.ok) {
             p.ktp = s1.ktp;
-            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf);
+            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf, ext);
             p.nt = 64 * s1.W;
             hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(p.nt), s1.lds, stream, p);
             return (int)hipGetLastError();
@@ -1029,6 +1170,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         }
         return 0;
     }
+    if (p.xv) return NMQ_ERR_SHAPE;  // values are staged by the one-token kernels only
     const MvShape s = plan_mv<F>(p.n_out, p.n_in, nc, n_mats, di);
     p.kt = s.kt;
     p.ktp = s.ktp;

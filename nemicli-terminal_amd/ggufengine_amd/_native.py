@@ -17,6 +17,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.abspath(os.path.join(HERE, "..", "libnmq.so"))
 
 NMQ_OK, NMQ_ERR_FORMAT, NMQ_ERR_SHAPE, NMQ_ERR_ARG, NMQ_ERR_DEVICE = 0, -1, -2, -3, -4
+X_BF16, X_F32, X_F32_BF16, X_SILU_MUL_BF16 = 0, 1, 2, 3   # include/nmq.h NMQ_X_*
+X_MAX_N_IN = 16384
 ABI_VERSION = 2
 MAX_COLS = 8
 
@@ -47,6 +49,9 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_moe_combine.argtypes, L.nmq_moe_combine.restype = [p, p, i, i, i, p, p], i
     L.nmq_mv_multi.argtypes = [i, i, p, p, p, p, p, p, p, i, p]
     L.nmq_mv_multi.restype = i
+    L.nmq_mv_x.argtypes, L.nmq_mv_x.restype = [i, i, p, p, p, p, i, p, i, p], i
+    L.nmq_mv_experts_x.argtypes = [i, p, p, p, i, i64, p, i, p, i, p, i, i, p]
+    L.nmq_mv_experts_x.restype = i
     f = ctypes.c_float
     L.nmq_norm_q8.argtypes, L.nmq_norm_q8.restype = [p, p, f, p, p, f, p, p, p, p, p, i64, p], i
     L.nmq_akt_q8.argtypes, L.nmq_akt_q8.restype = [p, p, i, p, p, p, p, p, i64, p], i

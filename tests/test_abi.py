@@ -85,6 +85,20 @@ def test_rejects_bad_arguments_without_launching(L):
     assert L.nmq_mv_multi(12, 2, W, N, Y, a16, a16, a16, a16, 300, None) == _native.NMQ_ERR_SHAPE
     N0 = (ctypes.c_int * 2)(4, 0)
     assert L.nmq_mv_multi(12, 2, W, N0, Y, a16, a16, a16, a16, 256, None) == _native.NMQ_ERR_SHAPE
+    # input given as values: mode range, alignment, second operand, row length
+    W1 = (ctypes.c_void_p * 1)(a16)
+    N1 = (ctypes.c_int * 1)(4)
+    Y1 = (ctypes.c_void_p * 1)(a16)
+    assert L.nmq_mv_x(12, 1, W1, N1, Y1, None, 1, None, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_x(12, 1, W1, N1, Y1, a16, 4, None, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_x(12, 1, W1, N1, Y1, a16 + 8, 1, None, 256, None) == _native.NMQ_ERR_ARG  # fp32: 16 B
+    assert L.nmq_mv_x(12, 1, W1, N1, Y1, a16, 3, None, 256, None) == _native.NMQ_ERR_ARG      # silu: x2
+    assert L.nmq_mv_x(12, 1, W1, N1, Y1, a16, 1, None, 16384 + 256, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mv_experts_x(12, a16, None, None, 2, 0, a16, 1, None, 1, a16, 4, 256, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_experts_x(12, a16, a16, a16, 40000, 4 * 144, a16, 1, None, 1, a16, 4, 256,
+                              None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mv_experts_x(12, a16, None, a16, 2, 144, a16, 1, None, 1, a16, 4, 256,
+                              None) == _native.NMQ_ERR_SHAPE
     # fused producers of the one-token step
     h, r, o = a16, a16 + 1024, a16 + 2048
     assert L.nmq_norm_q8(None, None, 1.0, None, a16, 1e-6, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG

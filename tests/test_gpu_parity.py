@@ -384,3 +384,100 @@ def test_mv_mehrere_mirror(nmq, oracle):
         assert torch.equal(y, s)
     with pytest.raises(ValueError):
         mmvq.mv_mehrere("Q4_K", ws[:2], xt, rows[:1], n_in)
+
+
+# ---- input given as values: the launch quantises it itself ---------------------------------------------
+
+# (format, n_in, rows of each matrix): chunk kernel, persistent kernel, long rows (several staging
+# rounds), a half Q8_0 unit with a padded staging tail, strided formats, segments
+VALUES = [("Q4_K", 4096, (4096,)), ("Q4_K", 4096, (7000, 7000)), ("Q6_K", 14336, (300,)), ("Q8_0", 1056, (37, 100)),
+          ("TQ2_0", 2048, (500,)), ("IQ2_XXS", 4096, (300, 200, 100)), ("Q4_0", 768, (2048,)),
+          ("Q6_K", 4096, (4096, 1024))]
+
+
+@pytest.mark.parametrize("fmt,n_in,rows", VALUES)
+@pytest.mark.parametrize("mode", ["f32", "f32_bf16", "bf16"])
+def test_mv_values_equal_quant_then_mv(nmq, oracle, fmt, n_in, rows, mode):
+    """nmq_mv_x: each output bit for bit what nmq_quant_q8 followed by nmq_mv gives (the staging
+    quantises with the same arithmetic), within the parity bar of the oracle."""
+    import ctypes
+    from ggufengine_amd.gguf_types import TYPE_ID
+    raws = [random_blocks(fmt, r * n_in // BV[fmt], seed=110 + i) for i, r in enumerate(rows)]
+    rng = np.random.default_rng(111)
+    x = (rng.standard_normal(n_in) * np.repeat(10.0 ** rng.uniform(-3, 2, n_in // 32), 32)).astype(np.float32)
+    x[32:64] = 0.0                                     # a zero group
+    xt = dev(x)
+    xin = xt.to(torch.bfloat16) if mode == "bf16" else xt
+    xm = {"f32": nmq.X_F32, "f32_bf16": nmq.X_F32_BF16, "bf16": nmq.X_BF16}[mode]
+    ws = [dev(r) for r in raws]
+    k = len(rows)
+    ys = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    ref = [torch.full((r,), float("nan"), device="cuda") for r in rows]
+    say("mv values", fmt, n_in, rows, mode)
+    L = nmq.lib()
+    nmq.check(L.nmq_mv_x(TYPE_ID[fmt], k, (ctypes.c_void_p * k)(*[w.data_ptr() for w in ws]), (ctypes.c_int * k)(*rows),
+                         (ctypes.c_void_p * k)(*[y.data_ptr() for y in ys]), xin.data_ptr(), xm, None, n_in,
+                         nmq.stream_ptr()))
+    from ggufengine_amd import mmvq
+    e = mmvq.Eingang(n=n_in, device=torch.device("cuda"))
+    qmode = {"f32": 1, "f32_bf16": 2, "bf16": 0}[mode]
+    nmq.check(L.nmq_quant_q8(xin.data_ptr(), qmode, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+                             e.xs.data_ptr(), n_in, nmq.stream_ptr()))
+    for w, y, r in zip(ws, ref, rows):
+        nmq.check(L.nmq_mv(TYPE_ID[fmt], w.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+                           e.xs.data_ptr(), y.data_ptr(), r, n_in, 1, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    for y, yr in zip(ys, ref):
+        assert torch.equal(y, yr)
+    xr = oracle.round_bf16(x) if mode != "f32" else x
+    _check_mv(oracle, fmt, raws[0], rows[0], n_in, xr[None], ys[0])
+
+
+@pytest.mark.parametrize("two", [False, True])
+def test_experts_values(nmq, oracle, two):
+    """nmq_mv_experts_x: fp32 tokens rounded to bf16 (the gate/up call) and bf16(silu(g) * u) (the down
+    call) against the quantisation launches followed by the gathered launches, bit for bit."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_exp, n_out, n_in, Lt, k = 10, 256, 2048, 3, 4
+    A = dev(random_blocks("Q4_K", n_exp * n_out * n_in // 256, seed=121))
+    B = dev(random_blocks("Q4_K", n_exp * n_out * n_in // 256, seed=122))
+    per = A.numel() // n_exp
+    ids = torch.tensor(np.random.default_rng(123).integers(0, n_exp, Lt * k), dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(124)
+    x = dev(rng.standard_normal((Lt, n_in)).astype(np.float32))
+    n_inst = (2 if two else 1) * Lt * k
+    y = torch.full((n_inst, n_out), float("nan"), device="cuda")
+    say("experts values", two)
+    L = nmq.lib()
+    nmq.check(L.nmq_mv_experts_x(TYPE_ID["Q4_K"], A.data_ptr(), B.data_ptr() if two else None, ids.data_ptr(),
+                                 Lt * k, per, x.data_ptr(), nmq.X_F32_BF16, None, k, y.data_ptr(), n_out, n_in,
+                                 nmq.stream_ptr()))
+    from ggufengine_amd import mmvq
+    e = mmvq.eingang_bf16(x)
+    yr = torch.full_like(y, float("nan"))
+    nmq.check(L.nmq_mv_experts(TYPE_ID["Q4_K"], A.data_ptr(), ids.data_ptr(), Lt * k, per, e.xq.data_ptr(),
+                               e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, yr.data_ptr(), n_out, n_in,
+                               nmq.stream_ptr()))
+    if two:
+        nmq.check(L.nmq_mv_experts(TYPE_ID["Q4_K"], B.data_ptr(), ids.data_ptr(), Lt * k, per, e.xq.data_ptr(),
+                                   e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, yr[Lt * k:].data_ptr(),
+                                   n_out, n_in, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    assert torch.equal(y, yr)
+    # the down call: input bf16(silu(g) * u) of each slot's own rows (x_group 1), from fp32 g and u
+    D = dev(random_blocks("Q6_K", n_exp * n_in * n_out // 256, seed=125))      # n_out -> n_in
+    g = dev((rng.standard_normal((Lt * k, n_out)) * 3).astype(np.float32))
+    u = dev(rng.standard_normal((Lt * k, n_out)).astype(np.float32))
+    yd = torch.full((Lt * k, n_in), float("nan"), device="cuda")
+    perd = D.numel() // n_exp
+    nmq.check(L.nmq_mv_experts_x(TYPE_ID["Q6_K"], D.data_ptr(), None, ids.data_ptr(), Lt * k, perd, g.data_ptr(),
+                                 nmq.X_SILU_MUL_BF16, u.data_ptr(), 1, yd.data_ptr(), n_in, n_out, nmq.stream_ptr()))
+    a = mmvq.Eingang(n=Lt * k * n_out, device=torch.device("cuda"))
+    nmq.check(L.nmq_silu_mul_quant(g.data_ptr(), u.data_ptr(), a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(),
+                                   a.xs.data_ptr(), Lt * k * n_out, nmq.stream_ptr()))
+    ydr = torch.full_like(yd, float("nan"))
+    nmq.check(L.nmq_mv_experts(TYPE_ID["Q6_K"], D.data_ptr(), ids.data_ptr(), Lt * k, perd, a.xq.data_ptr(),
+                               a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), 1, ydr.data_ptr(), n_in, n_out,
+                               nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    assert torch.equal(yd, ydr)

@@ -191,7 +191,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     if (i >= (int64_t)L * E) return;
     const int t = (int)(i / E), e = (int)(i % E);
     float acc = 0.f;
-    for (int j = 0; j < k; ++j) acc = fmaf(gp<float>(w)[(int64_t)t * k + j], gp<float>(y)[((int64_t)t * k + j) * E + e], acc);
+    if (k <= 16) {  // every read issued before the first sum (one memory round trip, not k)
+        float wv[16], yv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const int jj = j < k ? j : 0;
+            wv[j] = gp<float>(w)[(int64_t)t * k + jj];
+            yv[j] = gp<float>(y)[((int64_t)t * k + jj) * E + e];
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            if (j < k) acc = fmaf(wv[j], yv[j], acc);
+    } else {
+        for (int j = 0; j < k; ++j)
+            acc = fmaf(gp<float>(w)[(int64_t)t * k + j], gp<float>(y)[((int64_t)t * k + j) * E + e], acc);
+    }
     gpw<float>(out)[i] = acc;
 }
 

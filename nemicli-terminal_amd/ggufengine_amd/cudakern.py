@@ -17,7 +17,7 @@ import torch
 
 from . import _native
 from .gguf_types import TYPE_ID
-from .mmvq import _starten, eingang_bf16
+from .mmvq import _starten, _werte, eingang_bf16
 
 THREADS = 256
 FORMATE = {"Q4_0": (32, 18), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "IQ2_XXS": (256, 66), "TQ2_0": (256, 66)}
@@ -50,7 +50,6 @@ def mv(fmt: str, raw: torch.Tensor, ids: torch.Tensor, x: torch.Tensor, n_out: i
     geraet = x.device
     ids = ids.to(geraet, torch.int64).contiguous()
     k = ids.numel()
-    e = eingang_bf16(x)
     y = torch.empty(k, n_out, dtype=torch.float32, device=geraet)
     if adressen is None:
         quelle, per = raw, raw.shape[1] if raw.dim() == 2 else raw.numel()
@@ -58,6 +57,12 @@ def mv(fmt: str, raw: torch.Tensor, ids: torch.Tensor, x: torch.Tensor, n_out: i
         quelle, per = adressen.to(geraet, torch.int64).contiguous(), -1
     x_group = 1 if x.dim() == 2 else k
     L = _native.lib()
+    w = _werte(x, n_in, bf16=True)
+    if w is not None:   # the launch rounds x to bf16 and quantises it (no quantisation launch)
+        _starten("mv_experts", L.nmq_mv_experts_x, TYPE_ID[fmt], quelle.data_ptr(), None, ids.data_ptr(), k, per,
+                 w[0].data_ptr(), w[1], None, x_group, y.data_ptr(), n_out, n_in, _native.stream_ptr(geraet))
+        return y
+    e = eingang_bf16(x)
     _starten("mv_experts", L.nmq_mv_experts, TYPE_ID[fmt], quelle.data_ptr(), ids.data_ptr(), k, per,
              e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), x_group, y.data_ptr(),
              n_out, n_in, _native.stream_ptr(geraet))

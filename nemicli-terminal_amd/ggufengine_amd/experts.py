@@ -9,10 +9,10 @@ The reference's expert path around the gathered mat-vec, on this library's kerne
     renormalised to sum 1 (+1e-20), times the weights scale.
   - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  Every
     (token, slot) pair on its own, in (token, slot) order (the reference's one-token and graph paths),
-    the weighted sum per token in slot order.  Five launches: each token's input quantised once (after
-    rounding to bf16, as cudakern.mv does), gate and up in one gathered launch reading that input
-    through the token's k slots (x_group = k), silu(gate) * up rounded to bf16 and quantised in one
-    launch, down on each slot's own activation, the combine.
+    the weighted sum per token in slot order.  Three launches: gate and up in one gathered launch
+    reading each token's input through its k slots (x_group = k), the input rounded to bf16 (as
+    cudakern.mv does) and quantised inside the launch; down on each slot's own activation
+    bf16(silu(gate) * up), also formed and quantised inside its launch; the combine.
 
 Every expert product runs on libnmq's HIP kernels; without the library the constructor raises.
 """
@@ -25,7 +25,7 @@ import torch.nn.functional as F
 
 from . import _native, cudakern
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
-from .mmvq import Eingang, _starten, eingang_bf16
+from .mmvq import WERTE_BIS, Eingang, _starten, _werte, eingang_bf16
 
 
 class PackedExperts:
@@ -61,23 +61,37 @@ class PackedExperts:
         return cudakern.mv(self.name, self.raw, ids, a.reshape(ids.numel(), -1), self.n_out, self.n_in,
                            self.adressen)
 
+    def _quelle(self, dev):
+        if self.adressen is None:
+            return self.raw, self.raw.shape[1]
+        return self.adressen.to(dev, torch.int64).contiguous(), -1
+
     def matvec_tokens(self, ids: torch.Tensor, x) -> torch.Tensor:
         """ids (L, k), x (L, n_in) or its Eingang: expert ids[t, j] applied to token t's input ->
-        (L*k, n_out) float32, rows in (token, slot) order (each token's input quantised once, read by its
-        k slots).  A tensor x is rounded to bf16 first, as cudakern.mv does."""
+        (L*k, n_out) float32, rows in (token, slot) order (each token's input read by its k slots).  A
+        tensor x is rounded to bf16 first, as cudakern.mv does (in the launch itself for rows of up to
+        WERTE_BIS values)."""
         L_, k = ids.shape
+        dev = x.xq.device if isinstance(x, Eingang) else x.device
+        flat = ids.reshape(-1).to(dev, torch.int64).contiguous()
+        y = torch.empty(L_ * k, self.n_out, dtype=torch.float32, device=dev)
+        quelle, per = self._quelle(dev)
+        L = _native.lib()
+        if not isinstance(x, Eingang):
+            if x.numel() != L_ * self.n_in:
+                raise ValueError(f"matvec_tokens: input of {x.numel()} values for {L_} tokens of {self.n_in}")
+            w = _werte(x.reshape(L_, self.n_in), self.n_in, bf16=True)
+            if w is not None:
+                _starten("mv_experts", L.nmq_mv_experts_x, TYPE_ID[self.name], quelle.data_ptr(), None,
+                         flat.data_ptr(), L_ * k, per, w[0].data_ptr(), w[1], None, k, y.data_ptr(), self.n_out,
+                         self.n_in, _native.stream_ptr(dev))
+                return y
         e = x if isinstance(x, Eingang) else eingang_bf16(x.reshape(L_, self.n_in))
         if e.n != L_ * self.n_in:
             raise ValueError(f"matvec_tokens: input of {e.n} values for {L_} tokens of {self.n_in}")
-        flat = ids.reshape(-1).to(e.xq.device, torch.int64).contiguous()
-        y = torch.empty(L_ * k, self.n_out, dtype=torch.float32, device=e.xq.device)
-        if self.adressen is None:
-            quelle, per = self.raw, self.raw.shape[1]
-        else:
-            quelle, per = self.adressen.to(e.xq.device, torch.int64).contiguous(), -1
-        _starten("mv_experts", _native.lib().nmq_mv_experts, TYPE_ID[self.name], quelle.data_ptr(), flat.data_ptr(),
+        _starten("mv_experts", L.nmq_mv_experts, TYPE_ID[self.name], quelle.data_ptr(), flat.data_ptr(),
                  L_ * k, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, y.data_ptr(),
-                 self.n_out, self.n_in, _native.stream_ptr(e.xq.device))
+                 self.n_out, self.n_in, _native.stream_ptr(dev))
         return y
 
 
@@ -113,8 +127,37 @@ class Experten:
 
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights.
-        Five launches: the tokens' input (rounded to bf16, two-stage int8), gate and up together on every
-        (token, slot), silu(gate) * up made the down input, down on every slot, the weighted combine."""
+        Three launches: gate and up together on every (token, slot), each token's input rounded to bf16
+        and quantised in the launch; down on every slot, its input bf16(silu(gate) * up) formed and
+        quantised in the launch; the weighted combine.  (Rows longer than WERTE_BIS values, or a gate
+        and up of different layout: the input quantisations as launches of their own.)"""
+        L_, E = x.shape
+        k = idx.shape[1]
+        dev = x.device
+        if not self._fused() or max(E, self.gate.n_out) > WERTE_BIS or x.dtype != torch.float32:
+            return self._aufgeteilt(x, idx, w)
+        L = _native.lib()
+        st = _native.stream_ptr(dev)
+        n = L_ * k
+        FF = self.gate.n_out
+        xc = x.contiguous()
+        flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
+        gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
+        (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
+        _starten("mv_experts2", L.nmq_mv_experts_x, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
+                 flat.data_ptr(), n, per, xc.data_ptr(), _native.X_F32_BF16, None, k, gu.data_ptr(), FF, E, st)
+        y = torch.empty(n, E, dtype=torch.float32, device=dev)
+        wd, perd = self.down._quelle(dev)
+        _starten("mv_experts", L.nmq_mv_experts_x, TYPE_ID[self.down.name], wd.data_ptr(), None, flat.data_ptr(), n,
+                 perd, gu.data_ptr(), _native.X_SILU_MUL_BF16, gu[n:].data_ptr(), 1, y.data_ptr(), E, FF, st)
+        out = torch.empty(L_, E, dtype=torch.float32, device=dev)
+        wf = w.to(dev, torch.float32).contiguous()
+        _starten("moe_combine", L.nmq_moe_combine, y.data_ptr(), wf.data_ptr(), L_, k, E, out.data_ptr(), st)
+        return out
+
+    def _aufgeteilt(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """The same layer with the inputs quantised by launches of their own (five launches when gate
+        and up share a layout, else the per-tensor path)."""
         L_, E = x.shape
         k = idx.shape[1]
         if not self._fused():
@@ -131,11 +174,7 @@ class Experten:
         e = eingang_bf16(x)
         flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
         gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
-        if self.gate.adressen is None:
-            wa, wb, per = self.gate.raw, self.up.raw, self.gate.raw.shape[1]
-        else:
-            wa = self.gate.adressen.to(dev, torch.int64).contiguous()
-            wb, per = self.up.adressen.to(dev, torch.int64).contiguous(), -1
+        (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
         _starten("mv_experts2", L.nmq_mv_experts2, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
                  flat.data_ptr(), n, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k,
                  gu.data_ptr(), FF, E, st)
@@ -143,10 +182,7 @@ class Experten:
         _starten("silu_mul_quant", L.nmq_silu_mul_quant, gu.data_ptr(), gu[n:].data_ptr(), a.xq.data_ptr(),
                  a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), n * FF, st)
         y = torch.empty(n, E, dtype=torch.float32, device=dev)
-        if self.down.adressen is None:
-            wd, perd = self.down.raw, self.down.raw.shape[1]
-        else:
-            wd, perd = self.down.adressen.to(dev, torch.int64).contiguous(), -1
+        wd, perd = self.down._quelle(dev)
         _starten("mv_experts", L.nmq_mv_experts, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), n, perd,
                  a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), 1, y.data_ptr(), E, FF, st)
         out = torch.empty(L_, E, dtype=torch.float32, device=dev)

@@ -127,6 +127,42 @@ def _eingang(x: torch.Tensor) -> Eingang:
     return e
 
 
+# Longest input a one-token launch quantises itself (measured on MI355X: past this, staging the values
+# in every workgroup costs more than one quantisation launch).
+WERTE_BIS = 8192
+
+
+def _werte(x: torch.Tensor, n_in: int, bf16: bool):
+    """(values tensor, x_mode) for a launch that quantises one token's input itself, or None where the
+    quantisation launch is used (long rows, views that are not 16-byte aligned).  fp32 stays fp32
+    (bf16: rounded to bf16 in the launch, the cudakern convention), other types go to bf16 first as
+    in Eingang."""
+    if n_in > WERTE_BIS or x.numel() % n_in or not x.is_contiguous():
+        return None
+    if x.dtype == torch.float32:
+        t, mode = x, (_native.X_F32_BF16 if bf16 else _native.X_F32)
+    else:
+        t, mode = (x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16).contiguous()), _native.X_BF16
+    if t.data_ptr() % 16:
+        return None
+    return t, mode
+
+
+def _mv_werte(fmt: str, raws, t: torch.Tensor, mode: int, n_outs, n_in: int) -> list:
+    """One launch (per MAX_MATRIZEN matrices) on one token given as values -> [(n_out,) float32]."""
+    dev = raws[0].device
+    ys = [torch.empty(n, dtype=torch.float32, device=dev) for n in n_outs]
+    L = _native.lib()
+    for a in range(0, len(raws), MAX_MATRIZEN):
+        part = range(a, min(a + MAX_MATRIZEN, len(raws)))
+        k = len(part)
+        _starten("mv", L.nmq_mv_x, TYPE_ID[fmt], k, (ctypes.c_void_p * k)(*[raws[i].data_ptr() for i in part]),
+                 (ctypes.c_int * k)(*[int(n_outs[i]) for i in part]),
+                 (ctypes.c_void_p * k)(*[ys[i].data_ptr() for i in part]), t.data_ptr(), mode, None, n_in,
+                 _native.stream_ptr(dev))
+    return ys
+
+
 def _mv(fmt: str, raw: torch.Tensor, e: Eingang, n_out: int, n_in: int) -> torch.Tensor:
     if e.n % n_in:
         raise ValueError(f"mv: input of {e.n} values is not a multiple of n_in={n_in}")
@@ -143,6 +179,11 @@ def mv(fmt: str, raw: torch.Tensor, x, n_out: int, n_in: int) -> torch.Tensor:
     Eingang of M rows -> (M, n_out) float32, or (n_out,) for a vector (reference mmvq.py:852-865)."""
     if fmt not in FORMATE:
         raise ValueError(f"mmvq.mv: format {fmt} (this module serves {tuple(FORMATE)})")
+    if not isinstance(x, Eingang) and x.numel() == n_in:
+        w = _werte(x.reshape(-1), n_in, bf16=False)
+        if w is not None:   # one token: the launch quantises it (no separate quantisation launch)
+            y = _mv_werte(fmt, [raw], w[0], w[1], [n_out], n_in)[0]
+            return y if x.dim() == 1 else y.view(1, n_out)
     e = x if isinstance(x, Eingang) else _eingang(x)
     y = _mv(fmt, raw, e, n_out, n_in)
     vektor = y.shape[0] == 1 if isinstance(x, Eingang) else x.dim() == 1
@@ -161,6 +202,12 @@ def mv_mehrere(fmt: str, raws, x, n_outs, n_in: int) -> list:
         raise ValueError(f"mmvq.mv_mehrere: format {fmt} (this module serves {tuple(FORMATE)})")
     if len(raws) != len(n_outs) or not raws:
         raise ValueError("mv_mehrere: one n_out per matrix")
+    if not isinstance(x, Eingang):
+        if x.numel() != n_in:
+            raise ValueError(f"mv_mehrere: one token of {n_in} values expected, the input holds {x.numel()}")
+        w = _werte(x.reshape(-1), n_in, bf16=False)
+        if w is not None:
+            return _mv_werte(fmt, raws, w[0], w[1], n_outs, n_in)
     e = x if isinstance(x, Eingang) else _eingang(x.reshape(-1))
     if e.n != n_in:
         raise ValueError(f"mv_mehrere: one token of {n_in} values expected, the input holds {e.n}")

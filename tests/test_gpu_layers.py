@@ -309,3 +309,23 @@ def test_moe_combine(nmq):
     torch.cuda.synchronize()
     ref = (y.astype(np.float64).reshape(L, k, E) * w.astype(np.float64)[:, :, None]).sum(1)
     assert np.max(np.abs(out.cpu().numpy() - ref)) <= 1e-5 * np.max(np.abs(ref))
+
+
+@pytest.mark.parametrize("L", [1, 4])
+def test_expert_layer_three_launches_equal_five(nmq, L):
+    """Experten: the three-launch layer (inputs quantised inside the gathered launches) equals, bit for
+    bit, the layer with its two input quantisations as launches of their own."""
+    from ggufengine_amd import experts
+    n_exp, k, E, FF = 16, 8, 2048, 768
+    gate = experts.PackedExperts(dev(random_blocks("Q4_K", n_exp * FF * E // 256, seed=131)), 12, n_exp, FF, E)
+    up = experts.PackedExperts(dev(random_blocks("Q4_K", n_exp * FF * E // 256, seed=132)), 12, n_exp, FF, E)
+    down = experts.PackedExperts(dev(random_blocks("Q6_K", n_exp * E * FF // 256, seed=133)), 14, n_exp, E, FF)
+    layer = experts.Experten(gate, up, down)
+    rng = np.random.default_rng(134 + L)
+    x = dev(rng.standard_normal((L, E)).astype(np.float32))
+    idx, w = experts.auswahl(dev(rng.standard_normal((L, n_exp)).astype(np.float32)), k)
+    say("expert layer 3 vs 5 launches", L)
+    a = layer(x, idx, w)
+    b = layer._aufgeteilt(x, idx, w)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)

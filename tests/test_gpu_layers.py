@@ -329,3 +329,40 @@ def test_expert_layer_three_launches_equal_five(nmq, L):
     b = layer._aufgeteilt(x, idx, w)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def test_llama3_8b_layer_full_size(nmq, oracle):
+    """The mat-vecs of a full Llama-3-8B decoder layer at batch 1 (q, k, v, o, gate, up Q4_K; down Q6_K
+    4096x14336), weights ~N(0, 0.02) quantised by the library's encoders, run as the layer runs them
+    (q/k/v and gate/up each in one launch on the fp32 input, o on its own, down through an Eingang):
+    every output within the parity bar of the oracle (dequantise + fp64 matmul) and within 2e-5 of the
+    oracle's integer decomposition."""
+    import os
+    from ggufengine_amd import encode, mmvq
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    spec = {"q": ("Q4_K", 4096, 4096, 21), "k": ("Q4_K", 1024, 4096, 22), "v": ("Q4_K", 1024, 4096, 23),
+            "o": ("Q4_K", 4096, 4096, 24), "gate": ("Q4_K", 14336, 4096, 25), "up": ("Q4_K", 14336, 4096, 26),
+            "down": ("Q6_K", 4096, 14336, 27)}
+    raw = {}
+    for n, (f, r, c, sd) in spec.items():
+        w = np.random.Generator(np.random.PCG64(sd)).standard_normal(r * c, dtype=np.float32) * np.float32(0.02)
+        raw[n] = encode.encode(f, w, threads=threads)
+    xs = {n: np.random.Generator(np.random.PCG64(sd)).standard_normal(c, dtype=np.float32)
+          for n, (c, sd) in {"x_attn": (4096, 28), "attn_out": (4096, 30), "x_ffn": (4096, 31), "act": (14336, 29)}.items()}
+    wd = {n: dev(r) for n, r in raw.items()}
+    xd = {n: dev(x) for n, x in xs.items()}
+    say("llama3-8b layer")
+    y = dict(zip(("q", "k", "v"), mmvq.mv_mehrere("Q4_K", [wd["q"], wd["k"], wd["v"]], xd["x_attn"],
+                                                  [4096, 1024, 1024], 4096)))
+    y["o"] = mmvq.mv("Q4_K", wd["o"], xd["attn_out"], 4096, 4096)
+    y.update(zip(("gate", "up"), mmvq.mv_mehrere("Q4_K", [wd["gate"], wd["up"]], xd["x_ffn"], [14336, 14336], 4096)))
+    y["down"] = mmvq.mv("Q6_K", wd["down"], xd["act"], 4096, 14336)
+    torch.cuda.synchronize()
+    inp = {"q": "x_attn", "k": "x_attn", "v": "x_attn", "o": "attn_out", "gate": "x_ffn", "up": "x_ffn", "down": "act"}
+    for n, (f, r, c, _) in spec.items():
+        x = xs[inp[n]][None]
+        got = y[n].cpu().numpy()[None]
+        err = oracle.rel_err_rows(got, oracle.mv_deq(f, raw[n], r, c, x)).max()
+        assert err <= 1e-3, (n, err)
+        err_i = oracle.rel_err_rows(got, oracle.mv_int(f, raw[n], r, c, *oracle.quant_q8(x))).max()
+        assert err_i <= 2e-5, (n, err_i)

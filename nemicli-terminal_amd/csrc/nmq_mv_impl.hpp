@@ -349,7 +349,9 @@ __device__ __forceinline__ void stagev_store(const VRound& r, int rnd, u8* lds, 
 // and the stores wait only for the older input reads.  Several rounds: everything is staged before
 // the weight reads, so that no input read can still be pending where the two paths meet (a pending
 // read there makes the compiler wait for every outstanding read, the weights included).
-template <int F, bool EXT, typename Issue>
+// MAXR: rounds of the two-stage input a thread may hold in registers while the weight reads go out
+// (longer inputs are staged completely before them).
+template <int F, bool EXT, int MAXR, typename Issue>
 __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
     using FM = Fmt<F>;
     const int nt = p.nt;
@@ -389,15 +391,19 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
     const float* xd = p.xd + xrow * (p.n_in / 32);
     const float* xs = p.xs + xrow * (p.n_in / 32);
     const int rounds = (p.ktp / 16 + nt - 1) / nt;
-    if (rounds == 1) {
-        XRound r;
-        stage1_load(r, 0, xq, xq2, xd, xs, p.n_in, nt);
+    if (rounds <= MAXR) {
+        XRound r[MAXR];
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k)
+            if (k < rounds) stage1_load(r[k], k, xq, xq2, xd, xs, p.n_in, nt);
         const u64 gv = tab_load<F>();
         __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
         issue();
         __builtin_amdgcn_sched_barrier(0);
         tab_store<F>(tab, gv, nt);
-        stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp, nt);
+#pragma unroll
+        for (int k = 0; k < MAXR; ++k)
+            if (k < rounds) stage1_store<FM::STRIDED>(r[k], k, lds, p.n_in, p.ktp, nt);
     } else {
         for (int k = 0; k < rounds; ++k) {
             XRound r;
@@ -657,7 +663,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     Mv1Step<F, T, RW, NITM> buf[NBUF];
     const int stride = nw * SR;
     int base = gw * SR;
-    stage1_around<F, EXT>(lds, tab, p, xrow, [&] {
+    stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] {
 #pragma unroll
         for (int i = 0; i < NBUF - 1; ++i)
             buf[i].load(rm, base + i * stride + off, lt, U, base + off);
@@ -772,7 +778,7 @@ __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
     const int stride = gridDim.x * W * RW;
     int base = (blockIdx.x * W + wave) * RW;
     Mv1Step<F, 64, RW, NIT> a;
-    stage1_around<F, EXT>(lds, tab, p, xrow, [&] { a.load(rm, base, lane, U, base); });
+    stage1_around<F, EXT, 4>(lds, tab, p, xrow, [&] { a.load(rm, base, lane, U, base); });
     const LaneConst lc = lane_const<F, 64, NIT>(lane);
     if constexpr (!PIPE) {
         // the launch gives every wave at most one row group (grid x W >= groups)
@@ -814,7 +820,7 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
     const int U = (p.n_in + 63) >> 6;
     const int r0 = ((blockIdx.x * W + wave) * P + team) * RW;
     Mv1Step<F, T, RW, 1> a;
-    stage1_around<F, EXT>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
+    stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
     const LaneConst lc = lane_const<F, T, 1>(lt);

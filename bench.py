@@ -239,8 +239,53 @@ def run_configs(which, steps, warmup):
                 _record("lowbit", f"{fmt} {rows}x4096 batch 1", fmt, us, alg_bytes(fmt, rows, 4096), err)
                 del ws
 
+    if which in ("prefill", "all"):
+        run_prefill(L, stream, steps, warmup)
+
     if which in ("moe", "all"):
         run_moe(steps, warmup, threads)
+
+
+def run_prefill(L, stream, steps, warmup):
+    """Several tokens per call (the reference's mmvq.mm range, 17..112, and 16): the fp16 matrix-core
+    path (nmq_mm_input + nmq_mm) against the int8 mat-vec path (nmq_mv in launches of 16) on the Llama
+    matrices, W ~N(0,0.02) (seeds 31, 32, 27), x ~N(0,1) (seed 34).  `us` is nmq_mm alone,
+    `us_with_input` adds the input launch; algorithmic bytes as for nmq_mv (weights once, fp32 x read
+    once, y written)."""
+    import torch
+    import oracle
+    from ggufengine_amd import _native
+    for fmt, rows, n_in, seed in (("Q4_K", 14336, 4096, 31), ("Q4_K", 4096, 4096, 32), ("Q6_K", 4096, 14336, 27)):
+        raw = make_weights(fmt, rows, n_in, seed)
+        ws = _copies(torch.from_numpy(raw).cuda())
+        X = _x(34, (112, n_in))
+        for n in (16, 64, 112):
+            xd = torch.from_numpy(X[:n]).cuda()
+            pad = (n + 15) // 16 * 16
+            xh = torch.empty(pad, n_in, dtype=torch.float16, device="cuda")
+            xl = torch.empty_like(xh)
+            xsum = torch.empty(pad, n_in // 32, dtype=torch.float32, device="cuda")
+            xs = torch.empty(n, dtype=torch.float32, device="cuda")
+            y = torch.empty(n, rows, dtype=torch.float32, device="cuda")
+
+            def prep(i):
+                _native.check(L.nmq_mm_input(xd.data_ptr(), 1, xh.data_ptr(), xl.data_ptr(), xsum.data_ptr(),
+                                             xs.data_ptr(), n_in, n, stream))
+
+            def go(i):
+                _native.check(L.nmq_mm(TYPE[fmt], ws[i % len(ws)].data_ptr(), xh.data_ptr(), xl.data_ptr(),
+                                       xsum.data_ptr(), xs.data_ptr(), y.data_ptr(), rows, n_in, n, stream))
+            prep(0)
+            us = _events_us(go, steps, warmup)
+            us_in = _events_us(prep, steps, warmup)
+            go(0)
+            torch.cuda.synchronize()
+            err = float(oracle.rel_err_rows(y.cpu().numpy(), oracle.mv_deq(fmt, raw, rows, n_in, X[:n])).max())
+            us_int8, _ = _mv_case(L, stream, fmt, ws, raw, rows, n_in, X[:n], steps, warmup)
+            ab = weight_bytes(fmt, rows, n_in) + n * (4 * n_in + 4 * rows)
+            _record("prefill", f"{fmt} {rows}x{n_in} n={n}", fmt, us, ab, err, us_with_input=round(us + us_in, 3),
+                    us_int8_path=round(us_int8, 3), tokens_per_s=round(n / ((us + us_in) * 1e-6)))
+        del ws
 
 
 def run_moe(steps, warmup, threads):
@@ -334,9 +379,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
     ap.add_argument("--config", default="headline",
-                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "moe", "all"),
+                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "all"),
                     help="headline (default): the metric line; the others print one record per case of "
-                         "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, MoE)")
+                         "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, "
+                         "16..112 tokens on the fp16 matrix cores, MoE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the mat-vec path is single-GPU "

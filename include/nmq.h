@@ -113,6 +113,38 @@ int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, i
 int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs,
            float* y, int n_out, int n_in, int ncols, void* stream);
 
+/*
+ * Two-stage fp16 input of nmq_mm for ncols token rows of n_in values (x: fp32 if x_is_f32 else bf16,
+ * rows back to back): per row xs = 2^(e - 8) where max|x| = f * 2^e, f in [0.5, 1) (e >= -100),
+ * v = x / xs (exact), xh = fp16(v), xl = fp16(v - xh), rounded to nearest even (xh + xl is v to
+ * about 2^-22), and per 32 values the fp32 sum of xh + xl.  xs: ncols fp32.  xh, xl: ceil(ncols/16)*16
+ * rows of n_in fp16 each (16-byte aligned), xsum: ceil(ncols/16)*16 rows of n_in/32 fp32, in the
+ * matrix cores' operand order:
+ *   xh, xl: value k of token t at ((t/16 * (n_in/32) + k/32) * 64 + (k%32)/8 * 16 + t%16) * 8 + k%8
+ *   xsum:   sub-block s of token t at (t/16 * (n_in/32) + s) * 16 + t%16
+ * (the rows past ncols are written as zeros; the sign of a zero in xh, xl is not specified).
+ * n_in % 32 == 0, n_in <= 1<<20.
+ * Replaces the mmq_eingang launch of mmvq._mmq_eingang (mmvq.py:617-641, 882-899), which keeps one
+ * fp16 stage scaled by max|x| / 256.
+ */
+int nmq_mm_input(const void* x, int x_is_f32, uint16_t* xh, uint16_t* xl, float* xsum, float* xs, int n_in,
+                 int ncols, void* stream);
+
+/*
+ * Several tokens on the fp16 matrix cores (Q4_K and Q6_K; other formats NMQ_ERR_FORMAT):
+ *   y[c][r] = xs[c] * sum_k w[r][k] * (xh + xl)[c][k]
+ * with w the exact dequantised weights: per 256-value block, d times the integer products q*sc
+ * (Q4_K; Q6_K as (8h + l)*sc with q - 32 = 8h + l, every part exact in fp16) summed with the input on
+ * the matrix cores (exact products, fp32 sums), minus dmin * sum_s mn_s * xsum_s (Q4_K, an fp32
+ * matrix product).  xh, xl, xsum, xs from nmq_mm_input for the same ncols and n_in.  Up to 64 tokens
+ * per launch; larger ncols loop.  y: fp32, token-major (ncols x n_out).
+ * Replaces the mmq_<fmt>_<nt> launches of mmvq.mm (mmvq.py:536-724, 902-920), which round the
+ * weights and the input to fp16; y written directly instead of split-K atomic adds into zeros.
+ * n_in % 256 == 0, 1 <= n_out, n_in <= 1<<20; w 16-byte aligned for Q4_K.
+ */
+int nmq_mm(int fmt, const void* w, const uint16_t* xh, const uint16_t* xl, const float* xsum, const float* xs,
+           float* y, int n_out, int n_in, int ncols, void* stream);
+
 /* Most matrices one nmq_mv_multi call takes. */
 #define NMQ_MAX_MATS 4
 

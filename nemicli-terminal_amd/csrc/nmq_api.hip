@@ -182,6 +182,132 @@ __global__ __launch_bounds__(256) void akt_q8_kernel(const float* __restrict__ g
     quant32_store(v, i, xq, xq2, xd, xs);
 }
 
+// ---- two-stage fp16 input of the several-token matrix-core kernels (reference mmvq.py:617-641) ---
+// One workgroup of 1024 threads per token row: m = max|x| over the row, xs = 2^(e - 8) for m = f 2^e
+// (f in [0.5, 1); e >= -100, m == 0 gives e = 0), v = x / xs (exact: a power of two), xh = fp16(v)
+// and xl = fp16(v - xh), both rounded to nearest even (v - xh is exact in fp32).  |xh| <= 256 and
+// xh + xl is v to about 2^-22 relative.  x: fp32 (F32 = 1) or bf16; 8 values per thread and round.
+// xh and xl are written in the matrix cores' operand order (mmh_kernel reads one contiguous 1 KB
+// fragment per 16 tokens and 32 values): value k of token t at
+//   ((t / 16 * (n / 32) + k / 32) * 64 + (k % 32) / 8 * 16 + t % 16) * 8 + k % 8,
+// and xsum[(t / 16 * (n / 32) + k / 32) * 16 + t % 16] = the sum of xh + xl over the 32 values of
+// sub-block k / 32: each thread adds its 8 values in order (fp32), then the 4 threads of the
+// sub-block add pairwise (xor 1, then xor 2).  Rows past ncols up to the next multiple of 16
+// (blockIdx.x >= ncols) are written as zeros.
+template <int F32>
+__device__ __forceinline__ void load8(const void* x, int64_t i, float (&v)[8]) {
+    if constexpr (F32) {
+        const u32x4 a = *gp<u32x4>((const float*)x + i), b = *gp<u32x4>((const float*)x + i + 4);
+        const u32 w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = __uint_as_float(w[j]);
+    } else {
+        const u32x4 a = *gp<u32x4>((const u16*)x + i);
+        const u32 w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[2 * j] = __uint_as_float(w[j] << 16);
+            v[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+        }
+    }
+}
+
+// 8 values of the row (fp32 / bf16 input) at v: xh, xl in operand order, their sub-block sum.
+__device__ __forceinline__ void mm_input_store(const float (&v)[8], float inv, int i, int t, int64_t gbase,
+                                               int tid, u16* __restrict__ xh, u16* __restrict__ xl,
+                                               float* __restrict__ xsum) {
+    u32 hi[4], lo[4];
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        u32 h2b = 0, l2b = 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float a = v[2 * j + k] * inv;
+            const _Float16 h = (_Float16)a;
+            const _Float16 l = (_Float16)(a - (float)h);
+            sum += (float)h + (float)l;
+            h2b |= (u32)__builtin_bit_cast(u16, h) << (16 * k);
+            l2b |= (u32)__builtin_bit_cast(u16, l) << (16 * k);
+        }
+        hi[j] = h2b;
+        lo[j] = l2b;
+    }
+    // the 4 threads of a sub-block are 4 consecutive lanes (all active: n % 32 == 0)
+    sum += __shfl_xor(sum, 1);
+    sum += __shfl_xor(sum, 2);
+    const int64_t o = ((gbase + (i >> 5)) * 64 + ((i & 31) >> 3) * 16 + (t & 15)) * 8;
+    *gpw<u32x4>(xh + o) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    *gpw<u32x4>(xl + o) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    if ((tid & 3) == 0) gpw<float>(xsum)[(gbase + (i >> 5)) * 16 + (t & 15)] = sum;
+}
+
+// 1024 threads per row; NR > 0: rows of at most 8192 NR values, read once and held in registers
+// across the reduction; NR = 0: longer rows, read twice.
+template <int F32, int NR>
+__global__ __launch_bounds__(1024) void mm_input_kernel(const void* __restrict__ x, u16* __restrict__ xh,
+                                                        u16* __restrict__ xl, float* __restrict__ xsum,
+                                                        float* __restrict__ xs, int n, int ncols) {
+    asm volatile("" ::"s"(x), "s"(xh), "s"(xl), "s"(xsum), "s"(xs), "s"(n), "s"(ncols));
+    __shared__ float part[16];
+    const int t = blockIdx.x;
+    const bool real = t < ncols;  // workgroup-uniform
+    const int64_t row = (int64_t)t * n;
+    const int tid = threadIdx.x;
+    constexpr int R = NR > 0 ? NR : 1;
+    float v[R][8];
+    float m = 0.f;
+    if constexpr (NR > 0) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = 8 * tid + 8192 * r;
+            if (real && i < n) {
+                load8<F32>(x, row + i, v[r]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[r][j] = 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[r][j]));
+        }
+    } else if (real) {
+        for (int i = 8 * tid; i < n; i += 8192) {
+            load8<F32>(x, row + i, v[0]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[0][j]));
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) part[tid >> 6] = m;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) m = fmaxf(m, part[k]);
+    int e = 0;
+    frexpf(m, &e);
+    if (e < -100) e = -100;
+    const float inv = ldexpf(1.0f, 8 - e);
+    if (real && tid == 0) xs[t] = ldexpf(1.0f, e - 8);
+    const int64_t gbase = (int64_t)(t >> 4) * (n >> 5);  // first step of this token's group
+    if constexpr (NR > 0) {
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const int i = 8 * tid + 8192 * r;
+            if (i < n) mm_input_store(v[r], inv, i, t, gbase, tid, xh, xl, xsum);
+        }
+    } else {
+        for (int i = 8 * tid; i < n; i += 8192) {
+            if (real) {
+                load8<F32>(x, row + i, v[0]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) v[0][j] = 0.f;
+            }
+            mm_input_store(v[0], inv, i, t, gbase, tid, xh, xl, xsum);
+        }
+    }
+}
+
 // ---- weighted combine of expert outputs (reference models/moe.py:275-277, 319-320) --------------
 // out[t][e] = sum_j w[t*k + j] * y[t*k + j][e], j = 0..k-1 in this order (a fixed order).
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ y, const float* __restrict__ w,
@@ -324,6 +450,11 @@ extern template int launch_mv<NMQ_Q4_K>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_Q6_K>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_IQ2_XXS>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_TQ2_0>(MvParams, int, int, hipStream_t);
+
+template <int F>
+int launch_mmh(MmhParams p, hipStream_t stream);
+extern template int launch_mmh<NMQ_Q4_K>(MmhParams, hipStream_t);
+extern template int launch_mmh<NMQ_Q6_K>(MmhParams, hipStream_t);
 
 static int launch_any(int fmt, const MvParams& p, int nc, int n_mats, hipStream_t s) {
     switch (fmt) {
@@ -529,6 +660,48 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
         p.n_in = n_in;
         p.x_group = 1;
         e = launch_any(fmt, p, nc, 1, (hipStream_t)stream);
+        if (e) return e;
+    }
+    return NMQ_OK;
+}
+
+int nmq_mm_input(const void* x, int x_is_f32, uint16_t* xh, uint16_t* xl, float* xsum, float* xs, int n_in,
+                 int ncols, void* stream) {
+    if (!x || !xh || !xl || !xsum || !xs || x_is_f32 < 0 || x_is_f32 > 1) return NMQ_ERR_ARG;
+    if (!aligned(x, 16) || !aligned(xh, 16) || !aligned(xl, 16) || !aligned(xsum, 4) || !aligned(xs, 4))
+        return NMQ_ERR_ARG;
+    if (n_in < 32 || n_in % 32 || n_in > (1 << 20) || ncols < 1) return NMQ_ERR_SHAPE;
+    const dim3 g((unsigned)((ncols + 15) / 16 * 16)), b(1024);
+    const hipStream_t s = (hipStream_t)stream;
+    const int nr = n_in <= 8192 ? 1 : n_in <= 16384 ? 2 : 0;
+    void (*k)(const void*, u16*, u16*, float*, float*, int, int) =
+        x_is_f32 ? (nr == 1 ? mm_input_kernel<1, 1> : nr == 2 ? mm_input_kernel<1, 2> : mm_input_kernel<1, 0>)
+                 : (nr == 1 ? mm_input_kernel<0, 1> : nr == 2 ? mm_input_kernel<0, 2> : mm_input_kernel<0, 0>);
+    hipLaunchKernelGGL(k, g, b, 0, s, x, (u16*)xh, (u16*)xl, xsum, xs, n_in, ncols);
+    return (int)hipGetLastError();
+}
+
+int nmq_mm(int fmt, const void* w, const uint16_t* xh, const uint16_t* xl, const float* xsum, const float* xs,
+           float* y, int n_out, int n_in, int ncols, void* stream) {
+    if (fmt != NMQ_Q4_K && fmt != NMQ_Q6_K) return NMQ_ERR_FORMAT;
+    int e = check_w(fmt, w, y, n_out, n_in);
+    if (e) return e;
+    if (!xh || !xl || !xsum || !xs || !aligned(xh, 16) || !aligned(xl, 16) || !aligned(xsum, 4) || !aligned(xs, 4))
+        return NMQ_ERR_ARG;
+    if (ncols < 1) return NMQ_ERR_ARG;
+    for (int c0 = 0; c0 < ncols; c0 += MMH_MAX_COLS) {
+        MmhParams p{};
+        p.w = (const u8*)w;
+        p.xh = (const u16*)xh + (int64_t)c0 * n_in;
+        p.xl = (const u16*)xl + (int64_t)c0 * n_in;
+        p.xsum = xsum + (int64_t)c0 * (n_in / 32);
+        p.xs = xs + c0;
+        p.y = y + (int64_t)c0 * n_out;
+        p.n_out = n_out;
+        p.n_in = n_in;
+        p.nc = ncols - c0 < MMH_MAX_COLS ? ncols - c0 : MMH_MAX_COLS;
+        e = fmt == NMQ_Q4_K ? launch_mmh<NMQ_Q4_K>(p, (hipStream_t)stream)
+                            : launch_mmh<NMQ_Q6_K>(p, (hipStream_t)stream);
         if (e) return e;
     }
     return NMQ_OK;

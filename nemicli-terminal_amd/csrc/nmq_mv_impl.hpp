@@ -958,6 +958,7 @@ inline int env_int(const char* name, int dflt) {
 
 }  // namespace nmq
 #include "nmq_mfma.hpp"
+#include "nmq_mmh.hpp"
 namespace nmq {
 
 struct Mv1Shape {

@@ -41,6 +41,8 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_device_arch.argtypes, L.nmq_device_arch.restype = [ctypes.c_char_p, i], i
     L.nmq_quant_q8.argtypes, L.nmq_quant_q8.restype = [p, i, p, p, p, p, i64, p], i
     L.nmq_mv.argtypes, L.nmq_mv.restype = [i, p, p, p, p, p, p, i, i, i, p], i
+    L.nmq_mm_input.argtypes, L.nmq_mm_input.restype = [p, i, p, p, p, p, i, i, p], i
+    L.nmq_mm.argtypes, L.nmq_mm.restype = [i, p, p, p, p, p, p, i, i, i, p], i
     L.nmq_mv_experts.argtypes = [i, p, p, i, i64, p, p, p, p, i, p, i, i, p]
     L.nmq_mv_experts.restype = i
     L.nmq_mv_experts2.argtypes = [i, p, p, p, i, i64, p, p, p, p, i, p, i, i, p]

@@ -12,9 +12,11 @@ gfx950 device, and calls raise.
 
 Differences from the reference (documented, same results within the parity tolerance):
   - up to 16 tokens per launch on the int8 matrix cores, SPALTEN = 8 on the dot4 kernels (the
-    reference compiles 1..9 per launch);
-  - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs the same int8
-    kernels in groups of 16 tokens, on the two-stage input (more precise than fp16);
+    reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for Q4_K and 2
+    for Q6_K, measured on MI355X (the reference: 16);
+  - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs on the fp16 matrix
+    cores with exact integer weights and a two-stage fp16 input (about 22 bits against the
+    reference's fp16 weights and input), 64 tokens per launch;
   - of the fused one-token steps, norm_q8 and akt_q8 are provided; rope_kv and attention1 are not,
     so `schritt_moeglich` returns False and callers take their unfused layer path
     (models/baukasten.py:205).
@@ -36,7 +38,10 @@ WARPS = 4                     # waves per workgroup (at most; fewer for short ma
 SPALTEN = _native.MAX_COLS    # tokens (input rows) per launch, weights read once for all of them
 # weight rows per team of lanes by token count (the kernels are compiled for these)
 ZEILEN_JE_WARP = {"Q4_K": lambda nc: 1 if nc == 1 else 2, "Q6_K": lambda nc: 1 if nc == 1 else 2}
-MMVQ_BIS = {"Q4_K": 16, "Q6_K": 16}
+# Most tokens per call for the int8 mat-vec kernels; from one more token on, callers take `mm` (the fp16
+# matrix cores).  Measured on MI355X (14336x4096, 4096x4096 Q4_K and 4096x14336 Q6_K): the reference's
+# 16 / 16 (mmvq.py:32) become 8 / 2 here.
+MMVQ_BIS = {"Q4_K": 8, "Q6_K": 2}
 MMQ_BIS = {"Q4_K": 112, "Q6_K": 112}
 
 
@@ -225,13 +230,45 @@ def mv_mehrere(fmt: str, raws, x, n_outs, n_in: int) -> list:
     return ys
 
 
+def _mmq_eingang(x2: torch.Tensor) -> tuple:
+    """(xh, xl float16, xsum, xs float32) for x2 (M, n): the two-stage fp16 input of `mm` in one launch
+    (reference mmvq.py:882-899); inside eingang_teilen() built once per input."""
+    geteilt = getattr(_TEILEN, "werte", None)
+    key = ("mm", x2.data_ptr(), tuple(x2.shape), x2.dtype)
+    if geteilt is not None and key in geteilt:
+        return geteilt[key]
+    if x2.dtype not in (torch.float32, torch.bfloat16):
+        x2 = x2.to(torch.bfloat16)
+    x2 = x2.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    M, n = x2.shape
+    # in the matrix cores' operand order, rows padded to a multiple of 16 (include/nmq.h)
+    xh = torch.empty((M + 15) // 16 * 16, n, dtype=torch.float16, device=x2.device)
+    xl = torch.empty_like(xh)
+    xsum = torch.empty(xh.shape[0], n // 32, dtype=torch.float32, device=x2.device)
+    xs = torch.empty(M, dtype=torch.float32, device=x2.device)
+    _starten("mmq_eingang", _native.lib().nmq_mm_input, x2.data_ptr(), int(x2.dtype == torch.float32),
+             xh.data_ptr(), xl.data_ptr(), xsum.data_ptr(), xs.data_ptr(), n, M, _native.stream_ptr(x2.device))
+    if geteilt is not None:
+        geteilt[key] = (xh, xl, xsum, xs)
+    return xh, xl, xsum, xs
+
+
 def mm(fmt: str, raw: torch.Tensor, x: torch.Tensor, n_out: int, n_in: int) -> torch.Tensor:
-    """Several tokens: x (M, n_in) -> (M, n_out) float32 (reference mmvq.py:902-920).  Runs the int8
-    mat-vec kernels in groups of SPALTEN tokens."""
+    """Several tokens on the matrix cores: x (M, n_in) bf16/float32 -> (M, n_out) float32 (reference
+    mmvq.py:902-920).  The weights are unpacked once per launch of up to 64 tokens as exact fp16
+    integer products, the input goes in as two fp16 stages (about 22 bits), d and the min term are
+    applied in fp32 per block."""
     if fmt not in FORMATE:
         raise ValueError(f"mmvq.mm: format {fmt}")
     x2 = x.reshape(-1, n_in)
-    return _mv(fmt, raw, _eingang(x2), n_out, n_in)
+    xh, xl, xsum, xs = _mmq_eingang(x2)
+    M = x2.shape[0]
+    y = torch.empty(M, n_out, dtype=torch.float32, device=raw.device)
+    _starten("mmq", _native.lib().nmq_mm, TYPE_ID[fmt], raw.data_ptr(), xh.data_ptr(), xl.data_ptr(),
+             xsum.data_ptr(), xs.data_ptr(), y.data_ptr(), n_out, n_in, M, _native.stream_ptr(raw.device))
+    return y
 
 
 def entpacken(fmt: str, raw: torch.Tensor, n_out: int, n_in: int) -> torch.Tensor:

@@ -161,6 +161,33 @@ def mv_deq(fmt, raw, n_out, n_in, x) -> np.ndarray:
     return y
 
 
+def mm_input(x: np.ndarray):
+    """Two-stage fp16 input of the several-token path, per token row (the per-token scaling of
+    mmvq.py:617-641 with a power-of-two scale and a second stage): xs = 2^(e - 8) for
+    max|x| = f 2^e (f in [0.5, 1), e >= -100), v = x / xs, xh = fp16(v), xl = fp16(v - xh), both
+    rounded to nearest even, and per 32 values the fp32 sum of xh + xl (each run of 8 added in order,
+    then the 4 runs pairwise) -> (xh, xl float16 (M, n), xsum float32 (M, n/32), xs float32 (M,))."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    x = x.reshape(-1, x.shape[-1])
+    m = np.abs(x).max(axis=1).astype(np.float64)
+    _, e = np.frexp(m)
+    e = np.maximum(e, -100)
+    v = (x.astype(np.float64) * np.ldexp(1.0, 8 - e)[:, None]).astype(np.float32)   # exact
+    xh = v.astype(np.float16)
+    xl = (v - xh.astype(np.float32)).astype(np.float16)                              # v - xh exact
+    w = (xh.astype(np.float32) + xl.astype(np.float32)).reshape(x.shape[0], -1, 4, 8)
+    run = w[..., 0]
+    for j in range(1, 8):
+        run = run + w[..., j]                                                         # float32 adds
+    xsum = (run[..., 0] + run[..., 1]) + (run[..., 2] + run[..., 3])
+    return xh, xl, xsum.astype(np.float32), np.ldexp(1.0, e - 8).astype(np.float32)
+
+
+def mm_x(x: np.ndarray) -> np.ndarray:
+    """The input the several-token path multiplies with: xs * (xh + xl) in float64 (M, n)."""
+    xh, xl, _, xs = mm_input(x)
+    return (xh.astype(np.float64) + xl.astype(np.float64)) * xs.astype(np.float64)[:, None]
+
 def gemv_f32(w: np.ndarray, x: np.ndarray, threads: int) -> np.ndarray:
     """CPU baseline GEMV (F.linear of the Linear path, models/common.py:526-527)."""
     w = np.ascontiguousarray(w, dtype=np.float32)

@@ -373,29 +373,33 @@ int or_mv_int(int fmt, const uint8_t* raw, int n_out, int n_in, const int8_t* xq
     const int nb = n_in / bv;
     int8_t w[256];
     double ws[16], wm[8];
-    for (int r = 0; r < n_out; ++r) {
-        double acc[64];
-        for (int c = 0; c < ncols && c < 64; ++c) acc[c] = 0.0;
-        for (int blk = 0; blk < nb; ++blk) {
-            decode_int(fmt, raw + ((int64_t)r * nb + blk) * bb, w, ws, wm);
-            for (int c = 0; c < ncols && c < 64; ++c) {
-                const int8_t* q1 = xq + (int64_t)c * n_in + blk * bv;
-                const int8_t* q2 = xq2 + (int64_t)c * n_in + blk * bv;
-                const float* d = xd + ((int64_t)c * n_in + blk * bv) / 32;
-                const float* s = xs + ((int64_t)c * n_in + blk * bv) / 32;
-                for (int g = 0; g < bv / 16; ++g) {
-                    int32_t a = 0, e = 0;
-                    for (int j = 0; j < 16; ++j) {
-                        a += (int32_t)w[16 * g + j] * q1[16 * g + j];
-                        e += (int32_t)w[16 * g + j] * q2[16 * g + j];
+    for (int c0 = 0; c0 < ncols; c0 += 64) {  /* tokens in chunks of 64 (one accumulator each) */
+        const int nc = ncols - c0 < 64 ? ncols - c0 : 64;
+        for (int r = 0; r < n_out; ++r) {
+            double acc[64];
+            for (int c = 0; c < nc; ++c) acc[c] = 0.0;
+            for (int blk = 0; blk < nb; ++blk) {
+                decode_int(fmt, raw + ((int64_t)r * nb + blk) * bb, w, ws, wm);
+                for (int c = 0; c < nc; ++c) {
+                    const int64_t t = c0 + c;
+                    const int8_t* q1 = xq + t * n_in + blk * bv;
+                    const int8_t* q2 = xq2 + t * n_in + blk * bv;
+                    const float* d = xd + (t * n_in + blk * bv) / 32;
+                    const float* s = xs + (t * n_in + blk * bv) / 32;
+                    for (int g = 0; g < bv / 16; ++g) {
+                        int32_t a = 0, e = 0;
+                        for (int j = 0; j < 16; ++j) {
+                            a += (int32_t)w[16 * g + j] * q1[16 * g + j];
+                            e += (int32_t)w[16 * g + j] * q2[16 * g + j];
+                        }
+                        acc[c] += ws[g] * (double)d[g / 2] * ((double)a + (double)e / 254.0);
                     }
-                    acc[c] += ws[g] * (double)d[g / 2] * ((double)a + (double)e / 254.0);
+                    if (fmt == OR_Q4_K)
+                        for (int sb = 0; sb < 8; ++sb) acc[c] -= wm[sb] * (double)s[sb];
                 }
-                if (fmt == OR_Q4_K)
-                    for (int sb = 0; sb < 8; ++sb) acc[c] -= wm[sb] * (double)s[sb];
             }
+            for (int c = 0; c < nc; ++c) y[(c0 + c) * (int64_t)n_out + r] = acc[c];
         }
-        for (int c = 0; c < ncols && c < 64; ++c) y[(int64_t)c * n_out + r] = acc[c];
     }
     return 0;
 }

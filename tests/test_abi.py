@@ -113,6 +113,18 @@ def test_rejects_bad_arguments_without_launching(L):
     assert L.nmq_akt_q8(a16, None, 2, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
     assert L.nmq_akt_q8(a16, a16 + 2, 1, a16, a16, a16, a16, a16, 32, None) == _native.NMQ_ERR_ARG
     assert L.nmq_akt_q8(a16, None, 1, a16, a16, a16, a16, a16, 40, None) == _native.NMQ_ERR_SHAPE
+    # several tokens on the fp16 matrix cores: Q4_K and Q6_K only, whole 256-value blocks
+    assert L.nmq_mm_input(None, 1, a16, a16, a16, a16, 256, 2, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mm_input(a16, 2, a16, a16, a16, a16, 256, 2, None) == _native.NMQ_ERR_ARG      # x kind
+    assert L.nmq_mm_input(a16, 1, a16 + 2, a16, a16, a16, 256, 2, None) == _native.NMQ_ERR_ARG  # xh alignment
+    assert L.nmq_mm_input(a16, 1, a16, a16, None, a16, 256, 2, None) == _native.NMQ_ERR_ARG     # xsum
+    assert L.nmq_mm_input(a16, 1, a16, a16, a16, a16, 260, 2, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mm_input(a16, 1, a16, a16, a16, a16, 256, 0, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mm(8, a16, a16, a16, a16, a16, a16, 4, 256, 2, None) == _native.NMQ_ERR_FORMAT   # Q8_0
+    assert L.nmq_mm(12, a16, a16, a16, a16, a16, a16, 4, 288, 2, None) == _native.NMQ_ERR_SHAPE
+    assert L.nmq_mm(12, a16, None, a16, a16, a16, a16, 4, 256, 2, None) == _native.NMQ_ERR_ARG
+    assert L.nmq_mm(14, a16, a16, a16 + 8, a16, a16, a16, 4, 256, 2, None) == _native.NMQ_ERR_ARG  # xl alignment
+    assert L.nmq_mm(12, a16, a16, a16, a16, a16, a16, 4, 256, 0, None) == _native.NMQ_ERR_ARG
 
 
 def test_python_api_without_gpu():

@@ -202,6 +202,146 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
+def test_mv_tokens_17_to_112(nmq, oracle, fmt):
+    """17..112 tokens through nmq_mv (launches of 16 on the matrix cores, or 8 on the dot4 kernels).
+    200 rows: partial tiles; Q8_0 / Q4_0 also on 1056 values (not whole 256-value blocks)."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    for n_in in ((1280, 1056) if BV[fmt] == 32 else (1280,)):
+        n_out = 200
+        raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=91)
+        raw_d = dev(raw)  # kept alive until the launches have run
+        for nc in (17, 24, 33, 64, 65, 112):
+            x = np.random.default_rng(92 + nc).standard_normal((nc, n_in)).astype(np.float32)
+            x[:, 7] = 30.0
+            x[nc // 2, :] *= 1e-3   # a token of much smaller scale next to the others
+            e = quant_dev(dev(x))
+            y = torch.full((nc, n_out), float("nan"), device="cuda")
+            say("mv 17..112 tokens", fmt, n_in, nc)
+            nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                       e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                       nmq.stream_ptr()))
+            torch.cuda.synchronize()
+            _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+# ---- several tokens on the fp16 matrix cores (nmq_mm) ---------------------------------------------------
+
+MM_TOL = 2e-5   # against the dequantised weights times the exact x (fp64)
+
+
+@pytest.mark.parametrize("f32", [True, False])
+@pytest.mark.parametrize("n_in", [4096 + 32, 14336, 16384 + 32])
+def test_mm_input_bitexact(nmq, oracle, f32, n_in):
+    """nmq_mm_input equals the oracle's two-stage fp16 input value for value (the sign of a zero aside):
+    rows of very different scales, a zero row, an all-equal row, a row of subnormal-range values (bf16:
+    some round to -0); rows held in registers in one or two rounds, and longer rows read twice."""
+    rng = np.random.default_rng(101)
+    nc = 19
+    x = (rng.standard_normal((nc, n_in)) * 10.0 ** rng.uniform(-5, 5, (nc, 1))).astype(np.float32)
+    x[2] = 0.0
+    x[3] = 0.75
+    x[4] *= 1e-35
+    if not f32:
+        x = oracle.round_bf16(x)
+    xd = dev(x) if f32 else dev(x).to(torch.bfloat16)
+    xh = torch.full(((nc + 15) // 16 * 16, n_in), float("nan"), dtype=torch.float16, device="cuda")
+    xl = torch.full_like(xh, float("nan"))
+    xsum = torch.full((xh.shape[0], n_in // 32), float("nan"), dtype=torch.float32, device="cuda")
+    xs = torch.empty(nc, dtype=torch.float32, device="cuda")
+    say("mm input", f32, n_in)
+    nmq.check(nmq.lib().nmq_mm_input(xd.data_ptr(), int(f32), xh.data_ptr(), xl.data_ptr(), xsum.data_ptr(),
+                                     xs.data_ptr(), n_in, nc, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    rh, rl, rsum, rs = oracle.mm_input(x)
+    pad = (nc + 15) // 16 * 16 - nc
+    for got, ref in ((xh, rh), (xl, rl)):
+        ref = np.concatenate([ref, np.zeros((pad, n_in), np.float16)])
+        got = _operand_order(host(got), n_in)
+        # exact values; the sign of a zero is not specified (-0 input may come out as xh = +0, xl = -0)
+        assert not np.isnan(got).any() and np.array_equal(got, ref)
+    g = xh.shape[0] // 16
+    got = host(xsum).reshape(g, n_in // 32, 16).transpose(0, 2, 1).reshape(16 * g, n_in // 32)
+    ref = np.concatenate([rsum, np.zeros((pad, n_in // 32), np.float32)])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(host(xs), rs)
+
+
+def _operand_order(a: np.ndarray, n_in: int) -> np.ndarray:
+    """nmq_mm_input's operand order back to token-major rows: value k of token t sits at
+    ((t/16 * n_in/32 + k/32) * 64 + (k%32)/8 * 16 + t%16) * 8 + k%8."""
+    g = a.size // (16 * n_in)
+    return a.reshape(g, n_in // 32, 4, 16, 8).transpose(0, 3, 1, 2, 4).reshape(16 * g, n_in)
+
+
+def _mm_run(nmq, fmt, raw_d, x_np, n_out, n_in):
+    from ggufengine_amd.gguf_types import TYPE_ID
+    nc = x_np.shape[0]
+    xd = dev(x_np)
+    xh = torch.empty((nc + 15) // 16 * 16, n_in, dtype=torch.float16, device="cuda")
+    xl = torch.empty_like(xh)
+    xsum = torch.empty(xh.shape[0], n_in // 32, dtype=torch.float32, device="cuda")
+    xs = torch.empty(nc, dtype=torch.float32, device="cuda")
+    y = torch.full((nc, n_out), float("nan"), device="cuda")
+    L = nmq.lib()
+    nmq.check(L.nmq_mm_input(xd.data_ptr(), 1, xh.data_ptr(), xl.data_ptr(), xsum.data_ptr(), xs.data_ptr(), n_in, nc,
+                             nmq.stream_ptr()))
+    nmq.check(L.nmq_mm(TYPE_ID[fmt], raw_d.data_ptr(), xh.data_ptr(), xl.data_ptr(), xsum.data_ptr(), xs.data_ptr(),
+                       y.data_ptr(), n_out, n_in, nc, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    return host(y)
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
+@pytest.mark.parametrize("tiles,groups", [("1", "0"), ("2", "0"), ("4", "0"), ("4", "1"), ("2", "3")])
+def test_mm_tokens(nmq, oracle, monkeypatch, fmt, tiles, groups):
+    """1..112 tokens (1..4 groups of 16 per launch, launches of 64) with 1, 2 and 4 row tiles per
+    workgroup and all, one or three token groups per workgroup (three: the last workgroup of 4 groups
+    repeats the last one, unstored): against the dequantised weights times the same two-stage input
+    (only the order of the fp32 sums differs) and times the exact input.  Shapes: partial tiles and
+    workgroups whose tiles lie past the matrix (200, 37 rows), one block per row (256: three of the
+    four K quarters empty), an odd number of blocks per quarter (1280)."""
+    monkeypatch.setenv("NMQ_MMH_T", tiles)
+    monkeypatch.setenv("NMQ_MMH_G", groups)
+    for n_out, n_in in ((200, 1280), (37, 256), (64, 4096)):
+        raw = random_blocks(fmt, n_out * n_in // 256, seed=103)
+        raw_d = dev(raw)
+        for nc in (1, 5, 16, 17, 33, 64, 65, 112):
+            x = np.random.default_rng(104 + nc).standard_normal((nc, n_in)).astype(np.float32)
+            x[:, 7] = 30.0
+            x[nc // 2, :] *= 1e-3
+            say("mm", fmt, tiles, groups, n_out, n_in, nc)
+            y = _mm_run(nmq, fmt, raw_d, x, n_out, n_in)
+            ref_same = oracle.mv_deq(fmt, raw, n_out, n_in, oracle.mm_x(x).astype(np.float32))
+            assert oracle.rel_err_rows(y, ref_same).max() <= 1e-5, (fmt, n_out, n_in, nc)
+            err = oracle.rel_err_rows(y, oracle.mv_deq(fmt, raw, n_out, n_in, x))
+            assert err.max() <= MM_TOL, (fmt, n_out, n_in, nc, float(err.max()))
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
+def test_mm_mirror_112_tokens(nmq, oracle, fmt):
+    """mmvq.mm over the reference's MMQ range (17..112 tokens, MMQ_BIS) on a Llama-width matrix, fp32
+    and bf16 input, and its input shared inside eingang_teilen()."""
+    from ggufengine_amd import mmvq
+    n_out, n_in, nc = 512, 4096, 112
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=95)
+    x = np.random.default_rng(96).standard_normal((nc, n_in)).astype(np.float32)
+    say("mm mirror", fmt, nc)
+    raw_d = dev(raw)
+    y = mmvq.mm(fmt, raw_d, dev(x), n_out, n_in)
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (nc, n_out)
+    assert oracle.rel_err_rows(host(y), oracle.mv_deq(fmt, raw, n_out, n_in, x)).max() <= MM_TOL
+    xb = dev(x).to(torch.bfloat16)
+    with mmvq.eingang_teilen():
+        y1 = mmvq.mm(fmt, raw_d, xb, n_out, n_in)
+        y2 = mmvq.mm(fmt, raw_d, xb, n_out, n_in)
+    torch.cuda.synchronize()
+    ref = oracle.mv_deq(fmt, raw, n_out, n_in, oracle.round_bf16(x))
+    assert oracle.rel_err_rows(host(y1), ref).max() <= MM_TOL
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("fmt", FMTS)
 def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
     """2..8 tokens on the dot4 kernel (the path below each format's matrix-core threshold), forced for
     every token count."""

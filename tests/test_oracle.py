@@ -153,6 +153,41 @@ def test_quant_q8_matches_numpy_and_bound(oracle):
     assert np.max(np.abs(xs - x.reshape(-1, 32).astype(np.float64).sum(1)) / np.abs(x).reshape(-1, 32).sum(1)) < 1e-6
 
 
+def test_mm_input_closed_forms(oracle):
+    """The several-token input: xs = 2^(e-8) for max|x| = f 2^e, xh = fp16(x/xs), xl = fp16 of the rest."""
+    x = np.zeros((5, 64), np.float32)
+    x[0] = 0.75                        # 0.75 = 0.75 * 2^0: xs = 2^-8, v = 192 exactly
+    x[1, 3] = 1.0                      # 1 = 0.5 * 2^1: xs = 2^-7, v = 128
+    x[2, 0] = np.float32(1 + 2.0 ** -15)  # v = 128 + 2^-8: fp16 spacing at 128 is 1/8, so xl = 2^-8
+    x[3, 9] = -3.0e-38                 # e clamped at -100: xs = 2^-108, finite
+    xh, xl, xsum, xs = oracle.mm_input(x)
+    assert xsum[0, 0] == 32 * 192 and xsum[1, 0] == 128 and xsum[2, 0] == 128 + 2.0 ** -8
+    assert xs[0] == 2.0 ** -8 and np.all(xh[0] == 192) and np.all(xl[0] == 0)
+    assert xs[1] == 2.0 ** -7 and xh[1, 3] == 128 and np.count_nonzero(xh[1]) == 1 and np.all(xl[1] == 0)
+    assert xh[2, 0] == 128 and xl[2, 0] == np.float16(2.0 ** -8)
+    assert xs[3] == np.float32(2.0 ** -108) and np.isfinite(xh[3]).all() and xh[3, 9] < 0
+    assert xs[4] == 2.0 ** -8 and not xh[4].any() and not xl[4].any()   # zero row: e = 0
+
+
+def test_mm_input_reconstruction_bound(oracle):
+    """xs * (xh + xl) is x to 2^-21 of the row's max (xh alone only to about 2^-12, so a wrong second
+    stage fails), xs is a power of two and |xh| <= 256."""
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 512)) * 10.0 ** rng.uniform(-6, 6, (64, 1))).astype(np.float32)
+    x[5, 100] = 0.0
+    xh, xl, xsum, xs = oracle.mm_input(x)
+    rec = (xh.astype(np.float64) + xl.astype(np.float64)) * xs.astype(np.float64)[:, None]
+    exact = (xh.astype(np.float64) + xl.astype(np.float64)).reshape(64, -1, 32).sum(axis=2)
+    assert np.all(np.abs(xsum - exact) <= 1e-6 * np.abs(rec / xs[:, None]).reshape(64, -1, 32).sum(axis=2))
+    m = np.abs(x).max(axis=1)
+    assert np.all(np.abs(rec - x).max(axis=1) <= m * 2.0 ** -21)
+    assert np.all(np.abs(xh.astype(np.float64) * xs[:, None] - x).max(axis=1) > m * 2.0 ** -21)
+    mant, _ = np.frexp(xs)
+    assert np.all(mant == 0.5)
+    assert np.abs(xh).max() <= 256 and np.all(np.abs(xh).max(axis=1) >= 128)
+    assert np.array_equal(oracle.mm_x(x), rec)
+
+
 # ---- integer decomposition and the two mat-vec oracles -----------------------------------------------
 
 @pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q4_K", "Q6_K", "TQ2_0", "IQ2_XXS"])
@@ -244,6 +279,23 @@ def test_mv_int_agrees_with_dequant_matmul(oracle, fmt):
     # and the dequant path itself against a float64 numpy matmul of the dequantised matrix
     w = oracle.dequant(fmt, raw).astype(np.float64).reshape(n_out, n_in)
     assert np.allclose(y_deq, x.astype(np.float64) @ w.T, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_K"])
+def test_mv_int_many_tokens_equals_one_by_one(oracle, fmt):
+    """More tokens than one accumulator chunk (70 > 64): every token's row equals its own one-token
+    call (a chunk that stops at 64 tokens, or offsets them wrongly, fails here)."""
+    n_out, n_in, nc = 8, 512, 70
+    bv = 32 if fmt == "Q8_0" else 256
+    raw = random_blocks(fmt, n_out * n_in // bv, seed=11)
+    x = np.random.default_rng(12).standard_normal((nc, n_in)).astype(np.float32)
+    xq, xq2, xd, xs = oracle.quant_q8(x)
+    y = oracle.mv_int(fmt, raw, n_out, n_in, xq, xq2, xd, xs, ncols=nc)
+    g = n_in // 32
+    for t in range(nc):
+        one = oracle.mv_int(fmt, raw, n_out, n_in, xq[t * n_in:(t + 1) * n_in], xq2[t * n_in:(t + 1) * n_in],
+                            xd[t * g:(t + 1) * g], xs[t * g:(t + 1) * g], ncols=1)
+        assert np.array_equal(y[t], one[0]), t
 
 
 def test_cpu_baseline_gemv(oracle):

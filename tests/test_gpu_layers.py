@@ -366,3 +366,38 @@ def test_llama3_8b_layer_full_size(nmq, oracle):
         assert err <= 1e-3, (n, err)
         err_i = oracle.rel_err_rows(got, oracle.mv_int(f, raw[n], r, c, *oracle.quant_q8(x))).max()
         assert err_i <= 2e-5, (n, err_i)
+
+
+def test_gguf_upload_and_matvec(nmq, oracle, tmp_path):
+    """A GGUF file with Llama-named Q4_K / Q6_K / F32 tensors (the library's writer and encoder): the
+    Uploader moves each tensor's bytes through its ring of pinned buffers unchanged (chunks of 300 KB,
+    so the ring of 4 wraps), and the mat-vecs on the uploaded blocks match the oracle on the file's
+    bytes."""
+    from ggufengine_amd import encode, gguf as G, mmvq
+    rng = np.random.default_rng(131)
+    gate = encode.encode("Q4_K", (rng.standard_normal(512 * 4096) * 0.02).astype(np.float32), threads=8)
+    down = encode.encode("Q6_K", (rng.standard_normal(256 * 1024) * 0.02).astype(np.float32), threads=8)
+    norm = rng.standard_normal(4096).astype(np.float32)
+    path = tmp_path / "blk.gguf"
+    G.write_gguf(path, {"general.architecture": (G.T_STRING, "llama"), "llama.block_count": (G.T_UINT32, 1)},
+                 [("blk.0.attn_norm.weight", (4096,), 0, norm.tobytes()),
+                  ("blk.0.ffn_gate.weight", (4096, 512), 12, gate.tobytes()),
+                  ("blk.0.ffn_down.weight", (1024, 256), 14, down.tobytes())])
+    say("gguf upload")
+    up = G.Uploader("cuda")
+    up.CHUNK = 300_000
+    with G.GGUFFile(path) as gf:
+        g_dev = G.load_raw(gf, "blk.0.ffn_gate.weight", "cuda", up)
+        d_dev = G.load_raw(gf, "blk.0.ffn_down.weight", "cuda", up)
+        n_dev = G.load_raw(gf, "blk.0.attn_norm.weight", "cuda", up)
+        torch.cuda.synchronize()
+        assert np.array_equal(g_dev.cpu().numpy(), gate) and np.array_equal(d_dev.cpu().numpy(), down)
+        assert np.array_equal(n_dev.cpu().numpy().view(np.float32), norm)
+        for raw, raw_np, fmt, n_out, n_in in ((g_dev, gate, "Q4_K", 512, 4096), (d_dev, down, "Q6_K", 256, 1024)):
+            x = rng.standard_normal(n_in).astype(np.float32)
+            y = mmvq.mv(fmt, raw, torch.from_numpy(x).cuda(), n_out, n_in).cpu().numpy()
+            err = oracle.rel_err_rows(y[None], oracle.mv_deq(fmt, raw_np, n_out, n_in, x[None]))
+            assert err.max() <= 1e-3, (fmt, float(err.max()))
+        cpu = G.load_raw(gf, "blk.0.ffn_gate.weight", "cpu")
+        assert np.array_equal(cpu.numpy(), gate)
+        del cpu

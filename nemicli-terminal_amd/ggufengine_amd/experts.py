@@ -7,6 +7,8 @@ The reference's expert path around the gathered mat-vec, on this library's kerne
   - `auswahl(logits, k)`: the softmax router of `_Schicht._auswahl` (models/baukasten.py:171-190)
     without the grouped and sigmoid variants: p = softmax(logits), the k largest, their p optionally
     renormalised to sum 1 (+1e-20), times the weights scale.
+  - `ExpertenLager` (models/moe.py:133-192): VRAM slots for the most used experts of a layer kept in
+    pinned RAM (`hostmem`), read by the kernels through per-part address tables.
   - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  Every
     (token, slot) pair on its own, in (token, slot) order (the reference's one-token and graph paths),
     the weighted sum per token in slot order.  Three launches: gate and up in one gathered launch
@@ -93,6 +95,71 @@ class PackedExperts:
                  L_ * k, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, y.data_ptr(),
                  self.n_out, self.n_in, _native.stream_ptr(dev))
         return y
+
+
+class ExpertenLager:
+    """VRAM slots for the most used experts of one layer whose tensors live in pinned RAM (reference
+    models/moe.py:133-192; the RAM side from `hostmem.empty` / `hostmem.abbilden`).
+
+    Every part (gate, up, down ...) gets an address table on the GPU with one entry per expert: its
+    slot in VRAM or its bytes in RAM.  The gathered kernels read through the table, so a HIP graph
+    keeps working when experts move.  `zaehlen(ids)` counts on the GPU how often each expert is
+    chosen (also inside a graph); `umsortieren()` (between steps, never inside a graph) moves the
+    most used ones into the slots, after which the counts fade by half."""
+
+    def __init__(self, teile, plaetze: int, device):
+        self.teile = list(teile)
+        self.n_exp = self.teile[0].n_exp
+        self.plaetze = min(int(plaetze), self.n_exp)
+        self.device = torch.device(device)
+        self.zaehler = torch.zeros(self.n_exp, dtype=torch.float32, device=self.device)
+        self.belegt = list(range(self.plaetze))           # expert held by each slot
+        self.cache = [torch.empty(self.plaetze, t.raw.shape[1], dtype=torch.uint8, device=self.device)
+                      for t in self.teile]
+        for c, t in zip(self.cache, self.teile):
+            c.copy_(t.raw[:self.plaetze], non_blocking=True)
+            t.adressen = torch.empty(self.n_exp, dtype=torch.int64, device=self.device)
+        self.verankern()
+
+    def _tabelle(self, t: PackedExperts, c: torch.Tensor) -> torch.Tensor:
+        per = t.raw.shape[1]
+        table = torch.arange(self.n_exp, dtype=torch.int64) * per + t.raw.data_ptr()
+        if self.plaetze:
+            table[torch.tensor(self.belegt)] = torch.arange(self.plaetze, dtype=torch.int64) * per + c.data_ptr()
+        return table
+
+    def verankern(self) -> None:
+        """Write the address tables from the current slots (again after the slots moved)."""
+        for t, c in zip(self.teile, self.cache):
+            t.adressen.copy_(self._tabelle(t, c))
+
+    def zaehlen(self, ids: torch.Tensor) -> None:
+        """Count the chosen experts (any shape, on the GPU)."""
+        ids = ids.reshape(-1)
+        self.zaehler.index_add_(0, ids, torch.ones(ids.numel(), dtype=torch.float32, device=ids.device))
+
+    def treffer(self) -> float:
+        """Share of the counted choices that the slots hold now."""
+        total = float(self.zaehler.sum())
+        return float(self.zaehler[self.belegt].sum()) / total if total and self.plaetze else 0.0
+
+    def umsortieren(self) -> int:
+        """The most used experts into the slots; returns how many moved in."""
+        if not self.plaetze:
+            return 0
+        top = self.zaehler.topk(self.plaetze).indices.tolist()
+        held = set(self.belegt)
+        wanted = set(top)
+        free = [p for p, e in enumerate(self.belegt) if e not in wanted]
+        incoming = [e for e in top if e not in held]
+        for p, e in zip(free, incoming):
+            for t, c in zip(self.teile, self.cache):
+                c[p].copy_(t.raw[e], non_blocking=True)
+            self.belegt[p] = e
+        if incoming:
+            self.verankern()
+        self.zaehler.mul_(0.5)
+        return len(incoming)
 
 
 def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float = 1.0

@@ -401,3 +401,61 @@ def test_gguf_upload_and_matvec(nmq, oracle, tmp_path):
         cpu = G.load_raw(gf, "blk.0.ffn_gate.weight", "cpu")
         assert np.array_equal(cpu.numpy(), gate)
         del cpu
+
+
+def test_experts_in_pinned_ram_with_vram_slots(nmq, oracle):
+    """Experts kept in pinned RAM (hostmem.empty + abbilden: hipHostMalloc, mapped at the same address)
+    are read by the gathered kernels over PCIe; ExpertenLager puts the most used ones into VRAM slots
+    behind an address table.  Every result equals the same experts in VRAM bit for bit: directly from
+    RAM, through the slots before and after re-sorting, and from a HIP graph replayed across
+    re-sorts (the graph reads the table on the device)."""
+    from ggufengine_amd import experts, hostmem
+    n_exp, n_out, n_in = 16, 256, 1024
+    raw = random_blocks("Q4_K", n_exp * n_out * n_in // 256, seed=141)
+    say("experts in pinned RAM")
+    host = hostmem.empty(raw.size, "cuda")
+    host.numpy()[:] = raw
+    mapped = hostmem.abbilden(host, "cuda")
+    assert mapped.is_cuda and mapped.data_ptr() == host.data_ptr() and hostmem.abgebildet(mapped)
+    in_ram = experts.PackedExperts(mapped, 12, n_exp, n_out, n_in)
+    in_vram = experts.PackedExperts(dev(raw), 12, n_exp, n_out, n_in)
+    rng = np.random.default_rng(142)
+    x = torch.from_numpy(rng.standard_normal(n_in).astype(np.float32)).cuda()
+    ids = torch.tensor([3, 7, 0, 15, 9, 9, 1, 12], dtype=torch.int64, device="cuda")
+    want = in_vram.matvec(ids, x)
+    assert torch.equal(in_ram.matvec(ids, x), want)
+    ref = oracle.mv_deq("Q4_K", raw.reshape(n_exp, -1)[ids.cpu().numpy()].ravel(), 8 * n_out, n_in,
+                        oracle.round_bf16(x.cpu().numpy())[None])
+    err = oracle.rel_err_rows(want.cpu().numpy(), ref.reshape(8, n_out))
+    assert err.max() <= 1e-3
+    lager = experts.ExpertenLager([in_ram], plaetze=4, device="cuda")
+    assert lager.belegt == [0, 1, 2, 3]
+    assert torch.equal(in_ram.matvec(ids, x), want)
+    for _ in range(3):
+        lager.zaehlen(torch.tensor([9, 12, 15, 7, 9], device="cuda"))
+    assert lager.umsortieren() == 4 and sorted(lager.belegt) == [7, 9, 12, 15]
+    assert lager.treffer() == 1.0
+    assert torch.equal(in_ram.matvec(ids, x), want)
+    # a graph of the gathered launch, replayed across re-sorts
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        in_ram.matvec(ids, x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = in_ram.matvec(ids, x)
+    for hot in ([0, 1, 2, 3], [3, 7, 0, 15], [12, 1, 9, 0]):
+        for _ in range(2):
+            lager.zaehlen(torch.tensor(hot, device="cuda"))
+        lager.umsortieren()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), hot
+        assert torch.equal(in_ram.matvec(ids, x), want)   # eager work between replays
+    del g, out, lager, in_ram, mapped, host
+    import gc
+    gc.collect()
+    assert hostmem.pending() >= 1
+    hostmem.flush()
+    assert hostmem.pending() == 0

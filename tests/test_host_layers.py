@@ -57,3 +57,17 @@ def test_block_layers_check_sizes():
         experts.PackedExperts(raw, TYPE_ID["Q6_K"], 2, 4, 4096)
     with pytest.raises(GGUFError):
         packed.PackedLinear(raw, 9, 1, 32)   # Q8_1 is not a weight format of this library
+
+
+def test_hostmem_without_gpu():
+    """hostmem imports and answers without a device: ordinary tensors are not pinned blocks, nothing is
+    pending, flush() is a no-op, and abbilden() refuses memory that is not from hostmem.empty()."""
+    import torch
+    from ggufengine_amd import hostmem
+    t = torch.zeros(16, dtype=torch.uint8)
+    assert not hostmem.abgebildet(t)
+    assert hostmem.pending() == 0
+    hostmem.flush()
+    with pytest.raises(ValueError):
+        hostmem.abbilden(t, "cpu")
+    assert hostmem.ram_reicht(0) in (True, False)

@@ -60,6 +60,16 @@ struct MvParams {
 // reads expert ids[m'] of tensor w (m' = m) or, with a second tensor, of w2 (m' = m - n_ids for
 // m >= n_ids), at ids[m'] * per_expert bytes or at the address table entry ids[m']; its input row is
 // m' / x_group.
+// The expert id and the table entry are moved into scalar registers (readfirstlane: they are uniform
+// per workgroup): left in vector registers, the weight addresses of every kernel would depend on a
+// vector load on one path, and where the paths meet the compiler would wait for every outstanding
+// read of the wave (the input reads issued ahead of the weight reads included) before any weight read.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const u32 lo = __builtin_amdgcn_readfirstlane((u32)v);
+    const u32 hi = __builtin_amdgcn_readfirstlane((u32)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
 __device__ __forceinline__ const u8* instance_weights(const MvParams& p, int m, int64_t& xrow) {
     if (!p.ids) {
         xrow = 0;
@@ -67,10 +77,10 @@ __device__ __forceinline__ const u8* instance_weights(const MvParams& p, int m, 
     }
     const bool second = p.w2 != nullptr && m >= p.n_ids;
     const int mm = second ? m - p.n_ids : m;
-    const int64_t e = gp<int64_t>(p.ids)[mm];
+    const int64_t e = uniform64(gp<int64_t>(p.ids)[mm]);
     xrow = mm / p.x_group;
     const u8* base = second ? p.w2 : p.w;
-    return p.per_expert >= 0 ? base + e * p.per_expert : (const u8*)(gp<int64_t>(base)[e]);
+    return p.per_expert >= 0 ? base + e * p.per_expert : (const u8*)uniform64(gp<int64_t>(base)[e]);
 }
 
 // Row addressing of the one-token kernels: one matrix (rows back to back from w, outputs from y) or
@@ -207,6 +217,27 @@ __device__ __forceinline__ void read_slice(const u8* base, int ktp, int u, XSlic
     }
 }
 
+// Reads issued by hand (inline assembly): the compiler's wait insertion does not see them, so its own
+// waits can only wait longer than needed, and the code that issues them places its own waits
+// (vm_wait<N>: until at most N reads of the wave are outstanding, the registers tied to the wait so
+// that nothing reads them before).  Used where the compiler would otherwise wait for every read of
+// the wave (buffers rotating through a loop, staging stores ahead of weight reads).
+__device__ __forceinline__ u32x4 gload16(const void* ptr) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr));
+    return v;
+}
+__device__ __forceinline__ u32x2 gload8(const void* ptr) {
+    u32x2 v;
+    asm volatile("global_load_dwordx2 %0, %1, off" : "=v"(v) : "v"(ptr));
+    return v;
+}
+__device__ __forceinline__ float gload4f(const void* ptr) {
+    float v;
+    asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(ptr));
+    return v;
+}
+
 // One token, whole row, in rounds of one 16-byte chunk of xq and of xq2 and one (xd, xs) pair per
 // thread.  Every read of a round is issued (threads past the row re-read its start), so a kernel can
 // issue round 0 before its weight reads and wait for it alone; the stores apply stage_tile's layout.
@@ -224,6 +255,23 @@ __device__ __forceinline__ void stage1_load(XRound& r, int rnd, const int8_t* xq
     const int g = i < n_in / 32 ? i : 0;
     r.d = gp<float>(xd)[g];
     r.s = gp<float>(xs)[g];
+}
+
+// stage1_load with the reads issued by hand; xround_wait<N>() waits for them with N later reads out.
+__device__ __forceinline__ void stage1_load_hand(XRound& r, int rnd, const int8_t* xq, const int8_t* xq2,
+                                                 const float* xd, const float* xs, int n_in, int nt) {
+    const int i = rnd * nt + (int)threadIdx.x;
+    const int ch = 16 * i < n_in ? i : 0;
+    r.a = gload16(xq + 16 * ch);
+    r.b = gload16(xq2 + 16 * ch);
+    const int g = i < n_in / 32 ? i : 0;
+    r.d = gload4f(xd + g);
+    r.s = gload4f(xs + g);
+}
+
+template <int N>
+__device__ __forceinline__ void xround_wait(XRound& r) {
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(r.a), "+v"(r.b), "+v"(r.d), "+v"(r.s) : "n"(N));
 }
 
 template <bool STRIDED>
@@ -417,6 +465,49 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
     lds_barrier();
 }
 
+// Input staging around hand-issued weight reads (Q4kStepAsm): two-stage input, one round (the row fits
+// one 16-byte chunk per thread; the launcher checks), straight-line code.  The input reads are issued
+// by hand before issue()'s HW weight reads and waited for with exactly those left outstanding.  No
+// branch may join between a hand-issued read and its wait: where paths join, the compiler may copy a
+// register whose read is still outstanding (it takes the value as present once the instruction issued).
+// The same for fp32 values (NMQ_X_F32, NMQ_X_F32_BF16: both read 16 bytes per lane and round), at most
+// two rounds of four values per thread (the launcher checks); the quantisation follows the wait.
+template <int F, int HW, typename Issue>
+__device__ __forceinline__ void stagev_hand(u8* lds, const MvParams& p, int64_t xrow, Issue issue) {
+    using FM = Fmt<F>;
+    const float* xv = (const float*)p.xv + xrow * p.n_in;
+    const int nt = p.nt;
+    const int j0 = (int)threadIdx.x, j1 = nt + (int)threadIdx.x;
+    u32x4 a0 = gload16(xv + (4 * j0 < p.n_in ? 4 * j0 : 0));  // past the row: its start (discarded)
+    u32x4 a1 = gload16(xv + (4 * j1 < p.n_in ? 4 * j1 : 0));
+    __builtin_amdgcn_sched_barrier(0);
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a0), "+v"(a1) : "n"(HW));
+    VRound r0, r1;
+    r0.v[0] = __uint_as_float(a0.x); r0.v[1] = __uint_as_float(a0.y);
+    r0.v[2] = __uint_as_float(a0.z); r0.v[3] = __uint_as_float(a0.w);
+    r1.v[0] = __uint_as_float(a1.x); r1.v[1] = __uint_as_float(a1.y);
+    r1.v[2] = __uint_as_float(a1.z); r1.v[3] = __uint_as_float(a1.w);
+    stagev_store<FM::STRIDED>(r0, 0, lds, p.x_mode, p.n_in, p.ktp, nt);
+    stagev_store<FM::STRIDED>(r1, 1, lds, p.x_mode, p.n_in, p.ktp, nt);
+    lds_barrier();
+}
+
+template <int F, int HW, typename Issue>
+__device__ __forceinline__ void stage1_hand(u8* lds, const MvParams& p, int64_t xrow, Issue issue) {
+    using FM = Fmt<F>;
+    XRound r;
+    stage1_load_hand(r, 0, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
+                     p.xs + xrow * (p.n_in / 32), p.n_in, p.nt);
+    __builtin_amdgcn_sched_barrier(0);
+    issue();
+    __builtin_amdgcn_sched_barrier(0);
+    xround_wait<HW>(r);
+    stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp, p.nt);
+    lds_barrier();
+}
+
 template <int F>
 __device__ __forceinline__ void fill_tables(u64* tab, int nt) {
     if (F == NMQ_IQ2_XXS) {
@@ -580,6 +671,36 @@ struct Mv1Step {
     }
 };
 
+// One step of Q4_K weight reads of the one-token kernel, issued by hand (gload16): with buffers
+// rotating through the loop, the compiler's wait insertion waits for every outstanding read at the
+// loop head (all of a wave's prefetched steps); wait<N>() waits for this step with N later reads out.
+template <int NITM>
+struct Q4kStepAsm {
+    Fmt<NMQ_Q4_K>::Raw raw[NITM];
+    template <int T>
+    __device__ __forceinline__ void load(const RowMap& rm, int r, int lt, int U, int fb) {
+        const u8* rp = rm.row(r < rm.n_out ? r : min(fb, rm.n_out - 1));
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            const int u = min(lt + it * T, U - 1);
+            const u8* blk = rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB + 32 * (u & 3);
+            raw[it].h = gload16(rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB);
+            raw[it].a = gload16(blk + 16);
+            raw[it].b = gload16(blk + 32);
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            if (it == 0)
+                asm volatile("s_waitcnt vmcnt(%3)" : "+v"(raw[it].h), "+v"(raw[it].a), "+v"(raw[it].b) : "n"(N));
+            else
+                asm volatile("" : "+v"(raw[it].h), "+v"(raw[it].a), "+v"(raw[it].b));
+        }
+    }
+};
+
 // Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
 struct LaneConst {
     bool hi[4];     // Q4_K: the unit's sub-blocks are 4..7
@@ -638,8 +759,15 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
 }
 
 // EXT: the variant that also takes segments and value input (the plain one keeps the shorter code).
-template <int F, int T, int RW, int NITM, int NBUF, bool EXT>
+// HR (Q4_K; 1: two-stage input, 2: fp32 values): the weight reads are issued by hand (Q4kStepAsm, the compiler waits for all of a wave's
+// outstanding reads at the head of its own loop) and the row results are held in registers (lane k of a
+// team: the team's k-th row), written when the team holds T of them (then every outstanding access is
+// waited for) and after the last row, so that the pipelined loop issues reads only.
+template <int F, int T, int RW, int NITM, int NBUF, bool EXT, int HR = 0>
 __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
+    static_assert(HR == 0 || (F == NMQ_Q4_K && RW == 1 && (HR == 1 || EXT)), "HR: Q4_K, one row per team");
+    // HR = 1: the launcher guarantees two-stage input staged in one round; HR = 2: fp32 values (x_mode
+    // NMQ_X_F32 or NMQ_X_F32_BF16) in at most two rounds
     args_early<EXT>(p);
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
@@ -661,13 +789,22 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     // NBUF step buffers rotate: while one step is computed, the next NBUF - 1 are in flight (the first
     // NBUF - 1 go out while the input is staged).
     Mv1Step<F, T, RW, NITM> buf[NBUF];
+    Q4kStepAsm<NITM> hb[NBUF];  // HR: the step buffers of the hand-issued reads
     const int stride = nw * SR;
     int base = gw * SR;
-    stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] {
+    if constexpr (HR) {
+        auto issue = [&] {
 #pragma unroll
-        for (int i = 0; i < NBUF - 1; ++i)
-            buf[i].load(rm, base + i * stride + off, lt, U, base + off);
-    });
+            for (int i = 0; i < NBUF - 1; ++i) hb[i].template load<T>(rm, base + i * stride + off, lt, U, base + off);
+        };
+        if constexpr (HR == 1) stage1_hand<F, 3 * NITM * (NBUF - 1)>(lds, p, xrow, issue);
+        else stagev_hand<F, 3 * NITM * (NBUF - 1)>(lds, p, xrow, issue);
+    } else {
+        stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] {
+#pragma unroll
+            for (int i = 0; i < NBUF - 1; ++i) buf[i].load(rm, base + i * stride + off, lt, U, base + off);
+        });
+    }
     XSlice x[NITM];
 #pragma unroll
     for (int it = 0; it < NITM; ++it) {
@@ -676,6 +813,43 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     }
 
     const LaneConst lc = lane_const<F, T, NITM>(lt);
+    if constexpr (HR) {
+        float res = 0.f;
+        int k = 0, first = base;
+        bool more = true;
+        while (more) {
+#pragma unroll
+            for (int i = 0; i < NBUF; ++i) {
+                if (base >= p.n_out) {  // wave-uniform
+                    more = false;
+                    break;
+                }
+                hb[(i + NBUF - 1) % NBUF].template load<T>(rm, base + (NBUF - 1) * stride + off, lt, U, base + off);
+                hb[i].template wait<3 * NITM * (NBUF - 1)>();  // this step's reads; the NBUF - 1 later steps stay out
+                float acc = 0.f;
+#pragma unroll
+                for (int it = 0; it < NITM; ++it) {
+                    const int u = lt + it * T;
+                    const float v = unit_dot1<F>(hb[i].raw[it], min(u, U - 1), tab, x[it], lc, it);
+                    acc += u < U ? v : 0.f;
+                }
+                acc = team_sum<T>(acc);
+                res = lt == k ? acc : res;
+                base += stride;
+                if (++k == T) {
+                    const int r = first + lt * stride + off;
+                    if (r < rm.n_out) *gpw<float>(rm.out(r)) = res;
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    k = 0;
+                    first = base;
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the surplus reads of the last steps
+        const int r = first + lt * stride + off;
+        if (lt < k && r < rm.n_out) *gpw<float>(rm.out(r)) = res;
+        return;
+    }
     for (;;) {
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
@@ -939,8 +1113,22 @@ inline MvKernel pick_mv1_ext(int nitm) {
     return nitm == 1 ? mv1_kernel<F, T, 1, 1, 3, true> : (nitm == 2 ? mv1_kernel<F, T, 1, 2, 3, true>
                                                                      : mv1_kernel<F, T, 1, 4, 3, true>);
 }
+// hr: the Q4_K variant with hand-issued weight reads and register-held results (one row per team,
+// 3 buffers)
+template <int F, int T, bool EXT, int HR>
+inline MvKernel pick_mv1_hr(int nitm) {
+    if constexpr (F != NMQ_Q4_K) return nullptr;
+    else return nitm == 1 ? mv1_kernel<F, T, 1, 1, 3, EXT, HR> : mv1_kernel<F, T, 1, 2, 3, EXT, HR>;
+}
+template <int F, bool EXT, int HR>
+inline MvKernel pick_mv1_hr_t(int T, int nitm) {
+    return T == 16 ? pick_mv1_hr<F, 16, EXT, HR>(nitm)
+                   : (T == 32 ? pick_mv1_hr<F, 32, EXT, HR>(nitm) : pick_mv1_hr<F, 64, EXT, HR>(nitm));
+}
 template <int F>
-inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf, bool ext) {
+inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf, bool ext, int hr = 0) {
+    if (hr == 2) return pick_mv1_hr_t<F, true, 2>(T, nitm);
+    if (hr == 1) return ext ? pick_mv1_hr_t<F, true, 1>(T, nitm) : pick_mv1_hr_t<F, false, 1>(T, nitm);
     if (ext) return T == 16 ? pick_mv1_ext<F, 16>(nitm) : (T == 32 ? pick_mv1_ext<F, 32>(nitm) : pick_mv1_ext<F, 64>(nitm));
     switch (T) {
         case 16: return pick_mv1_rw<F, 16>(rw, nitm, nbuf);
@@ -1159,7 +1347,14 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
         if (s1.ok) {
             p.ktp = s1.ktp;
-            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf, ext);
+            // Q4_K with the two-stage input staged in one round, or fp32 values in at most two: hand-issued
+            // reads (NMQ_MV1_HR=0 for the compiler-scheduled loop)
+            int hr = 0;
+            if (F == NMQ_Q4_K && s1.rw == 1 && s1.nbuf == 3 && s1.nitm <= 2 && env_int("NMQ_MV1_HR", 1) != 0) {
+                if (p.xv == nullptr) hr = s1.ktp / 16 <= 64 * s1.W ? 1 : 0;
+                else if (p.x_mode == NMQ_X_F32 || p.x_mode == NMQ_X_F32_BF16) hr = s1.ktp / 4 <= 2 * 64 * s1.W ? 2 : 0;
+            }
+            MvKernel k = pick_mv1<F>(s1.T, s1.rw, s1.nitm, s1.nbuf, ext, hr);
             p.nt = 64 * s1.W;
             hipLaunchKernelGGL(k, dim3((unsigned)s1.grid_x, (unsigned)n_mats), dim3(p.nt), s1.lds, stream, p);
             return (int)hipGetLastError();

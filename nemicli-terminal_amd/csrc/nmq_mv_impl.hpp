@@ -409,18 +409,18 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
         const void* xv2 = p.xv2 ? (const u8*)p.xv2 + xrow * p.n_in * 4 : p.xv;
         const int rounds = (p.ktp / 4 + nt - 1) / nt;
         if (rounds <= 2) {  // the value reads first, the weight reads next, then the quantisation
+            // Both rounds unconditionally (reads past the row are clamped to its start, stores past it
+            // skipped): with a branch per round the compiler waits for each round's reads before the next.
             VRound r[2];
 #pragma unroll
-            for (int k = 0; k < 2; ++k)
-                if (k < rounds) stagev_load(r[k], k, xv, xv2, p.x_mode, p.n_in, nt);
+            for (int k = 0; k < 2; ++k) stagev_load(r[k], k, xv, xv2, p.x_mode, p.n_in, nt);
             const u64 gv = tab_load<F>();
             __builtin_amdgcn_sched_barrier(0);
             issue();
             __builtin_amdgcn_sched_barrier(0);
             tab_store<F>(tab, gv, nt);
 #pragma unroll
-            for (int k = 0; k < 2; ++k)
-                if (k < rounds) stagev_store<FM::STRIDED>(r[k], k, lds, p.x_mode, p.n_in, p.ktp, nt);
+            for (int k = 0; k < 2; ++k) stagev_store<FM::STRIDED>(r[k], k, lds, p.x_mode, p.n_in, p.ktp, nt);
         } else {
             for (int k = 0; k < rounds; ++k) {
                 VRound r;
@@ -440,18 +440,18 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
     const float* xs = p.xs + xrow * (p.n_in / 32);
     const int rounds = (p.ktp / 16 + nt - 1) / nt;
     if (rounds <= MAXR) {
+        // All MAXR rounds unconditionally (reads past the row are clamped to its start, stores past it
+        // skipped): with a branch per round the compiler waits for each round's reads before the next.
         XRound r[MAXR];
 #pragma unroll
-        for (int k = 0; k < MAXR; ++k)
-            if (k < rounds) stage1_load(r[k], k, xq, xq2, xd, xs, p.n_in, nt);
+        for (int k = 0; k < MAXR; ++k) stage1_load(r[k], k, xq, xq2, xd, xs, p.n_in, nt);
         const u64 gv = tab_load<F>();
         __builtin_amdgcn_sched_barrier(0);  // keep the input reads ahead of the weight reads
         issue();
         __builtin_amdgcn_sched_barrier(0);
         tab_store<F>(tab, gv, nt);
 #pragma unroll
-        for (int k = 0; k < MAXR; ++k)
-            if (k < rounds) stage1_store<FM::STRIDED>(r[k], k, lds, p.n_in, p.ktp, nt);
+        for (int k = 0; k < MAXR; ++k) stage1_store<FM::STRIDED>(r[k], k, lds, p.n_in, p.ktp, nt);
     } else {
         for (int k = 0; k < rounds; ++k) {
             XRound r;

@@ -219,18 +219,37 @@ struct Fmt<NMQ_Q4_K> {
     }
 };
 
-// One-token fast path of Q4_K (mv1): decode and dot fused, branch free.  All eight 6-bit scales and
-// mins of the block are formed four at a time inside dwords (get_scale_min_k4 without byte loops):
+// One-token fast path of Q4_K (mv1): decode and dot fused, branch free.  The eight 6-bit scales and
+// mins of a block (get_scale_min_k4) are, four at a time inside dwords:
 //   sc[0..3] = scales[0..3] & 63              m[0..3] = scales[4..7] & 63
 //   sc[4..7] = (scales[8..11] & 15) | (scales[0..3] >> 6) << 4
 //   m[4..7]  = (scales[8..11] >> 4) | (scales[4..7] >> 6) << 4
-// and the lane's two (sub-blocks 2i, 2i+1 = bytes t0, t0+1 of the low or high dword) are converted
-// straight from their bytes.  Runs 0,1 and 2,3 are summed in one dot4 chain each.
-__device__ __forceinline__ float q4k_dot1(const Fmt<NMQ_Q4_K>::Raw& r, const XSlice& x, bool hi, u32 t0sh) {
-    const u32 sl = r.h.y & 0x3f3f3f3fu, ml = r.h.z & 0x3f3f3f3fu;
-    const u32 sh = (r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u);
-    const u32 mh = ((r.h.w >> 4) & 0x0f0f0f0fu) | ((r.h.z >> 2) & 0x30303030u);
-    const u32 sv = (hi ? sh : sl) >> t0sh, mv = (hi ? mh : ml) >> t0sh;
+// A lane's unit always takes sub-blocks 2i, 2i+1 = bytes t0, t0 + 1 of the low (i < 2) or high half, so
+// the choice of half and byte folds into lane-constant shifts and masks (Q4kLane):
+//   sc pair = ((h.w >> sw) & ma) | ((h.y >> sy) & mb),   m pair = ((h.w >> sm) & ma) | ((h.z >> sy) & mb)
+// with, low half: ma = 0, mb = 0x3f3f3f3f, sy = 8 t0; high half: ma = 0x0f0f0f0f, mb = 0x30303030,
+// sy = 8 t0 + 2, sw = 8 t0, sm = 8 t0 + 4; the scales and mins are then bytes 0 and 1.  Runs 0,1 and
+// 2,3 are summed in one dot4 chain each; the two stages combine as an integer 254 S1 + S2 (exact in
+// fp32: |254 S1 + S2| < 2^24) times xd / 254.
+struct Q4kLane {
+    u32 sw, sm, sy, ma, mb;
+};
+
+__device__ __forceinline__ Q4kLane q4k_lane(int u) {
+    const int i = u & 3;
+    const u32 t = 8u * (u32)((2 * i) & 3);
+    Q4kLane c;
+    if (i >= 2) {
+        c.ma = 0x0f0f0f0fu; c.mb = 0x30303030u; c.sy = t + 2u; c.sw = t; c.sm = t + 4u;
+    } else {
+        c.ma = 0u; c.mb = 0x3f3f3f3fu; c.sy = t; c.sw = 0u; c.sm = 0u;
+    }
+    return c;
+}
+
+__device__ __forceinline__ float q4k_dot1(const Fmt<NMQ_Q4_K>::Raw& r, const XSlice& x, const Q4kLane& c) {
+    const u32 sv = ((r.h.w >> c.sw) & c.ma) | ((r.h.y >> c.sy) & c.mb);
+    const u32 mv = ((r.h.w >> c.sm) & c.ma) | ((r.h.z >> c.sy) & c.mb);
     const float sc0 = (float)(sv & 0xffu), sc1 = (float)((sv >> 8) & 0xffu);  // v_cvt_f32_ubyte0/1
     const float m0 = (float)(mv & 0xffu), m1 = (float)((mv >> 8) & 0xffu);
     const u32 q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
@@ -243,8 +262,8 @@ __device__ __forceinline__ float q4k_dot1(const Fmt<NMQ_Q4_K>::Raw& r, const XSl
         a1 = dot4(hn, x.q[8 + k], a1);
         b1 = dot4(hn, x.q2[8 + k], b1);
     }
-    const float g0 = x.d[0] * ((float)a0 + FEIN * (float)b0);
-    const float g1 = x.d[1] * ((float)a1 + FEIN * (float)b1);
+    const float g0 = (float)(__mul24(a0, 254) + b0) * (x.d[0] * FEIN);  // |a0| <= 32 * 15 * 127: 24-bit
+    const float g1 = (float)(__mul24(a1, 254) + b1) * (x.d[1] * FEIN);
     const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
     return d * (sc0 * g0 + sc1 * g1) - dmin * (m0 * x.s[0] + m1 * x.s[1]);
 }

@@ -649,8 +649,17 @@ __device__ __forceinline__ float team_sum(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));  // xor 2
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));  // 8-lane mirror
     v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));  // 16-lane mirror
-    if (T >= 32) v += __shfl_xor(v, 16);
-    if (T >= 64) v += __shfl_xor(v, 32);
+    // across rows without LDS (gfx950 lane swaps): the two results of permlane16_swap(v, v) hold, in every
+    // lane, its own value and that of lane ^ 16 (permlane32_swap: lane ^ 32), so their sum is what
+    // v + shfl_xor(v, 16 / 32) gives, bit for bit (a + b = b + a)
+    if (T >= 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    if (T >= 64) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
     return v;
 }
 
@@ -674,19 +683,46 @@ struct Mv1Step {
 // One step of Q4_K weight reads of the one-token kernel, issued by hand (gload16): with buffers
 // rotating through the loop, the compiler's wait insertion waits for every outstanding read at the
 // loop head (all of a wave's prefetched steps); wait<N>() waits for this step with N later reads out.
+// With one row per wave (T = 64) the row address is uniform: the reads take it in scalar registers
+// and a lane-constant 32-bit offset (global_load with a scalar base), no 64-bit address arithmetic per
+// step.
+__device__ __forceinline__ u32x4 gload16s(const u8* base, u32 off) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+    return v;
+}
+__device__ __forceinline__ u32x4 gload16s_16(const u8* base, u32 off) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:16" : "=v"(v) : "v"(off), "s"(base));
+    return v;
+}
+
 template <int NITM>
 struct Q4kStepAsm {
     Fmt<NMQ_Q4_K>::Raw raw[NITM];
     template <int T>
     __device__ __forceinline__ void load(const RowMap& rm, int r, int lt, int U, int fb) {
-        const u8* rp = rm.row(r < rm.n_out ? r : min(fb, rm.n_out - 1));
+        const int rs = r < rm.n_out ? r : min(fb, rm.n_out - 1);
+        if constexpr (T == 64) {
+            const u8* rp = (const u8*)uniform64((int64_t)rm.row(rs));
 #pragma unroll
-        for (int it = 0; it < NITM; ++it) {
-            const int u = min(lt + it * T, U - 1);
-            const u8* blk = rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB + 32 * (u & 3);
-            raw[it].h = gload16(rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB);
-            raw[it].a = gload16(blk + 16);
-            raw[it].b = gload16(blk + 32);
+            for (int it = 0; it < NITM; ++it) {
+                const int u = min(lt + it * T, U - 1);
+                const u32 oh = (u32)((u >> 2) * Fmt<NMQ_Q4_K>::BB), oa = oh + 16u + 32u * (u32)(u & 3);
+                raw[it].h = gload16s(rp, oh);
+                raw[it].a = gload16s(rp, oa);
+                raw[it].b = gload16s_16(rp, oa);
+            }
+        } else {
+            const u8* rp = rm.row(rs);
+#pragma unroll
+            for (int it = 0; it < NITM; ++it) {
+                const int u = min(lt + it * T, U - 1);
+                const u8* blk = rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB + 32 * (u & 3);
+                raw[it].h = gload16(rp + (u >> 2) * Fmt<NMQ_Q4_K>::BB);
+                raw[it].a = gload16(blk + 16);
+                raw[it].b = gload16(blk + 32);
+            }
         }
     }
     template <int N>
@@ -703,19 +739,14 @@ struct Q4kStepAsm {
 
 // Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
 struct LaneConst {
-    bool hi[4];     // Q4_K: the unit's sub-blocks are 4..7
-    u32 t0sh[4];    // Q4_K: bit offset of the first of its two scale bytes
+    Q4kLane q4k[4];  // Q4_K: the unit's scale/min selection
 };
 
 template <int F, int T, int NITM>
 __device__ __forceinline__ LaneConst lane_const(int lt) {
     LaneConst c{};
 #pragma unroll
-    for (int it = 0; it < NITM && it < 4; ++it) {
-        const int i = (lt + it * T) & 3;
-        c.hi[it] = i >= 2;
-        c.t0sh[it] = (u32)(8 * ((2 * i) & 3));
-    }
+    for (int it = 0; it < NITM && it < 4; ++it) c.q4k[it] = q4k_lane(lt + it * T);
     return c;
 }
 
@@ -724,7 +755,7 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
                                            const LaneConst& lc, int it) {
     using FM = Fmt<F>;
     if constexpr (F == NMQ_Q4_K) {
-        return q4k_dot1(raw, x, lc.hi[it], lc.t0sh[it]);
+        return q4k_dot1(raw, x, lc.q4k[it]);
     } else if constexpr (F == NMQ_Q6_K) {
         return q6k_dot1(raw, x, u);
     } else {

@@ -111,6 +111,15 @@ __device__ __forceinline__ u32x2 ld2(const u8* p) { return *gp<u32x2_a2>(p); }
 __device__ __forceinline__ u32 ld1(const u8* p) { return *gp<u32_a2>(p); }
 __device__ __forceinline__ u32 ld16(const u8* p) { return *gp<u16>(p); }
 
+// Q6_K code bytes (0..63) of group g (0..3) from a dword of ql (la for even g, lb for odd) and of qh:
+// low nibbles of ql for g < 2, high ones for g >= 2, and qh bits 2g, 2g+1 of every byte at bits 4, 5
+// (qh shifted by 4 - 2g and masked: the same bytes as ((qh >> 2g) & 3) << 4, one instruction fewer).
+template <int G>
+__device__ __forceinline__ u32 q6k_codes(u32 ql, u32 qh) {
+    const u32 hb = G == 0 ? (qh << 4) : (G == 1 ? (qh << 2) : (G == 2 ? qh : (qh >> 2)));
+    return ((G >= 2 ? (ql >> 4) : ql) & 0x0f0f0f0fu) | (hb & 0x30303030u);
+}
+
 // q - 32 per byte for bytes 0..63 (Q6_K): ((q | 0x80) - 0x20) ^ 0x80 never borrows across bytes.
 __device__ __forceinline__ u32 sub32x4(u32 v) { return ((v | 0x80808080u) - 0x20202020u) ^ 0x80808080u; }
 // code - 1 per byte for codes 0..3 (TQ2_0): (c + 0x7f) ^ 0x80 never carries across bytes.
@@ -327,7 +336,9 @@ __device__ __forceinline__ float q6k_dot1(const Fmt<NMQ_Q6_K>::Raw& r, const XSl
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const u32 lo = (g & 1) ? lb[k] : la[k];
-            const u32 w = sub32x4(((lo >> (4 * (g >> 1))) & 0x0f0f0f0fu) | (((qh[k] >> (2 * g)) & 0x03030303u) << 4));
+            const u32 c = g == 0 ? q6k_codes<0>(lo, qh[k])
+                                 : (g == 1 ? q6k_codes<1>(lo, qh[k]) : (g == 2 ? q6k_codes<2>(lo, qh[k]) : q6k_codes<3>(lo, qh[k])));
+            const u32 w = sub32x4(c);
             s1 = dot4(w, x.q[4 * g + k], s1);
             s2 = dot4(w, x.q2[4 * g + k], s2);
         }

@@ -472,18 +472,36 @@ __device__ __forceinline__ void stage1_around(u8* lds, u64* tab, const MvParams&
 // register whose read is still outstanding (it takes the value as present once the instruction issued).
 // The same for fp32 values (NMQ_X_F32, NMQ_X_F32_BF16: both read 16 bytes per lane and round), at most
 // two rounds of four values per thread (the launcher checks); the quantisation follows the wait.
+// IQ2_XXS: the thread's grid entry is read by hand with the input and stored after the same wait
+// (the launcher gives such launches at least 256 threads).
+template <int F>
+__device__ __forceinline__ u32x2 tab_load_hand() {
+    if constexpr (F == NMQ_IQ2_XXS) return gload8(&IQ2XXS_GRID[min((int)threadIdx.x, 255)]);
+    else return u32x2{0u, 0u};
+}
+
+template <int F>
+__device__ __forceinline__ void tab_store_hand(u64* tab, u32x2 gv, int nt) {
+    if constexpr (F == NMQ_IQ2_XXS) {
+        if (threadIdx.x < 256) tab[threadIdx.x] = (u64)gv.x | ((u64)gv.y << 32);
+        for (int i = threadIdx.x; i < 128; i += nt) tab[256 + i] = iq2_sign_mask((u32)i);
+    }
+}
+
 template <int F, int HW, typename Issue>
-__device__ __forceinline__ void stagev_hand(u8* lds, const MvParams& p, int64_t xrow, Issue issue) {
+__device__ __forceinline__ void stagev_hand(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
     using FM = Fmt<F>;
     const float* xv = (const float*)p.xv + xrow * p.n_in;
     const int nt = p.nt;
     const int j0 = (int)threadIdx.x, j1 = nt + (int)threadIdx.x;
     u32x4 a0 = gload16(xv + (4 * j0 < p.n_in ? 4 * j0 : 0));  // past the row: its start (discarded)
     u32x4 a1 = gload16(xv + (4 * j1 < p.n_in ? 4 * j1 : 0));
+    u32x2 gv = tab_load_hand<F>();
     __builtin_amdgcn_sched_barrier(0);
     issue();
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt vmcnt(%2)" : "+v"(a0), "+v"(a1) : "n"(HW));
+    asm volatile("s_waitcnt vmcnt(%3)" : "+v"(a0), "+v"(a1), "+v"(gv) : "n"(HW));
+    tab_store_hand<F>(tab, gv, nt);
     VRound r0, r1;
     r0.v[0] = __uint_as_float(a0.x); r0.v[1] = __uint_as_float(a0.y);
     r0.v[2] = __uint_as_float(a0.z); r0.v[3] = __uint_as_float(a0.w);
@@ -495,15 +513,18 @@ __device__ __forceinline__ void stagev_hand(u8* lds, const MvParams& p, int64_t 
 }
 
 template <int F, int HW, typename Issue>
-__device__ __forceinline__ void stage1_hand(u8* lds, const MvParams& p, int64_t xrow, Issue issue) {
+__device__ __forceinline__ void stage1_hand(u8* lds, u64* tab, const MvParams& p, int64_t xrow, Issue issue) {
     using FM = Fmt<F>;
     XRound r;
     stage1_load_hand(r, 0, p.xq + xrow * p.n_in, p.xq2 + xrow * p.n_in, p.xd + xrow * (p.n_in / 32),
                      p.xs + xrow * (p.n_in / 32), p.n_in, p.nt);
+    u32x2 gv = tab_load_hand<F>();
     __builtin_amdgcn_sched_barrier(0);
     issue();
     __builtin_amdgcn_sched_barrier(0);
     xround_wait<HW>(r);
+    asm volatile("" : "+v"(gv));
+    tab_store_hand<F>(tab, gv, p.nt);
     stage1_store<FM::STRIDED>(r, 0, lds, p.n_in, p.ktp, p.nt);
     lds_barrier();
 }
@@ -737,6 +758,70 @@ struct Q4kStepAsm {
     }
 };
 
+__device__ __forceinline__ u32 gload2u(const u8* ptr) {
+    u32 v;
+    asm volatile("global_load_ushort %0, %1, off" : "=v"(v) : "v"(ptr));
+    return v;
+}
+__device__ __forceinline__ u32 gload2us(const u8* base, u32 off) {
+    u32 v;
+    asm volatile("global_load_ushort %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+    return v;
+}
+
+// The same for the formats whose unit is 16 code bytes and the block's fp16 scale (TQ2_0: codes at
+// 16 (u & 3), scale at 64; IQ2_XXS: scale at 0, codes at 2 + 16 (u & 3)): two reads per unit.
+template <int F, int NITM>
+struct QdStepAsm {
+    static_assert(F == NMQ_TQ2_0 || F == NMQ_IQ2_XXS, "16 code bytes + fp16 scale per unit");
+    static constexpr int QO = F == NMQ_TQ2_0 ? 0 : 2, DO = F == NMQ_TQ2_0 ? 64 : 0;
+    typename Fmt<F>::Raw raw[NITM];
+    template <int T>
+    __device__ __forceinline__ void load(const RowMap& rm, int r, int lt, int U, int fb) {
+        const int rs = r < rm.n_out ? r : min(fb, rm.n_out - 1);
+        if constexpr (T == 64) {
+            const u8* rp = (const u8*)uniform64((int64_t)rm.row(rs));
+#pragma unroll
+            for (int it = 0; it < NITM; ++it) {
+                const int u = min(lt + it * T, U - 1);
+                const u32 ob = (u32)((u >> 2) * Fmt<F>::BB);
+                raw[it].q = gload16s(rp, ob + (u32)(QO + 16 * (u & 3)));
+                raw[it].d = gload2us(rp, ob + (u32)DO);
+            }
+        } else {
+            const u8* rp = rm.row(rs);
+#pragma unroll
+            for (int it = 0; it < NITM; ++it) {
+                const int u = min(lt + it * T, U - 1);
+                const u8* blk = rp + (u >> 2) * Fmt<F>::BB;
+                raw[it].q = gload16(blk + QO + 16 * (u & 3));
+                raw[it].d = gload2u(blk + DO);
+            }
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            if (it == 0)
+                asm volatile("s_waitcnt vmcnt(%2)" : "+v"(raw[it].q), "+v"(raw[it].d) : "n"(N));
+            else
+                asm volatile("" : "+v"(raw[it].q), "+v"(raw[it].d));
+        }
+    }
+};
+
+// Hand-issued step buffers per format (HandStep<F, NITM>::NL reads per unit).
+template <int F, int NITM>
+struct HandStep : QdStepAsm<F, NITM> {
+    static constexpr int NL = 2;
+};
+template <int NITM>
+struct HandStep<NMQ_Q4_K, NITM> : Q4kStepAsm<NITM> {
+    static constexpr int NL = 3;
+};
+constexpr bool hand_format(int f) { return f == NMQ_Q4_K || f == NMQ_TQ2_0 || f == NMQ_IQ2_XXS; }
+
 // Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
 struct LaneConst {
     Q4kLane q4k[4];  // Q4_K: the unit's scale/min selection
@@ -790,13 +875,13 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
 }
 
 // EXT: the variant that also takes segments and value input (the plain one keeps the shorter code).
-// HR (Q4_K; 1: two-stage input, 2: fp32 values): the weight reads are issued by hand (Q4kStepAsm, the compiler waits for all of a wave's
+// HR (Q4_K, TQ2_0, IQ2_XXS; 1: two-stage input, 2: fp32 values): the weight reads are issued by hand (Q4kStepAsm, the compiler waits for all of a wave's
 // outstanding reads at the head of its own loop) and the row results are held in registers (lane k of a
 // team: the team's k-th row), written when the team holds T of them (then every outstanding access is
 // waited for) and after the last row, so that the pipelined loop issues reads only.
 template <int F, int T, int RW, int NITM, int NBUF, bool EXT, int HR = 0>
 __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
-    static_assert(HR == 0 || (F == NMQ_Q4_K && RW == 1 && (HR == 1 || EXT)), "HR: Q4_K, one row per team");
+    static_assert(HR == 0 || (hand_format(F) && RW == 1 && (HR == 1 || EXT)), "HR: hand formats, one row per team");
     // HR = 1: the launcher guarantees two-stage input staged in one round; HR = 2: fp32 values (x_mode
     // NMQ_X_F32 or NMQ_X_F32_BF16) in at most two rounds
     args_early<EXT>(p);
@@ -820,7 +905,8 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     // NBUF step buffers rotate: while one step is computed, the next NBUF - 1 are in flight (the first
     // NBUF - 1 go out while the input is staged).
     Mv1Step<F, T, RW, NITM> buf[NBUF];
-    Q4kStepAsm<NITM> hb[NBUF];  // HR: the step buffers of the hand-issued reads
+    using HS = HandStep<hand_format(F) ? F : NMQ_Q4_K, NITM>;
+    HS hb[NBUF];  // HR: the step buffers of the hand-issued reads
     const int stride = nw * SR;
     int base = gw * SR;
     if constexpr (HR) {
@@ -828,8 +914,8 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 #pragma unroll
             for (int i = 0; i < NBUF - 1; ++i) hb[i].template load<T>(rm, base + i * stride + off, lt, U, base + off);
         };
-        if constexpr (HR == 1) stage1_hand<F, 3 * NITM * (NBUF - 1)>(lds, p, xrow, issue);
-        else stagev_hand<F, 3 * NITM * (NBUF - 1)>(lds, p, xrow, issue);
+        if constexpr (HR == 1) stage1_hand<F, HS::NL * NITM * (NBUF - 1)>(lds, tab, p, xrow, issue);
+        else stagev_hand<F, HS::NL * NITM * (NBUF - 1)>(lds, tab, p, xrow, issue);
     } else {
         stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] {
 #pragma unroll
@@ -856,7 +942,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
                     break;
                 }
                 hb[(i + NBUF - 1) % NBUF].template load<T>(rm, base + (NBUF - 1) * stride + off, lt, U, base + off);
-                hb[i].template wait<3 * NITM * (NBUF - 1)>();  // this step's reads; the NBUF - 1 later steps stay out
+                hb[i].template wait<HS::NL * NITM * (NBUF - 1)>();  // this step's reads; the later steps stay out
                 float acc = 0.f;
 #pragma unroll
                 for (int it = 0; it < NITM; ++it) {
@@ -899,7 +985,9 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 // PIPE = false: one row group per wave (the launch has at least as many waves as groups).  PIPE: waves
 // with several row groups request the next group's weights before computing the current one.
 // Q6_K unit against the input staged in LDS (stage_tile layout), one 16-value group at a time:
-// q6k_dot1 with the group's 2 x 16 input bytes and its xd read just before use.
+// q6k_dot1 with the group's 2 x 16 input bytes and its xd read just before use.  (Unsigned codes with a
+// per-group offset -32 (sum xq + sum xq2 / 254) formed once per workgroup took 14 % fewer VALU
+// instructions but an extra LDS pass and barrier: 14.2 against 13.8 us for 4096x14336, not kept.)
 __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const u8* base, int ktp, int u) {
     const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
     const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
@@ -912,7 +1000,8 @@ __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const int ph = swz<true>(16 * b + 8 * h + 2 * g + j);
+        const int ch = 16 * b + 8 * h + 2 * g + j;
+        const int ph = swz<true>(ch);
         const u32x4 a = *(const u32x4*)(base + 16 * ph);
         const u32x4 c = *(const u32x4*)(base + ktp + 16 * ph);
         const u32 xa[4] = {a.x, a.y, a.z, a.w};
@@ -921,9 +1010,10 @@ __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const u32 lo = (g & 1) ? lb[k] : la[k];
-            const u32 w = sub32x4(((lo >> (4 * (g >> 1))) & 0x0f0f0f0fu) | (((qh[k] >> (2 * g)) & 0x03030303u) << 4));
-            s1 = dot4(w, xa[k], s1);
-            s2 = dot4(w, xc[k], s2);
+            const u32 w = g == 0 ? q6k_codes<0>(lo, qh[k])
+                                 : (g == 1 ? q6k_codes<1>(lo, qh[k]) : (g == 2 ? q6k_codes<2>(lo, qh[k]) : q6k_codes<3>(lo, qh[k])));
+            s1 = dot4(sub32x4(w), xa[k], s1);
+            s2 = dot4(sub32x4(w), xc[k], s2);
         }
         const float ws = d * (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
         acc += ws * xdg[g] * ((float)s1 + FEIN * (float)s2);
@@ -1148,7 +1238,7 @@ inline MvKernel pick_mv1_ext(int nitm) {
 // 3 buffers)
 template <int F, int T, bool EXT, int HR>
 inline MvKernel pick_mv1_hr(int nitm) {
-    if constexpr (F != NMQ_Q4_K) return nullptr;
+    if constexpr (!hand_format(F)) return nullptr;
     else return nitm == 1 ? mv1_kernel<F, T, 1, 1, 3, EXT, HR> : mv1_kernel<F, T, 1, 2, 3, EXT, HR>;
 }
 template <int F, bool EXT, int HR>
@@ -1378,10 +1468,12 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
         if (s1.ok) {
             p.ktp = s1.ktp;
-            // Q4_K with the two-stage input staged in one round, or fp32 values in at most two: hand-issued
-            // reads (NMQ_MV1_HR=0 for the compiler-scheduled loop)
+            // Q4_K, TQ2_0, IQ2_XXS (with at least 256 threads: the grid table) with the two-stage input
+            // staged in one round, or fp32 values in at most two: hand-issued reads (NMQ_MV1_HR=0 for the
+            // compiler-scheduled loop)
             int hr = 0;
-            if (F == NMQ_Q4_K && s1.rw == 1 && s1.nbuf == 3 && s1.nitm <= 2 && env_int("NMQ_MV1_HR", 1) != 0) {
+            if (hand_format(F) && s1.rw == 1 && s1.nbuf == 3 && s1.nitm <= 2 && (F != NMQ_IQ2_XXS || s1.W >= 4) &&
+                env_int("NMQ_MV1_HR", 1) != 0) {
                 if (p.xv == nullptr) hr = s1.ktp / 16 <= 64 * s1.W ? 1 : 0;
                 else if (p.x_mode == NMQ_X_F32 || p.x_mode == NMQ_X_F32_BF16) hr = s1.ktp / 4 <= 2 * 64 * s1.W ? 2 : 0;
             }

@@ -1,9 +1,10 @@
-"""The Q4_K one-token kernels with hand-issued reads (mv1_kernel<..., HR = 1 or 2>) rely on the
+"""The one-token kernels with hand-issued reads (mv1_kernel<..., HR = 1 or 2>: Q4_K, TQ2_0, IQ2_XXS) rely on the
 compiler never touching a register whose read is still outstanding: the compiler does not see those
 reads, so a copy of such a register (which it could place at a branch join or to split a live range)
-would silently take a stale value.  This test compiles the Q4_K source to gfx950 assembly and checks,
+would silently take a stale value.  This test compiles the sources to gfx950 assembly and checks,
 for every such kernel, that between a hand-issued read and the wait that covers it no instruction
-reads or writes the read's destination registers.  (CPU only: hipcc cross-compiles.)"""
+reads or writes the read's destination registers.  (CPU only: hipcc cross-compiles the three sources
+in parallel.)"""
 import os
 import re
 import shutil
@@ -73,34 +74,44 @@ def hazards(asm: str, name: str):
     return found
 
 
+SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip")
+
+
 @pytest.fixture(scope="module")
-def q4k_asm(tmp_path_factory):
+def asm(tmp_path_factory):
     if not os.path.exists(HIPCC):
         pytest.skip("hipcc not found")
-    out = tmp_path_factory.mktemp("isa") / "q4k.s"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
-           "-packed-fp32-ops", "-fno-fast-math", "--cuda-device-only", "-S",
-           os.path.join(CSRC, "nmq_mv_q4_k.hip"), "-o", str(out)]
-    subprocess.run(cmd, check=True, cwd=CSRC, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL, timeout=600)
-    return out.read_text()
+    out = tmp_path_factory.mktemp("isa")
+    procs = {}
+    for src in SOURCES:
+        cmd = [HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+               "-packed-fp32-ops", "-fno-fast-math", "--cuda-device-only", "-S", os.path.join(CSRC, src),
+               "-o", str(out / (src + ".s"))]
+        procs[src] = subprocess.Popen(cmd, cwd=CSRC, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL)
+    for src, pr in procs.items():
+        assert pr.wait(timeout=900) == 0, src
+    return {src: (out / (src + ".s")).read_text() for src in SOURCES}
 
 
-def test_hand_read_kernels_exist(q4k_asm):
-    names = HAND_KERNEL.findall(q4k_asm)
+@pytest.mark.parametrize("src", SOURCES)
+def test_hand_read_kernels_exist(asm, src):
+    names = HAND_KERNEL.findall(asm[src])
     # T = 16/32/64 x one or two units per lane x (two-stage plain, two-stage ext, fp32 values)
     assert len(names) == 18, names
 
 
-def test_no_access_to_registers_of_outstanding_reads(q4k_asm):
-    bad = [h for n in HAND_KERNEL.findall(q4k_asm) for h in hazards(q4k_asm, n)]
+@pytest.mark.parametrize("src", SOURCES)
+def test_no_access_to_registers_of_outstanding_reads(asm, src):
+    bad = [h for n in HAND_KERNEL.findall(asm[src]) for h in hazards(asm[src], n)]
     assert not bad, bad[:5]
 
 
-def test_checker_finds_a_planted_read(q4k_asm):
+def test_checker_finds_a_planted_read(asm):
     """The check itself: a copy of a pending register placed right after a hand-issued read is found."""
-    name = HAND_KERNEL.findall(q4k_asm)[0]
-    start = q4k_asm.index(name + ":")
-    m = re.compile(r"global_load_dwordx4 v\[(\d+):\d+\]").search(q4k_asm, q4k_asm.index(";;#ASMSTART", start))
-    end = q4k_asm.index(";;#ASMEND", m.end()) + len(";;#ASMEND")
-    planted = q4k_asm[:end] + f"\n\tv_mov_b32_e32 v250, v{m.group(1)}\n" + q4k_asm[end:]
+    text = asm[SOURCES[0]]
+    name = HAND_KERNEL.findall(text)[0]
+    start = text.index(name + ":")
+    m = re.compile(r"global_load_dwordx4 v\[(\d+):\d+\]").search(text, text.index(";;#ASMSTART", start))
+    end = text.index(";;#ASMEND", m.end()) + len(";;#ASMEND")
+    planted = text[:end] + f"\n\tv_mov_b32_e32 v250, v{m.group(1)}\n" + text[end:]
     assert hazards(planted, name)

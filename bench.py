@@ -200,8 +200,10 @@ def run_configs(which, steps, warmup):
                 us, err = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup)
                 extra = {}
                 if n > 1:
-                    us4, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "0"})
-                    usm, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "2"})
+                    us4, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
+                                      {"NMQ_MVM": "0", "NMQ_MVT_MAX": "1"})
+                    usm, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
+                                      {"NMQ_MVM": "2", "NMQ_MVT_MAX": "1"})
                     extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
                 _record("speculative", f"Q4_K {rows}x4096 n={n}", "Q4_K", us, alg_bytes("Q4_K", rows, 4096, n), err,
                         **extra)

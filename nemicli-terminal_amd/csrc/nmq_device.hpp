@@ -277,6 +277,38 @@ __device__ __forceinline__ float q4k_dot1(const Fmt<NMQ_Q4_K>::Raw& r, const XSl
     return d * (sc0 * g0 + sc1 * g1) - dmin * (m0 * x.s[0] + m1 * x.s[1]);
 }
 
+// NC tokens at once (the same weights, NC inputs): the nibble unpacking, scales and mins shared, each
+// token's result formed by exactly the expression of q4k_dot1.
+template <int NC>
+__device__ __forceinline__ void q4k_dotn(const Fmt<NMQ_Q4_K>::Raw& r, const XSlice* x, const Q4kLane& c, float* o) {
+    const u32 sv = ((r.h.w >> c.sw) & c.ma) | ((r.h.y >> c.sy) & c.mb);
+    const u32 mv = ((r.h.w >> c.sm) & c.ma) | ((r.h.z >> c.sy) & c.mb);
+    const float sc0 = (float)(sv & 0xffu), sc1 = (float)((sv >> 8) & 0xffu);
+    const float m0 = (float)(mv & 0xffu), m1 = (float)((mv >> 8) & 0xffu);
+    const u32 q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    int a0[NC], a1[NC], b0[NC], b1[NC];
+#pragma unroll
+    for (int t = 0; t < NC; ++t) a0[t] = a1[t] = b0[t] = b1[t] = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const u32 lo = q[k] & 0x0f0f0f0fu, hn = (q[k] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+        for (int t = 0; t < NC; ++t) {
+            a0[t] = dot4(lo, x[t].q[k], a0[t]);
+            b0[t] = dot4(lo, x[t].q2[k], b0[t]);
+            a1[t] = dot4(hn, x[t].q[8 + k], a1[t]);
+            b1[t] = dot4(hn, x[t].q2[8 + k], b1[t]);
+        }
+    }
+    const float d = h2f(r.h.x), dmin = h2f(r.h.x >> 16);
+#pragma unroll
+    for (int t = 0; t < NC; ++t) {
+        const float g0 = (float)(__mul24(a0[t], 254) + b0[t]) * (x[t].d[0] * FEIN);
+        const float g1 = (float)(__mul24(a1[t], 254) + b1[t]) * (x[t].d[1] * FEIN);
+        o[t] = d * (sc0 * g0 + sc1 * g1) - dmin * (m0 * x[t].s[0] + m1 * x[t].s[1]);
+    }
+}
+
 // Q6_K, 210-byte blocks (quant.py:140-159, mmvq.py:421-482): unit u = 4b + 2h + j takes
 // l = 16j .. 16j+15 of half h: ql[64h + l], ql[64h + 32 + l], qh[32h + l]; runs k = 0..3 are the
 // values 128h + 32k + l with the int8 scales sc[8h + 2k + j].

@@ -978,6 +978,99 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     }
 }
 
+// ---- 2..4 tokens (speculative verification), Q4_K ----------------------------------------------------
+// The one-token kernel with hand-issued reads for NC tokens: all inputs staged in LDS (one round each,
+// read by hand ahead of the first weight steps), all slices held in registers, every weight unit
+// decoded once for all (q4k_dotn); a row's NC results stay in registers like the one-token loop's and
+// are written to y + t n_out.
+template <int T, int NC>
+__global__ __launch_bounds__(256) void mvt_kernel(MvParams p) {
+    args_early<false>(p);
+    constexpr int NITM = 1, NBUF = 3;
+    using FM = Fmt<NMQ_Q4_K>;
+    using HS = HandStep<NMQ_Q4_K, NITM>;
+    constexpr int P = 64 / T;
+    constexpr int HW = HS::NL * NITM * (NBUF - 1);
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
+    const int team = lane / T, lt = lane % T;
+    const RowMap rm = row_map<false>(p, p.w, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    const int gw = blockIdx.x * W + wave, nw = gridDim.x * W;
+    const int off = team;
+    const int stride = nw * P;
+    int base = gw * P;
+    const int tok = p.ktp * 9 / 4;  // LDS bytes per token
+    HS hb[NBUF];
+    {
+        XRound r[NC];
+        const int64_t g = p.n_in / 32;
+#pragma unroll
+        for (int t = 0; t < NC; ++t)
+            stage1_load_hand(r[t], 0, p.xq + t * p.n_in, p.xq2 + t * p.n_in, p.xd + t * g, p.xs + t * g, p.n_in, p.nt);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NBUF - 1; ++i) hb[i].template load<T>(rm, base + i * stride + off, lt, U, base + off);
+        __builtin_amdgcn_sched_barrier(0);
+        xround_wait<HW>(r[0]);
+#pragma unroll
+        for (int t = 1; t < NC; ++t) asm volatile("" : "+v"(r[t].a), "+v"(r[t].b), "+v"(r[t].d), "+v"(r[t].s));
+#pragma unroll
+        for (int t = 0; t < NC; ++t) stage1_store<FM::STRIDED>(r[t], 0, lds + t * tok, p.n_in, p.ktp, p.nt);
+        lds_barrier();
+    }
+    XSlice x[NC];
+    const int u = min(lt, U - 1);
+#pragma unroll
+    for (int t = 0; t < NC; ++t) read_slice<FM::STRIDED>(lds + t * tok, p.ktp, u, x[t]);
+    const LaneConst lc = lane_const<NMQ_Q4_K, T, NITM>(lt);
+    float res[NC];
+#pragma unroll
+    for (int t = 0; t < NC; ++t) res[t] = 0.f;
+    int k = 0, first = base;
+    bool more = true;
+    while (more) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            if (base >= p.n_out) {  // wave-uniform
+                more = false;
+                break;
+            }
+            hb[(i + NBUF - 1) % NBUF].template load<T>(rm, base + (NBUF - 1) * stride + off, lt, U, base + off);
+            hb[i].template wait<HW>();
+            float v[NC];
+            q4k_dotn<NC>(hb[i].raw[0], x, lc.q4k[0], v);
+#pragma unroll
+            for (int t = 0; t < NC; ++t) {
+                const float a = team_sum<T>(0.f + (lt < U ? v[t] : 0.f));
+                res[t] = lt == k ? a : res[t];
+            }
+            base += stride;
+            if (++k == T) {
+                const int r = first + lt * stride + off;
+                if (r < p.n_out) {
+#pragma unroll
+                    for (int t = 0; t < NC; ++t) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = res[t];
+                }
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                k = 0;
+                first = base;
+            }
+        }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the surplus reads of the last steps
+    const int r = first + lt * stride + off;
+    if (lt < k && r < p.n_out) {
+#pragma unroll
+        for (int t = 0; t < NC; ++t) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = res[t];
+    }
+}
+
+template <int NC>
+inline void (*pick_mvt(int T))(MvParams) {
+    return T == 16 ? mvt_kernel<16, NC> : (T == 32 ? mvt_kernel<32, NC> : mvt_kernel<64, NC>);
+}
+
 // ---- one token, long rows (more than 128 units of 64 values) ---------------------------------------
 // A wave owns whole rows (RW at a time, T = 64 lanes, NIT units per lane): all of a row group's weights
 // are requested at once; the input is staged once per workgroup in LDS and each unit's slice is read
@@ -1425,6 +1518,31 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             q.xs += (int64_t)8 * (p.n_in / 32);
             q.y += (int64_t)8 * p.n_out;
             return launch_mv<F>(q, nc - 8, n_mats, stream);
+        }
+    }
+    if constexpr (F == NMQ_Q4_K) {
+        // 2..NMQ_MVT_MAX (default 4) tokens of one matrix: the one-token kernel's loop for all of them
+        // (one unit per lane: rows of up to 4096 values; the NC input slices take about 65 + 34 NC VGPRs
+        // (133 for 2 tokens, 174 for 3, 227 for 4), so 4-wave workgroups at 12 waves per CU for 2 tokens,
+        // 8 for 3 and 4)
+        if (nc >= 2 && nc <= env_int("NMQ_MVT_MAX", 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
+            p.n_seg == 0) {
+            const int U = (p.n_in + 63) / 64;
+            const int T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+            const int P = 64 / T;
+            const int ktp = (p.n_in + 127) / 128 * 128;
+            const size_t lds = (size_t)nc * ktp * 9 / 4;
+            const int W = 4;
+            const int64_t steps = ((int64_t)p.n_out + P - 1) / P;
+            int64_t waves = (int64_t)env_int("NMQ_MVT_WPC", nc == 2 ? 12 : 8) * di.cus;
+            if (waves > steps) waves = steps;
+            if (U <= 64 && ktp / 16 <= 64 * W && lds <= (size_t)di.lds_max) {
+                p.ktp = ktp;
+                p.nt = 64 * W;
+                MvKernel k = nc == 2 ? pick_mvt<2>(T) : (nc == 3 ? pick_mvt<3>(T) : pick_mvt<4>(T));
+                hipLaunchKernelGGL(k, dim3((unsigned)((waves + W - 1) / W)), dim3(p.nt), lds, stream, p);
+                return (int)hipGetLastError();
+            }
         }
     }
     if (nc >= 2 && p.ids == nullptr) {

@@ -185,6 +185,7 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=61 + ks)
     from ggufengine_amd.gguf_types import TYPE_ID
     monkeypatch.setenv("NMQ_MVM", "2")   # the matrix-core path from 2 tokens on, whatever the format
+    monkeypatch.setenv("NMQ_MVT_MAX", "1")   # (not the few-token Q4_K kernel)
     monkeypatch.setenv("NMQ_MVM_TPW", str(tpw))
     monkeypatch.setenv("NMQ_MVM_KS", str(ks))
     for nc in (2, 7, 8, 12, 16):
@@ -349,6 +350,7 @@ def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=71)
     from ggufengine_amd.gguf_types import TYPE_ID
     monkeypatch.setenv("NMQ_MVM", "0")
+    monkeypatch.setenv("NMQ_MVT_MAX", "1")
     for nc in (2, 5, 8, 13):                   # 13: launches of 8 and 5
         x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
         e = quant_dev(dev(x))
@@ -621,3 +623,36 @@ def test_experts_values(nmq, oracle, two):
                                nmq.stream_ptr()))
     torch.cuda.synchronize()
     assert torch.equal(yd, ydr)
+
+
+@pytest.mark.parametrize("nc", [2, 3, 4])
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 4096), (1000, 2048), (513, 1024), (37, 256)])
+def test_few_tokens_equal_one_by_one(nmq, oracle, monkeypatch, shape, nc):
+    """2..4 tokens of Q4_K (speculative verification) in one launch of the few-token kernel (enabled up to
+    4 tokens here): each token's output equals the one-token launch on that token bit for bit (the same
+    decode and combine expression, one weight read for all), and the oracle within tolerance.  Covers
+    64, 32 and 16 lanes per row and row counts that leave the last steps partial."""
+    monkeypatch.setenv("NMQ_MVT_MAX", "4")
+    n_out, n_in = shape
+    raw = random_blocks("Q4_K", n_out * n_in // 256, seed=131 + n_in)
+    x = np.random.default_rng(132 + n_out + nc).standard_normal((nc, n_in)).astype(np.float32)
+    x[1, 5] = -25.0
+    say("few tokens", shape, nc)
+    e = quant_dev(dev(x))
+    w = dev(raw)
+    L = nmq.lib()
+    y2 = torch.empty(nc, n_out, dtype=torch.float32, device="cuda")
+    nmq.check(L.nmq_mv(12, w.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(),
+                       y2.data_ptr(), n_out, n_in, nc, nmq.stream_ptr()))
+    ys = []
+    for t in range(nc):
+        y1 = torch.empty(n_out, dtype=torch.float32, device="cuda")
+        g = n_in // 32
+        nmq.check(L.nmq_mv(12, w.data_ptr(), e.xq[t * n_in:].data_ptr(), e.xq2[t * n_in:].data_ptr(),
+                           e.xd[t * g:].data_ptr(), e.xs[t * g:].data_ptr(), y1.data_ptr(), n_out, n_in, 1,
+                           nmq.stream_ptr()))
+        ys.append(y1)
+    torch.cuda.synchronize()
+    for t in range(nc):
+        assert torch.equal(y2[t], ys[t]), (shape, nc, t)
+    _check_mv(oracle, "Q4_K", raw, n_out, n_in, x, y2)

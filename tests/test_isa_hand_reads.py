@@ -15,7 +15,7 @@ import pytest
 REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(REPO, "nemicli-terminal_amd", "csrc")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-HAND_KERNEL = re.compile(r"^(_ZN3nmq10mv1_kernel\w*Li[12]EEEvNS_8MvParamsE):", re.M)
+HAND_KERNEL = re.compile(r"^(_ZN3nmq10mv1_kernel\w*Li[12]EEEvNS_8MvParamsE|_ZN3nmq10mvt_kernel\w*EEEvNS_8MvParamsE):", re.M)
 
 
 def _vregs(op):
@@ -96,8 +96,12 @@ def asm(tmp_path_factory):
 @pytest.mark.parametrize("src", SOURCES)
 def test_hand_read_kernels_exist(asm, src):
     names = HAND_KERNEL.findall(asm[src])
-    # T = 16/32/64 x one or two units per lane x (two-stage plain, two-stage ext, fp32 values)
-    assert len(names) == 18, names
+    one = [n for n in names if "mv1_kernel" in n]
+    two = [n for n in names if "mvt_kernel" in n]
+    # one token: T = 16/32/64 x one or two units per lane x (two-stage plain, two-stage ext, fp32 values);
+    # 2..4 tokens (Q4_K): T = 16/32/64 x NC = 2, 3, 4
+    assert len(one) == 18, one
+    assert len(two) == (9 if "q4_k" in src else 0), two
 
 
 @pytest.mark.parametrize("src", SOURCES)

@@ -1563,7 +1563,10 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     // to 4096 rows of 4096 values, the persistent kernel from 12288 rows).
     const bool ext = p.n_seg > 0 || p.xv != nullptr;  // the kernel variant with segments / value input
     const int64_t rows_per_cu = ((int64_t)p.n_out * n_mats + di.cus - 1) / di.cus;
-    const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > 24 ? 2 : 1);
+    // rows per CU up to which chunk mode runs: 24 for one matrix, 64 for gathered experts (MoE layer at
+    // one token, both expert launches in chunk mode: 17.9 against 18.5 us; at 4 tokens both stay above)
+    const int mvc_max = env_int("NMQ_MVC_ROWS", n_mats > 1 ? 64 : 24);
+    const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > mvc_max ? 2 : 1);
     if (nc == 1 && mode == 1) {
         const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di);
         if (sc.ok) {

@@ -437,6 +437,21 @@ def main():
     ab = alg_bytes(fmt, rows, n_in)
     gbs = ab / (ms * 1e-3) / 1e9
 
+    # reference point on the same box: the runtime's device copy of the same weight bytes, one launch
+    # per copy, source and destination rotating over copies larger than the last-level cache (it reads
+    # and writes every byte: its rate counts both)
+    dsts = [torch.empty_like(base) for _ in range(copies)]
+    for i in range(20):
+        dsts[i % copies].copy_(ws[(i + 1) % copies])
+    torch.cuda.synchronize()
+    t0.record()
+    for i in range(200):
+        dsts[i % copies].copy_(ws[(i + 1) % copies])
+    t1.record()
+    torch.cuda.synchronize()
+    copy_us = t0.elapsed_time(t1) / 200 * 1e3
+    del dsts
+
     # parity of the timed kernel's output against the oracle (cheap, full size)
     import oracle
     ref = oracle.mv_deq(fmt, raw, rows, n_in, x.cpu().numpy()[None])
@@ -445,7 +460,9 @@ def main():
     cfg = {"workload": "Q4_K 14336x4096 mat-vec, batch 1 (Llama-3-8B ffn gate/up)", "format": fmt, "rows": rows,
            "n_in": n_in, "batch": 1, "weight_copies": copies, "algorithmic_bytes": ab,
            "us_per_matvec": round(ms * 1e3, 3), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-           "max_rel_err_vs_oracle": parity}
+           "max_rel_err_vs_oracle": parity,
+           "device_copy_same_bytes": {"us": round(copy_us, 3), "bytes_read_and_written": 2 * wb,
+                                      "GB/s": round(2 * wb / (copy_us * 1e-6) / 1e9, 1)}}
 
     # ---- one Llama-3-8B layer: 4 activation quantisations + 7 mat-vecs ----
     if not args.no_layer:

@@ -1467,7 +1467,10 @@ inline MvKernel pick_mvc(int T, int rw, bool ext) {
 // CU (per instance for expert batches): rows per workgroup R = ceil(rows / WGs), then the smallest
 // rows-per-team RW with R <= P*RW*16 (at most 16 waves, 8 when RW = 8), so every CU streams the
 // same number of rows and all of them are in flight at once.
-inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
+// values: the launch forms the input from values in its staging (more rounds the fewer threads a
+// workgroup has), else it reads the two-stage input.
+inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di, bool values = true,
+                          bool four_rows = false) {
     Mv1Shape s{};
     const int U = (n_in + 63) / 64;
     s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
@@ -1478,7 +1481,11 @@ inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     if (wgs < 1) wgs = 1;
     const int64_t R = ((int64_t)n_out + wgs - 1) / wgs;  // rows per workgroup
     int rw = env_int("NMQ_MVC_RW", 0);
-    if (rw <= 0) {
+    if (rw <= 0 && !values && four_rows) {
+        rw = 4;  // two-stage input, Q4_K / TQ2_0: 4 rows per team, fewer waves per workgroup (measured on
+                 // MI355X: Q4_K 4096x4096 4.1 against 4.7 us, TQ2_0 4.2 against 4.4 us; Q8_0 and IQ2_XXS
+                 // were slower)
+    } else if (rw <= 0) {
         rw = 1;
         while (rw < 8 && R > (int64_t)P * rw * 16) rw *= 2;
     }
@@ -1568,7 +1575,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     const int mvc_max = env_int("NMQ_MVC_ROWS", n_mats > 1 ? 64 : 24);
     const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > mvc_max ? 2 : 1);
     if (nc == 1 && mode == 1) {
-        const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di);
+        const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di, p.xv != nullptr, F == NMQ_Q4_K || F == NMQ_TQ2_0);
         if (sc.ok) {
             p.ktp = sc.ktp;
             MvKernel k = pick_mvc<F>(sc.T, sc.rw, ext);

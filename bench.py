@@ -388,7 +388,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark runs on exactly one GPU: the mat-vec path is single-GPU "
-                                   "(multi-GPU sharding by output rows is described in DESIGN.md, not built)",
+                                   "(sharding by output rows over several GPUs is not built)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.config != "headline":

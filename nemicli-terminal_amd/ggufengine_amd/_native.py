@@ -64,7 +64,7 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
 
 
 def lib() -> ctypes.CDLL:
-    """The loaded library; raises if it is missing (build it with __graft_entry__.build())."""
+    """The loaded library; raises if it is missing (build it with `make -C nemicli-terminal_amd/csrc`)."""
     global _lib, _load_error
     if _lib is None:
         with _lock:

@@ -1431,6 +1431,60 @@ inline MvlShape plan_mvl(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     return s;
 }
 
+// ---- 2..4 tokens, long rows (Q6_K: the layer's down projection) ---------------------------------------
+// The long-row kernel for NC tokens: one row per wave in 16-wave workgroups (one per CU with the NC
+// staged inputs, 32 KB each for 14336 values), all of the row's weights requested at once, every token's
+// input staged in LDS (one round each, read before the weight reads, stored after them), and each
+// token's sum formed exactly as the one-token long-row kernel forms it (q6k_dot1_lds per unit, added in
+// unit order, team_sum): every output equals the one-token launch on that token bit for bit.
+template <int NC, int NIT>
+__global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
+    args_early<false>(p);
+    constexpr int F = NMQ_Q6_K;
+    using FM = Fmt<F>;
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
+    const RowMap rm = row_map<false>(p, p.w, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    const int row = blockIdx.x * W + wave;
+    const int tok = p.ktp * 9 / 4;  // LDS bytes per token
+    Mv1Step<F, 64, 1, NIT> a;
+    {
+        XRound r[NC];
+        const int64_t g = p.n_in / 32;
+#pragma unroll
+        for (int t = 0; t < NC; ++t)
+            stage1_load(r[t], 0, p.xq + t * p.n_in, p.xq2 + t * p.n_in, p.xd + t * g, p.xs + t * g, p.n_in, p.nt);
+        __builtin_amdgcn_sched_barrier(0);  // the input reads ahead of the weight reads
+        a.load(rm, row, lane, U, row);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NC; ++t) stage1_store<FM::STRIDED>(r[t], 0, lds + t * tok, p.n_in, p.ktp, p.nt);
+        lds_barrier();
+    }
+    if (row >= p.n_out) return;  // wave-uniform, after the workgroup's last barrier
+    float acc[NC];
+#pragma unroll
+    for (int t = 0; t < NC; ++t) acc[t] = 0.f;
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) {
+        const int u = lane + it * 64;
+        const int uc = min(u, U - 1);
+#pragma unroll
+        for (int t = 0; t < NC; ++t) {
+            const float v = q6k_dot1_lds(a.raw[0][it], lds + t * tok, p.ktp, uc);
+            acc[t] += u < U ? v : 0.f;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // one unit's input slices live at a time
+    }
+#pragma unroll
+    for (int t = 0; t < NC; ++t) acc[t] = team_sum<64>(acc[t]);
+    if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NC; ++t) gpw<float>(p.y)[(int64_t)t * p.n_out + row] = acc[t];
+    }
+}
+
 template <int F, bool EXT>
 inline MvKernel pick_mvl_e(int nit, bool pipe) {
     if (nit == 3) return pipe ? mvl_kernel<F, 1, 3, true, EXT> : mvl_kernel<F, 1, 3, false, EXT>;
@@ -1550,6 +1604,26 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
                 p.nt = 64 * W;
                 MvKernel k = nc == 2 ? pick_mvt<2>(T) : (nc == 3 ? pick_mvt<3>(T) : pick_mvt<4>(T));
                 hipLaunchKernelGGL(k, dim3((unsigned)((waves + W - 1) / W)), dim3(p.nt), lds, stream, p);
+                return (int)hipGetLastError();
+            }
+        }
+    }
+    if constexpr (F == NMQ_Q6_K) {
+        // 2..4 tokens of one matrix with long rows (129..256 units): the long-row loop for all of them
+        if (nc >= 2 && nc <= env_int("NMQ_MVLT_MAX", 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
+            p.n_seg == 0) {
+            const int U = (p.n_in + 63) / 64;
+            const int ktp = (p.n_in + 127) / 128 * 128;
+            const size_t lds = (size_t)nc * ktp * 9 / 4;
+            const int W = 16;
+            if (U > 128 && U <= 256 && ktp / 16 <= 64 * W && lds + 4096 <= (size_t)di.lds_max_big) {
+                p.ktp = ktp;
+                p.nt = 64 * W;
+                const bool n3 = U <= 192;  // units per lane: 3 or 4
+                MvKernel k = nc == 2 ? (n3 ? mvlt_kernel<2, 3> : mvlt_kernel<2, 4>)
+                           : nc == 3 ? (n3 ? mvlt_kernel<3, 3> : mvlt_kernel<3, 4>)
+                                     : (n3 ? mvlt_kernel<4, 3> : mvlt_kernel<4, 4>);
+                hipLaunchKernelGGL(k, dim3((unsigned)((p.n_out + W - 1) / W)), dim3(p.nt), lds, stream, p);
                 return (int)hipGetLastError();
             }
         }

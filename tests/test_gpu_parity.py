@@ -656,3 +656,34 @@ def test_few_tokens_equal_one_by_one(nmq, oracle, monkeypatch, shape, nc):
     for t in range(nc):
         assert torch.equal(y2[t], ys[t]), (shape, nc, t)
     _check_mv(oracle, "Q4_K", raw, n_out, n_in, x, y2)
+
+
+@pytest.mark.parametrize("nc", [2, 3, 4])
+@pytest.mark.parametrize("shape", [(4096, 14336), (1000, 8448), (37, 16384)])
+def test_few_tokens_long_rows_equal_one_by_one(nmq, oracle, shape, nc):
+    """2..4 tokens of Q6_K with long rows (the layer's down projection) in one launch of the few-token
+    long-row kernel: each token's output equals the one-token launch on that token bit for bit, and the
+    oracle within tolerance.  Covers 3 and 4 units per lane and a last workgroup with idle waves."""
+    n_out, n_in = shape
+    raw = random_blocks("Q6_K", n_out * n_in // 256, seed=141 + n_in)
+    x = np.random.default_rng(142 + n_out + nc).standard_normal((nc, n_in)).astype(np.float32)
+    x[nc - 1, 9] = 40.0
+    say("few tokens long rows", shape, nc)
+    e = quant_dev(dev(x))
+    w = dev(raw)
+    L = nmq.lib()
+    yn = torch.empty(nc, n_out, dtype=torch.float32, device="cuda")
+    nmq.check(L.nmq_mv(14, w.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(),
+                       yn.data_ptr(), n_out, n_in, nc, nmq.stream_ptr()))
+    g = n_in // 32
+    ys = []
+    for t in range(nc):
+        y1 = torch.empty(n_out, dtype=torch.float32, device="cuda")
+        nmq.check(L.nmq_mv(14, w.data_ptr(), e.xq[t * n_in:].data_ptr(), e.xq2[t * n_in:].data_ptr(),
+                           e.xd[t * g:].data_ptr(), e.xs[t * g:].data_ptr(), y1.data_ptr(), n_out, n_in, 1,
+                           nmq.stream_ptr()))
+        ys.append(y1)
+    torch.cuda.synchronize()
+    for t in range(nc):
+        assert torch.equal(yn[t], ys[t]), (shape, nc, t)
+    _check_mv(oracle, "Q6_K", raw, n_out, n_in, x, yn)

@@ -208,6 +208,18 @@ def run_configs(which, steps, warmup):
                 _record("speculative", f"Q4_K {rows}x4096 n={n}", "Q4_K", us, alg_bytes("Q4_K", rows, 4096, n), err,
                         **extra)
             del ws
+        # the layer's down projection under the same verification: Q6_K 4096x14336 (seed 27), n in 1..4
+        raw = make_weights("Q6_K", 4096, 14336, 27)
+        ws = _copies(torch.from_numpy(raw).cuda())
+        X = _x(29, (4, 14336))
+        for n in (1, 2, 3, 4):
+            us, err = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup)
+            extra = {}
+            if n > 1:
+                usg, _ = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup, {"NMQ_MVLT_MAX": "1"})
+                extra = {"us_without_few_token_kernel": round(usg, 3)}
+            _record("speculative", f"Q6_K 4096x14336 n={n}", "Q6_K", us, alg_bytes("Q6_K", 4096, 14336, n), err, **extra)
+        del ws
 
     if which in ("q4_0", "all"):
         # Q4_0 (no workload of its own among the headline configurations): W ~N(0,0.02) (seed 61),

@@ -102,8 +102,9 @@ int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, i
 
 /*
  * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of up to 2 * NMQ_MAX_COLS
- * tokens on the matrix cores, NMQ_MAX_COLS on the dot4 kernels).  Q4_K with 2..4 tokens and rows of up
- * to 4096 values: every token's output equals the ncols = 1 call on that token bit for bit.
+ * tokens on the matrix cores, NMQ_MAX_COLS on the dot4 kernels).  2..4 tokens of Q4_K with rows of up
+ * to 4096 values, or of Q6_K with rows of 8K..16K values: every token's output equals the ncols = 1 call
+ * on that token bit for bit.
  * w: n_out rows of n_in values in GGUF block format, rows back to back.  Token c's two-stage input
  * lies at xq + c*n_in, xq2 + c*n_in, xd + c*n_in/32, xs + c*n_in/32 (the layout of an Eingang of
  * ncols rows).  y: fp32, token-major (ncols x n_out).

@@ -12,7 +12,7 @@ gfx950 device, and calls raise.
 
 Differences from the reference (documented, same results within the parity tolerance):
   - up to 16 tokens per launch on the int8 matrix cores, SPALTEN = 8 on the dot4 kernels (the
-    reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for Q4_K and 2
+    reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for Q4_K and 4
     for Q6_K, measured on MI355X (the reference: 16);
   - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs on the fp16 matrix
     cores with exact integer weights and a two-stage fp16 input (about 22 bits against the
@@ -40,8 +40,9 @@ SPALTEN = _native.MAX_COLS    # tokens (input rows) per launch, weights read onc
 ZEILEN_JE_WARP = {"Q4_K": lambda nc: 1 if nc == 1 else 2, "Q6_K": lambda nc: 1 if nc == 1 else 2}
 # Most tokens per call for the int8 mat-vec kernels; from one more token on, callers take `mm` (the fp16
 # matrix cores).  Measured on MI355X (14336x4096, 4096x4096 Q4_K and 4096x14336 Q6_K): the reference's
-# 16 / 16 (mmvq.py:32) become 8 / 2 here.
-MMVQ_BIS = {"Q4_K": 8, "Q6_K": 2}
+# 16 / 16 (mmvq.py:32) become 8 / 4 here (Q6_K 4096x14336 through mv / mm: 2-4 tokens 22-26 / 35-36 us,
+# 5 tokens 51 / 36 us).
+MMVQ_BIS = {"Q4_K": 8, "Q6_K": 4}
 MMQ_BIS = {"Q4_K": 112, "Q6_K": 112}
 
 

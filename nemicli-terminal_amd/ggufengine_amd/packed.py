@@ -10,8 +10,9 @@ number of input rows M exactly as `PackedLinear._rechnen` does (common.py:400-43
   - else: W unpacked to the compute dtype piecewise (ZEILEN_JE_STUECK values at a time) and multiplied.
 
 Every branch runs on libnmq's HIP kernels (the unpack too); without the library the constructor
-raises instead of falling back.  Streaming weights from pinned host memory (`im_ram`, `band`) is not
-part of this library.
+raises instead of falling back.  Weights in pinned RAM (`hostmem`): `im_ram` is set and the kernels
+read them over PCIe, or, with a `band` (band.Fliessband) and the layer's number `nr` on it, each call
+computes on the matrix copied whole into a VRAM slot a few layers ahead (reference common.py:387-399).
 """
 from __future__ import annotations
 
@@ -19,7 +20,8 @@ from typing import Optional
 
 import torch
 
-from . import _native, cudakern, mmvq
+from . import _native, cudakern, hostmem, mmvq
+from .band import Fliessband
 from .gguf_types import GGML_TYPES, GGUFError
 from .mmvq import _starten
 
@@ -59,11 +61,19 @@ class PackedLinear:
         self.kernel = cudakern.verfuegbar(raw.device, name, n_in)
         self.mmvq = name in mmvq.FORMATE and mmvq.verfuegbar(raw.device, name, n_in)
         self.mm_bis = min(self.KERNEL_BIS, cudakern.mm_bis(raw.device)) if self.kernel else 1
-        self.im_ram = False
+        self.im_ram = hostmem.abgebildet(raw)    # pinned RAM, read over PCIe
+        self.band: Optional[Fliessband] = None   # with it: whole copies a few matrices ahead
+        self.nr = -1
         self._nullen: dict = {}
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
-        return self._rechnen(x, self.raw)
+        if self.band is None:
+            return self._rechnen(x, self.raw)
+        roh = self.band.holen(self.nr).view(1, -1)
+        try:
+            return self._rechnen(x, roh)
+        finally:
+            self.band.fertig(self.nr)
 
     def _rechnen(self, x: torch.Tensor, raw: torch.Tensor) -> torch.Tensor:
         x2 = x.reshape(-1, self.n_in)

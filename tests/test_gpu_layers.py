@@ -459,3 +459,55 @@ def test_experts_in_pinned_ram_with_vram_slots(nmq, oracle):
     assert hostmem.pending() >= 1
     hostmem.flush()
     assert hostmem.pending() == 0
+
+
+def test_packed_linear_band_from_pinned_ram(nmq):
+    """Layers whose weights live in pinned RAM, computed through a Fliessband (4 VRAM slots filled by
+    whole-matrix copies a few layers ahead on a copy stream, ordered by events only): over several
+    passes, eagerly and as a HIP graph replayed with eager passes between the replays, every output
+    equals the same layers held in VRAM bit for bit.  Seven layers of two formats and sizes, so the
+    ring wraps within a pass."""
+    from ggufengine_amd import band, hostmem, packed
+    specs = [("Q4_K", 12, 512, 1024), ("Q6_K", 14, 256, 2048), ("Q4_K", 12, 768, 1024), ("Q8_0", 8, 256, 1024),
+             ("Q4_K", 12, 512, 2048), ("Q6_K", 14, 512, 1024), ("Q4_K", 12, 256, 1024)]
+    fl = band.Fliessband("cuda")
+    vram, ram, xs = [], [], []
+    rng = np.random.default_rng(171)
+    say("band layers", len(specs))
+    for i, (fmt, tid, n_out, n_in) in enumerate(specs):
+        raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=172 + i)
+        vram.append(packed.PackedLinear(dev(raw), tid, n_out, n_in, dtype=torch.float32))
+        host = hostmem.empty(raw.size, "cuda")
+        host.numpy()[:] = raw
+        lay = packed.PackedLinear(hostmem.abbilden(host, "cuda"), tid, n_out, n_in, dtype=torch.float32)
+        assert lay.im_ram
+        lay.band, lay.nr = fl, fl.anmelden(host)
+        ram.append(lay)
+        xs.append(dev(rng.standard_normal((1, n_in)).astype(np.float32)))
+    want = [lay(x) for lay, x in zip(vram, xs)]
+
+    def one_pass():
+        return [lay(x) for lay, x in zip(ram, xs)]
+
+    for _ in range(3):
+        got = one_pass()
+        torch.cuda.synchronize()
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert torch.equal(g, w), i
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        one_pass()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = one_pass()
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (o, w) in enumerate(zip(outs, want)):
+            assert torch.equal(o, w), (rep, i)
+        got = one_pass()                          # eager work between the replays
+        torch.cuda.synchronize()
+        for i, (o, w) in enumerate(zip(got, want)):
+            assert torch.equal(o, w), ("eager", rep, i)

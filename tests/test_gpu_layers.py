@@ -511,3 +511,37 @@ def test_packed_linear_band_from_pinned_ram(nmq):
         torch.cuda.synchronize()
         for i, (o, w) in enumerate(zip(got, want)):
             assert torch.equal(o, w), ("eager", rep, i)
+
+
+@pytest.mark.parametrize("L", [1, 4])
+def test_expert_layer_with_experts_in_pinned_ram(nmq, L):
+    """The whole expert layer (Experten: gate and up in one launch, down, combine) with all three parts'
+    experts in pinned RAM behind one ExpertenLager (4 VRAM slots per part, address tables read by the
+    kernels): equal bit for bit to the layer on VRAM experts, before and after the slots are re-sorted."""
+    from ggufengine_amd import experts, hostmem
+    n_exp, k, E, FF = 16, 4, 1024, 512
+    raws = [random_blocks("Q4_K", n_exp * FF * E // 256, seed=181), random_blocks("Q4_K", n_exp * FF * E // 256, seed=182),
+            random_blocks("Q6_K", n_exp * E * FF // 256, seed=183)]
+    shapes = [(12, FF, E), (12, FF, E), (14, E, FF)]
+
+    def part(raw, shape, in_ram):
+        t, n_out, n_in = shape
+        if not in_ram:
+            return experts.PackedExperts(dev(raw), t, n_exp, n_out, n_in)
+        host = hostmem.empty(raw.size, "cuda")
+        host.numpy()[:] = raw
+        return experts.PackedExperts(hostmem.abbilden(host, "cuda"), t, n_exp, n_out, n_in)
+
+    vram = experts.Experten(*[part(r, s, False) for r, s in zip(raws, shapes)])
+    ram_parts = [part(r, s, True) for r, s in zip(raws, shapes)]
+    ram = experts.Experten(*ram_parts)
+    lager = experts.ExpertenLager(ram_parts, plaetze=4, device="cuda")
+    rng = np.random.default_rng(184 + L)
+    x = dev(rng.standard_normal((L, E)).astype(np.float32))
+    idx, w = experts.auswahl(dev(rng.standard_normal((L, n_exp)).astype(np.float32)), k)
+    say("expert layer in RAM", L)
+    want = vram(x, idx, w)
+    assert torch.equal(ram(x, idx, w), want)
+    lager.zaehlen(idx)
+    lager.umsortieren()
+    assert torch.equal(ram(x, idx, w), want)

@@ -256,6 +256,9 @@ def run_configs(which, steps, warmup):
     if which in ("prefill", "all"):
         run_prefill(L, stream, steps, warmup)
 
+    if which in ("offload",):
+        run_offload(steps, warmup, len(os.sched_getaffinity(0)))
+
     if which in ("moe", "all"):
         run_moe(steps, warmup, threads)
 
@@ -300,6 +303,94 @@ def run_prefill(L, stream, steps, warmup):
             _record("prefill", f"{fmt} {rows}x{n_in} n={n}", fmt, us, ab, err, us_with_input=round(us + us_in, 3),
                     us_int8_path=round(us_int8, 3), tokens_per_s=round(n / ((us + us_in) * 1e-6)))
         del ws
+
+
+def run_offload(steps, warmup, threads):
+    """Weights in pinned RAM.  (a) The expert layer of run_moe at one token with all experts in RAM
+    (hostmem, read over PCIe through the address tables) against the same experts in VRAM, eager calls.
+    The VRAM figures read the same 8 experts (2.6 MB) on every call, so they are cache-warm; the RAM
+    figure crosses PCIe on every call (host memory is not cached by the GPU).
+    (b) A pass over 8 Q4_K 4096x4096 layers (9.4 MB each, the same generator) streamed through a
+    Fliessband (4 VRAM slots, whole copies a few layers ahead) against the same layers in VRAM; the
+    copy rate is the weight bytes of the pass over its time.  Every result is checked equal to the
+    VRAM one bit for bit before timing.  The RAM paths get at least half a second of warm-up: PCIe
+    reads and copies of fresh pinned blocks run about a fifth slower during their first ~0.5 s."""
+    import numpy as np
+    import torch
+    from ggufengine_amd import band, encode, experts, hostmem, packed
+    dev = torch.device("cuda", 0)
+    n_exp, k, E, FF = 128, 8, 2048, 768
+    g = np.random.Generator(np.random.PCG64(41))
+
+    def enc(fmt, rows, n_in, n=n_exp):
+        w = g.standard_normal(n * rows * n_in, dtype=np.float32) * np.float32(0.02)
+        return encode.encode(fmt, w, threads=threads)
+
+    def pinned(raw):
+        h = hostmem.empty(raw.size, dev)
+        h.numpy()[:] = raw
+        return h
+
+    def timed(fn, reps, warm):
+        for _ in range(warm):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(reps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / reps * 1e3
+
+    raw = {"gate": enc("Q4_K", FF, E), "up": enc("Q4_K", FF, E), "down": enc("Q6_K", E, FF)}
+    shapes = {"gate": (12, FF, E), "up": (12, FF, E), "down": (14, E, FF)}
+    hosts = {n: pinned(r) for n, r in raw.items()}
+    names = ("gate", "up", "down")
+    ram_parts = [experts.PackedExperts(hostmem.abbilden(hosts[n], dev), shapes[n][0], n_exp, *shapes[n][1:])
+                 for n in names]
+    in_ram = experts.Experten(*ram_parts)
+    in_vram = experts.Experten(*[experts.PackedExperts(torch.from_numpy(raw[n]).to(dev), shapes[n][0], n_exp,
+                                                       *shapes[n][1:]) for n in names])
+    logits = torch.from_numpy(_x(42, (1, n_exp))).to(dev)
+    x = torch.from_numpy(_x(43, (1, E))).to(dev)
+    idx, w = experts.auswahl(logits, k)
+    assert torch.equal(in_ram(x, idx, w), in_vram(x, idx, w))
+    us_ram = timed(lambda: in_ram(x, idx, w), steps, max(warmup, 1000))
+    us_vram = timed(lambda: in_vram(x, idx, w), steps, warmup)
+    # the routed experts moved into VRAM slots (ExpertenLager, 8 slots per part): kernels read the slots
+    lager = experts.ExpertenLager(ram_parts, plaetze=k, device=dev)
+    lager.zaehlen(idx)
+    lager.umsortieren()
+    assert torch.equal(in_ram(x, idx, w), in_vram(x, idx, w))
+    us_slots = timed(lambda: in_ram(x, idx, w), steps, warmup)
+    moved = k * sum(r.size for r in raw.values()) // n_exp
+    _record("offload", "128 experts top-8, 1 token, experts in pinned RAM", "Q4_K+Q6_K", us_ram, moved, None,
+            us_experts_in_vram=round(us_vram, 3), us_routed_experts_in_vram_slots=round(us_slots, 3),
+            pcie_GBs=round(moved / (us_ram * 1e-6) / 1e9, 1), equal_to_vram=True, timing="eager calls (all three)")
+    del in_ram, in_vram, ram_parts, lager, hosts
+
+    n_lay, rows, n_in = 8, 4096, 4096
+    raws = [enc("Q4_K", rows, n_in, 1) for _ in range(n_lay)]
+    fl = band.Fliessband(dev)
+    ram_l, vram_l, keep = [], [], []
+    for r in raws:
+        h = pinned(r)
+        keep.append(h)
+        lay = packed.PackedLinear(hostmem.abbilden(h, dev), 12, rows, n_in, dtype=torch.float32)
+        lay.band, lay.nr = fl, fl.anmelden(h)
+        ram_l.append(lay)
+        vram_l.append(packed.PackedLinear(torch.from_numpy(r).to(dev), 12, rows, n_in, dtype=torch.float32))
+    xs = torch.from_numpy(_x(62, (1, n_in))).to(dev)
+    for a, b in zip(ram_l, vram_l):
+        assert torch.equal(a(xs), b(xs))
+    us_band = timed(lambda: [lay(xs) for lay in ram_l], max(20, steps // 10), max(warmup, 300))
+    us_vram = timed(lambda: [lay(xs) for lay in vram_l], max(20, steps // 10), warmup)
+    moved = sum(r.size for r in raws)
+    _record("offload", "8 Q4_K 4096x4096 layers through the band (pinned RAM -> 4 VRAM slots)", "Q4_K", us_band,
+            moved, None, us_layers_in_vram=round(us_vram, 3), copy_GBs=round(moved / (us_band * 1e-6) / 1e9, 1),
+            equal_to_vram=True, timing="eager calls (both)")
+    hostmem.flush()
 
 
 def run_moe(steps, warmup, threads):
@@ -393,7 +484,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
     ap.add_argument("--config", default="headline",
-                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "all"),
+                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "offload", "all"),
                     help="headline (default): the metric line; the others print one record per case of "
                          "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, "
                          "16..112 tokens on the fp16 matrix cores, MoE)")

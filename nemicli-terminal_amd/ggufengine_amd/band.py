@@ -2,9 +2,10 @@
 Whole matrices streamed from pinned RAM into a ring of VRAM slots: the reference's `Fliessband`
 (models/common.py:295-361), used by `PackedLinear` for weights kept in RAM (`hostmem`).
 
-One large copy per matrix runs at full PCIe speed, where kernels reading RAM over PCIe reach about
-half of it; so each matrix is copied whole, on a copy stream of its own (default priority), a few
-matrices ahead of its use.  Matrices are numbered in the order they are registered, which is their
+Each matrix is copied whole, on a copy stream of its own (default priority), a few matrices ahead
+of its use, so a matrix read more than once (several tokens, prefill) is read from VRAM.  On MI355X
+a lone copy from pinned RAM runs at 54 GB/s and a pass over 8 Q4_K 4096x4096 layers through the ring
+at 44.6 GB/s; kernels reading RAM directly reach 52 GB/s.  Matrices are numbered in the order they are registered, which is their
 order of use in a forward pass; a number not above the previous one starts a new pass.  Ordering is
 by events only (no host synchronisation), so the band also runs inside a HIP graph capture:
 

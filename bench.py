@@ -6,7 +6,9 @@ Llama-3-8B decoder layer) -- GB/s of algorithmic bytes, % of the 8 TB/s HBM peak
 plus us per Llama-3-8B layer: the 7 mat-vecs on their 4 fp32 inputs in 5 launches (q, k, v in one
 nmq_mv_x launch, gate and up in another, o, each quantising its 4096-value input itself; the down
 input quantised by its own launch), checked against the oracle.  Beside it: the same layer with 4 quantisation launches and nmq_mv_multi
-(us_per_layer_multi), and with one launch per matrix (us_per_layer_separate).
+(us_per_layer_multi), and with one launch per matrix (us_per_layer_separate); the layer and the layer
+with its inputs formed (us_per_layer_fused_inputs) also as HIP graphs of 1 and 32 layers, replayed
+(us_per_layer_graph*).
 
 A "step" is one launch of the mat-vec kernel over one token whose two-stage int8 input (Eingang) is
 already resident in HBM.  The weight matrix of each step is one of several identical copies whose
@@ -590,7 +592,7 @@ def main():
             return (f, k, [lw[n].data_ptr() for n in names], [spec[n][2] for n in names],
                     [ys[n].data_ptr() for n in names])
 
-        def one_layer(li, how):
+        def one_layer(li, how, st=stream):
             """The 7 mat-vecs and their 4 inputs.  how = "separate": each input quantised by nmq_quant_q8,
             one nmq_mv launch per matrix; "multi": the matrices of one input (q, k, v and gate, up) in
             one nmq_mv_multi launch; "values": the launches on 4096-value inputs take the fp32 input
@@ -603,17 +605,17 @@ def main():
                 if how == "values" and k <= VALUES_MAX_N_IN:
                     _native.check(L.nmq_mv_x(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
                                              (ctypes.c_void_p * m)(*yp), xin[inp].data_ptr(), _native.X_F32, None,
-                                             k, stream))
+                                             k, st))
                     continue
                 ei = eg[inp]
                 ep = (ei.xq.data_ptr(), ei.xq2.data_ptr(), ei.xd.data_ptr(), ei.xs.data_ptr())
-                _native.check(L.nmq_quant_q8(xin[inp].data_ptr(), 1, *ep, ei.n, stream))
+                _native.check(L.nmq_quant_q8(xin[inp].data_ptr(), 1, *ep, ei.n, st))
                 if how != "separate" and m > 1:
                     _native.check(L.nmq_mv_multi(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
-                                                 (ctypes.c_void_p * m)(*yp), *ep, k, stream))
+                                                 (ctypes.c_void_p * m)(*yp), *ep, k, st))
                 else:
                     for w_, r_, y_ in zip(wp, rows_, yp):
-                        _native.check(L.nmq_mv(TYPE[f], w_, *ep, y_, r_, k, 1, stream))
+                        _native.check(L.nmq_mv(TYPE[f], w_, *ep, y_, r_, k, 1, st))
 
         reps = max(20, args.steps // 10)
         for how in ("separate", "multi", "values"):
@@ -629,6 +631,37 @@ def main():
             if how != "values":
                 cfg[f"us_per_layer_{how}"] = round(us_layer, 3)
         cfg["us_per_layer"] = round(us_layer, 3)
+
+        def graph_us(fn, per=1):
+            """fn(li, stream) for `per` consecutive layers captured as one HIP graph, one graph per weight
+            copy, the graphs replayed in turn: the one-token step as the reference runs it (captured,
+            replayed).  The first replay is checked against the eager outputs.  us per layer."""
+            graphs = []
+            for j in range(nl):
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for q in range(per):
+                        fn(j + q, torch.cuda.current_stream().cuda_stream)
+                graphs.append(gr)
+            fn(per - 1, stream)
+            torch.cuda.synchronize()
+            eager = {n: y.clone() for n, y in ys.items()}
+            graphs[0].replay()
+            torch.cuda.synchronize()
+            assert all(torch.equal(eager[n], ys[n]) for n in ys), "graph replay differs from the eager layer"
+            for i in range(max(5, args.warmup // 10)):
+                graphs[i % nl].replay()
+            torch.cuda.synchronize()
+            n_rep = max(5, reps // per)
+            t0.record()
+            for i in range(n_rep):
+                graphs[i % nl].replay()
+            t1.record()
+            torch.cuda.synchronize()
+            return round(t0.elapsed_time(t1) / (n_rep * per) * 1e3, 3)
+
+        cfg["us_per_layer_graph"] = graph_us(lambda j, st: one_layer(j, "values", st))
+        cfg["us_per_layer_graph_32_layers"] = graph_us(lambda j, st: one_layer(j, "values", st), 32)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
         # the layer's outputs (last step, value input; the weight copies are identical) against
@@ -657,29 +690,29 @@ def main():
         def ptrs(e):
             return e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr()
 
-        def mv_named(lw, name, ei):
+        def mv_named(lw, name, ei, st):
             _, f, r, k, _, _ = next(t for t in LAYER if t[0] == name)
-            _native.check(L.nmq_mv(TYPE[f], lw[name].data_ptr(), *ptrs(ei), ys[name].data_ptr(), r, k, 1, stream))
+            _native.check(L.nmq_mv(TYPE[f], lw[name].data_ptr(), *ptrs(ei), ys[name].data_ptr(), r, k, 1, st))
 
-        def mv_shared(lw, names, ei):
+        def mv_shared(lw, names, ei, st):
             f, k, wp, rows_, yp = mats_of(lw, names)
             m = len(names)
             _native.check(L.nmq_mv_multi(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
-                                         (ctypes.c_void_p * m)(*yp), *ptrs(ei), k, stream))
+                                         (ctypes.c_void_p * m)(*yp), *ptrs(ei), k, st))
 
-        def step_layer(li):
+        def step_layer(li, st=stream):
             lw = layers[li % nl]
             _native.check(L.nmq_norm_q8(h_s.data_ptr(), None, 1.0, None, nw_s.data_ptr(), 1e-5, xn_s.data_ptr(),
-                                        *ptrs(eg["x_attn"]), E, stream))
-            mv_shared(lw, ("q", "k", "v"), eg["x_attn"])
-            _native.check(L.nmq_quant_q8(xin["attn_out"].data_ptr(), 1, *ptrs(eg["attn_out"]), E, stream))
-            mv_named(lw, "o", eg["attn_out"])
+                                        *ptrs(eg["x_attn"]), E, st))
+            mv_shared(lw, ("q", "k", "v"), eg["x_attn"], st)
+            _native.check(L.nmq_quant_q8(xin["attn_out"].data_ptr(), 1, *ptrs(eg["attn_out"]), E, st))
+            mv_named(lw, "o", eg["attn_out"], st)
             _native.check(L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(), nw_s.data_ptr(),
-                                        1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E, stream))
-            mv_shared(lw, ("gate", "up"), eg["x_ffn"])
+                                        1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E, st))
+            mv_shared(lw, ("gate", "up"), eg["x_ffn"], st)
             _native.check(L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
-                                       *ptrs(eg["act"]), FF, stream))
-            mv_named(lw, "down", eg["act"])
+                                       *ptrs(eg["act"]), FF, st))
+            mv_named(lw, "down", eg["act"], st)
 
         for i in range(max(5, args.warmup // 10)):
             step_layer(i)
@@ -690,6 +723,8 @@ def main():
         t1.record()
         torch.cuda.synchronize()
         cfg["us_per_layer_fused_inputs"] = round(t0.elapsed_time(t1) / reps * 1e3, 3)
+        cfg["us_per_layer_fused_inputs_graph"] = graph_us(step_layer)
+        cfg["us_per_layer_fused_inputs_graph_32_layers"] = graph_us(step_layer, 32)
         del layers
         # per-matrix breakdown: each mat-vec timed alone, rotating over its own copies (> 2x the LLC)
         parts = {}

@@ -35,6 +35,7 @@ class Fliessband:
         self._strom: Optional[torch.cuda.Stream] = None
         self._inhalt: List[int] = []             # matrix held (or being copied) per slot, -1: none
         self._gelesen: List[bool] = []           # the slot's "done" event belongs to this pass
+        self._ausgegeben: List[int] = []         # matrix handed out by holen() and not yet fertig(), -1: none
         self._fertig: list = []                  # per slot: the last computation that read it
         self._bereit: list = []                  # per slot: its copy has landed
         self._zuletzt = 1 << 62                  # number of the last matrix handed out
@@ -56,6 +57,7 @@ class Fliessband:
         self._strom = torch.cuda.Stream(self.device)
         self._inhalt = [-1] * self.PLAETZE
         self._gelesen = [False] * self.PLAETZE
+        self._ausgegeben = [-1] * self.PLAETZE
         self._fertig = [torch.cuda.Event() for _ in range(self.PLAETZE)]
         self._bereit = [torch.cuda.Event() for _ in range(self.PLAETZE)]
 
@@ -63,6 +65,9 @@ class Fliessband:
         platz = nr % self.PLAETZE
         if self._inhalt[platz] == nr:
             return
+        if self._ausgegeben[platz] >= 0:         # its computation may not even be queued yet
+            raise RuntimeError(f"Fliessband: matrix {nr} would overwrite matrix {self._ausgegeben[platz]}, "
+                               f"which holen() handed out and fertig() has not released")
         if self._gelesen[platz]:                 # its reader in this pass must be done first
             self._strom.wait_event(self._fertig[platz])
         q = self.quellen[nr]
@@ -74,21 +79,28 @@ class Fliessband:
 
     def holen(self, nr: int) -> torch.Tensor:
         """The bytes of matrix `nr` in VRAM (the current stream waits for their copy); the copies of the
-        next PLAETZE - 1 matrices are queued behind it."""
+        next PLAETZE - 1 matrices are queued behind it.  Every matrix handed out is released with
+        `fertig(nr)` once its computation is queued; a copy that would overwrite a matrix not yet
+        released raises RuntimeError (the band's state is unchanged for that slot)."""
         if not 0 <= nr < len(self.quellen):
             raise IndexError(f"Fliessband: matrix {nr} of {len(self.quellen)}")
         if self._ring is None:
             self._anlegen()
         rechnen = torch.cuda.current_stream(self.device)
         if nr <= self._zuletzt:                  # a new pass: nothing queued before may be overwritten early
+            offen = [a for a in self._ausgegeben if a >= 0]
+            if offen:
+                raise RuntimeError(f"Fliessband: a new pass starts at matrix {nr} while matrices {offen} are "
+                                   f"handed out and not released by fertig()")
             self._strom.wait_stream(rechnen)
             self._inhalt = [-1] * self.PLAETZE
             self._gelesen = [False] * self.PLAETZE
-        self._zuletzt = nr
         for k in range(nr, min(nr + self.PLAETZE, len(self.quellen))):
             self._laden(k)
+        self._zuletzt = nr                       # after the copies: a refused holen() can be retried in its pass
         platz = nr % self.PLAETZE
         rechnen.wait_event(self._bereit[platz])
+        self._ausgegeben[platz] = nr
         return self._ring[platz, :self.quellen[nr].numel()]
 
     def fertig(self, nr: int) -> None:
@@ -96,3 +108,5 @@ class Fliessband:
         platz = nr % self.PLAETZE
         self._fertig[platz].record(torch.cuda.current_stream(self.device))
         self._gelesen[platz] = True
+        if self._ausgegeben[platz] == nr:
+            self._ausgegeben[platz] = -1

@@ -461,6 +461,33 @@ def test_experts_in_pinned_ram_with_vram_slots(nmq, oracle):
     assert hostmem.pending() == 0
 
 
+def test_band_refuses_to_overwrite_a_matrix_in_use():
+    """A copy into a slot whose matrix holen() handed out and fertig() has not released raises instead
+    of racing with that matrix's computation: within a pass (the ring wraps onto it) and at the start
+    of the next pass.  After fertig() the same calls go through and return the right bytes."""
+    from ggufengine_amd import band
+    fl = band.Fliessband("cuda")
+    src = [torch.full((1000 + i,), i, dtype=torch.uint8, device="cuda") for i in range(6)]
+    for t in src:
+        fl.anmelden(t)
+    say("band guard")
+    a = fl.holen(0)
+    with pytest.raises(RuntimeError, match="overwrite matrix 0"):
+        fl.holen(1)                          # queues matrix 4 into slot 0
+    fl.fertig(0)
+    for nr in range(1, 6):
+        got = fl.holen(nr)
+        assert got.numel() == 1000 + nr and bool((got == nr).all())
+        if nr < 5:
+            fl.fertig(nr)
+    with pytest.raises(RuntimeError, match=r"handed out"):
+        fl.holen(0)                          # a new pass while matrix 5 is still out
+    fl.fertig(5)
+    assert bool((fl.holen(0) == 0).all()) and a.numel() == 1000
+    fl.fertig(0)
+    torch.cuda.synchronize()
+
+
 def test_packed_linear_band_from_pinned_ram(nmq):
     """Layers whose weights live in pinned RAM, computed through a Fliessband (4 VRAM slots filled by
     whole-matrix copies a few layers ahead on a copy stream, ordered by events only): over several

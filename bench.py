@@ -397,10 +397,13 @@ def run_offload(steps, warmup, threads):
 
 def run_moe(steps, warmup, threads):
     """Qwen3-30B-A3B-style expert layer: 128 experts, gate/up 768x2048 Q4_K, down 2048x768 Q6_K
-    (seed 41), router logits ~N(0,1) (seed 42) -> top-8 softmax renormalised, x ~N(0,1) (seed 43),
-    1 and 4 tokens.  Timed: the whole expert layer after routing (2 activation quantisations, 3
-    gathered mat-vec launches, silu * up, weighted combine) captured as a HIP graph per copy of the
-    expert tensors and replayed, alternating copies; the eager Python-driven time is reported beside it."""
+    (seed 41) in 4 copies, 16 routings (router logits ~N(0,1), seeds 42, 44, ..., 72 -> top-8 softmax
+    renormalised), x ~N(0,1) (seed 43), 1 and 4 tokens.  Timed: the whole expert layer after routing
+    (2 activation quantisations, 3 gathered mat-vec launches, silu * up, weighted combine), 16 layers
+    in a row (routing q on copy (j + q) % 4, as a decode step holds one such layer per block) captured
+    in one HIP graph per j and replayed, us per layer: the experts a cycle reads (about 1 GB) exceed
+    the last-level cache.  One layer per graph and the eager Python-driven time beside it.  Checked:
+    every replayed output equals the eager layer; routing 0 on copy 0 against the oracle chain."""
     import numpy as np
     import torch
     import oracle
@@ -414,46 +417,70 @@ def run_moe(steps, warmup, threads):
     raw = {"gate": enc("Q4_K", FF, E), "up": enc("Q4_K", FF, E), "down": enc("Q6_K", E, FF)}
     dev = torch.device("cuda", 0)
     per_set = sum(r.size for r in raw.values())
-    nsets = max(2, -(-2 * LLC_BYTES // per_set))
+    NSETS, PER = 4, 16
     base = {n: torch.from_numpy(r).to(dev) for n, r in raw.items()}
-    sets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(nsets - 1)]
+    sets = [base] + [{n: t.clone() for n, t in base.items()} for _ in range(NSETS - 1)]
     layers = [experts.Experten(experts.PackedExperts(s["gate"], 12, n_exp, FF, E),
                                experts.PackedExperts(s["up"], 12, n_exp, FF, E),
                                experts.PackedExperts(s["down"], 14, n_exp, E, FF)) for s in sets]
     per_expert = per_set // n_exp
     for Ltok in (1, 4):
-        logits = torch.from_numpy(_x(42, (Ltok, n_exp))).to(dev)
+        # one routing per layer of a PER-layer step (logits seeds 42, 44, ...): layer q of a step uses
+        # routing q on expert set (j + q) % NSETS, so the experts read by consecutive steps (about 1 GB
+        # over all sets and routings) do not stay in the 256 MB last-level cache
+        routes = [experts.auswahl(torch.from_numpy(_x(42 + 2 * q, (Ltok, n_exp))).to(dev), k) for q in range(PER)]
+        idx, w = routes[0]
         x = torch.from_numpy(_x(43, (Ltok, E))).to(dev)
-        idx, w = experts.auswahl(logits, k)
+        touched = {((j + q) % NSETS, e) for j in range(NSETS) for q in range(PER)
+                   for e in routes[q][0].cpu().numpy().reshape(-1).tolist()}
+        eager = {}
+        for j in range(NSETS):
+            for q in range(PER):
+                if (j, q) not in eager:
+                    eager[(j, q)] = layers[j](x, *routes[q]).clone()
         out = {}
 
         def go(i):
-            out["y"] = layers[i % nsets](x, idx, w)
+            out["y"] = layers[(i // PER + i) % NSETS](x, *routes[i % PER])
         us_eager = _events_us(go, max(50, steps // 10), max(10, warmup // 10))
-        eager = [layers[j](x, idx, w).clone() for j in range(nsets)]
-        # the layer as the reference runs one step: captured in a graph (one per expert set), replayed
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
-        graphs, outs = [], []
         with torch.cuda.stream(side):
-            for j in range(nsets):
+            for j in range(NSETS):
                 layers[j](x, idx, w)
         torch.cuda.current_stream().wait_stream(side)
-        for j in range(nsets):
+        # one layer per graph (graph g: routing g, set g % NSETS) ...
+        graphs, outs = [], []
+        for q in range(PER):
             gr = torch.cuda.CUDAGraph()
             with torch.cuda.graph(gr):
-                outs.append(layers[j](x, idx, w))
+                outs.append(layers[q % NSETS](x, *routes[q]))
             graphs.append(gr)
-        us = _events_us(lambda i: graphs[i % nsets].replay(), steps, warmup)
+        us_one = _events_us(lambda i: graphs[i % PER].replay(), steps, warmup)
         torch.cuda.synchronize()
-        for j in range(nsets):           # every replayed graph still gives the eager result
-            graphs[j].replay()
+        for q in range(PER):
+            graphs[q].replay()
             torch.cuda.synchronize()
-            if not torch.equal(outs[j], eager[j]):
-                raise SystemExit(f"moe: graph replay of set {j} differs from the eager layer")
-        out["y"] = outs[0]
-        distinct = len(set(idx.cpu().numpy().reshape(-1).tolist()))
-        ab = distinct * per_expert + Ltok * 4 * E * 2
+            if not torch.equal(outs[q], eager[(q % NSETS, q)]):
+                raise SystemExit(f"moe: graph replay of routing {q} differs from the eager layer")
+        # ... and a whole decode step's worth, PER layers per graph, so the graph launch's own cost
+        # (~8 us on this stack) is spread as in a real step; every replayed output equals the eager one
+        mgraphs, mouts = [], []
+        for j in range(NSETS):
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                mouts.append([layers[(j + q) % NSETS](x, *routes[q]) for q in range(PER)])
+            mgraphs.append(gr)
+        us = _events_us(lambda i: mgraphs[i % NSETS].replay(), max(20, steps // PER), max(5, warmup // PER)) / PER
+        torch.cuda.synchronize()
+        for j in range(NSETS):
+            mgraphs[j].replay()
+            torch.cuda.synchronize()
+            if not all(torch.equal(mouts[j][q], eager[((j + q) % NSETS, q)]) for q in range(PER)):
+                raise SystemExit(f"moe: {PER}-layer graph replay of set {j} differs from the eager layer")
+        out["y"] = eager[(0, 0)]
+        distinct = sum(len(set(r[0].cpu().numpy().reshape(-1).tolist())) for r in routes) / PER
+        ab = int(distinct * per_expert) + Ltok * 4 * E * 2
         # end to end against the oracle chain on the selected experts (dequantised weights, fp64)
         ids = idx.cpu().numpy()
         wts = w.cpu().numpy().astype(np.float64)
@@ -472,9 +499,11 @@ def run_moe(steps, warmup, threads):
                 ref[t] += wts[t, j] * oracle.mv_deq("Q6_K", part("down", e), E, FF, a)[0]
         err = float(oracle.rel_err_rows(out["y"].cpu().numpy(), ref).max())
         _record("moe", f"128 experts top-8, {Ltok} token(s)", "Q4_K+Q6_K", us, ab, err,
-                distinct_experts=distinct, expert_sets=nsets, us_eager_python=round(us_eager, 3),
-                timing="graph replay of the whole expert layer")
-        del graphs, outs, eager
+                distinct_experts_per_layer=distinct, expert_sets=NSETS, routings=PER,
+                bytes_touched_per_cycle=len(touched) * per_expert, us_eager_python=round(us_eager, 3),
+                us_graph_of_one_layer=round(us_one, 3),
+                timing=f"graph replay, {PER} expert layers per graph, us per layer")
+        del graphs, outs, mgraphs, mouts, eager
 
 
 def main():

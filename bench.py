@@ -76,11 +76,21 @@ def traffic_bytes():
         return None
 
 
+def host_threads():
+    """(threads, reason): every host core this process may use -- its CPU affinity, capped by
+    OMP_NUM_THREADS where the machine sets one (the share of the host that belongs to one GPU)."""
+    n = len(os.sched_getaffinity(0))
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and 0 < int(cap) < n:
+        return int(cap), f"all {cap} host threads of this GPU's share (OMP_NUM_THREADS; affinity {n})"
+    return n, f"all {n} host threads in the process's affinity"
+
+
 def cpu_baseline(raw, fmt, rows, n_in, x, budget_s):
     """The oracle's restatement of the reference CPU path (models/common.py:190, 526-527): dequantise
     once, then fp32 GEMV per call, timed for about budget_s seconds."""
     import oracle
-    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    threads, why = host_threads()
     w = oracle.dequant(fmt, raw).reshape(rows, n_in)
     oracle.gemv_f32(w, x, threads)  # warm
     calls, t0 = 0, time.perf_counter()
@@ -102,24 +112,81 @@ def cpu_baseline(raw, fmt, rows, n_in, x, budget_s):
     return {"value": round(alg_bytes(fmt, rows, n_in) / per / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"{fmt} {rows}x{n_in} dequantised once by the oracle, fp32 GEMV (F.linear path) timed over "
-                      f"{calls} calls ({el:.1f} s, {per * 1e6:.0f} us/call) on {threads} threads of {cpu}"}
+                      f"{calls} calls ({el:.1f} s, {per * 1e6:.0f} us/call) on {threads} threads of {cpu}: {why}"}
 
 
 # ---- the other configurations: one JSON record per case on stdout ---------------------------------
 
-def _events_us(fn, steps, warmup):
-    """us per call of fn(i) (launches on the current stream), HIP events around `steps` calls."""
+_CLOCKS_PER_US = None
+
+
+def _hold_gpu(us):
+    """Keep the current stream busy for about `us` microseconds (torch.cuda._sleep: a one-wave kernel
+    counting shader clocks, bounded), so launches queued meanwhile by the host run back to back on the
+    GPU instead of at the host's launch rate."""
+    import torch
+    global _CLOCKS_PER_US
+    if _CLOCKS_PER_US is None:
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(1000)
+        a.record()
+        torch.cuda._sleep(2_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        _CLOCKS_PER_US = 2_000_000 / max(1.0, a.elapsed_time(b) * 1e3)
+    torch.cuda._sleep(int(us * _CLOCKS_PER_US))
+
+
+def _timed(fn, steps, warmup, pairs=False, chunk=200):
+    """fn(i) queues step i on the current stream.  W untimed steps, then `steps` timed ones in chunks of at
+    most `chunk`; before each chunk the GPU is held (spin kernel) longer than the host takes to queue it, so
+    the chunk runs back to back on the GPU.  Returns the us per step between events around each chunk
+    (back to back: the launch gaps between kernels included, the host's launch rate not) and, with
+    pairs=True, from a second timed pass with events recorded around every step, their mean (the step's
+    own duration on the stream, as a kernel trace sees it)."""
+    import time
     import torch
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    for i in range(steps):
+    probe = min(steps, 20)
+    t = time.perf_counter()
+    for i in range(probe):
         fn(i)
-    b.record()
+    host_us = (time.perf_counter() - t) / probe * 1e6
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / steps * 1e3
+
+    def timed_pass(with_pairs):
+        total_ms, pair_ms, done = 0.0, [], 0
+        while done < steps:
+            n = min(chunk, steps - done)
+            _hold_gpu(3 * host_us * n + 300)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(n if with_pairs else 0)]
+            a.record()
+            for j in range(n):
+                if with_pairs:
+                    ev[j][0].record()
+                fn(done + j)
+                if with_pairs:
+                    ev[j][1].record()
+            b.record()
+            torch.cuda.synchronize()
+            total_ms += a.elapsed_time(b)
+            pair_ms += [e0.elapsed_time(e1) for e0, e1 in ev]
+            done += n
+        return total_ms / steps * 1e3, (sum(pair_ms) / len(pair_ms) * 1e3 if pair_ms else None)
+
+    out = {"us_back_to_back": timed_pass(False)[0], "host_us_per_step": host_us}
+    if pairs:
+        out["us_event_pairs"] = timed_pass(True)[1]
+    return out
+
+
+def _events_us(fn, steps, warmup):
+    """us per call of fn(i) (launches on the current stream), run back to back on the GPU (see _timed)."""
+    return _timed(fn, steps, warmup)["us_back_to_back"]
 
 
 def _copies(t, total_bytes=None):
@@ -138,15 +205,13 @@ def _record(config, case, fmt, us, ab, err, **extra):
     print(json.dumps(rec), flush=True)
 
 
-def _mv_case(L, stream, fmt, ws, raw_np, rows, n_in, x_np, steps, warmup, env=None):
+def _mv_case(L, stream, fmt, ws, raw_np, rows, n_in, x_np, steps, warmup, knobs=None):
     """Time nmq_mv on n = x_np.shape[0] tokens rotating over the weight copies ws; parity of the last
-    output against the oracle.  env: tuning variables set for this case only."""
+    output against the oracle.  knobs: launch-plan overrides (nmq_set_tuning) for this case only."""
     import torch
     import oracle
     from ggufengine_amd import _native, mmvq
-    saved = {k: os.environ.get(k) for k in (env or {})}
-    os.environ.update(env or {})
-    try:
+    with _native.tuning(**(knobs or {})):
         dev = ws[0].device
         n = x_np.shape[0]
         e = mmvq.Eingang(torch.from_numpy(x_np).to(dev))
@@ -160,12 +225,6 @@ def _mv_case(L, stream, fmt, ws, raw_np, rows, n_in, x_np, steps, warmup, env=No
         us = _events_us(go, steps, warmup)
         err = float(oracle.rel_err_rows(y.cpu().numpy(), oracle.mv_deq(fmt, raw_np, rows, n_in, x_np)).max())
         return us, err
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
 
 
 def _x(seed, shape):
@@ -203,9 +262,9 @@ def run_configs(which, steps, warmup):
                 extra = {}
                 if n > 1:
                     us4, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
-                                      {"NMQ_MVM": "0", "NMQ_MVT_MAX": "1"})
+                                      {"MVM": 0, "MVT_MAX": 1})
                     usm, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
-                                      {"NMQ_MVM": "2", "NMQ_MVT_MAX": "1"})
+                                      {"MVM": 2, "MVT_MAX": 1})
                     extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
                 _record("speculative", f"Q4_K {rows}x4096 n={n}", "Q4_K", us, alg_bytes("Q4_K", rows, 4096, n), err,
                         **extra)
@@ -218,7 +277,7 @@ def run_configs(which, steps, warmup):
             us, err = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup)
             extra = {}
             if n > 1:
-                usg, _ = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup, {"NMQ_MVLT_MAX": "1"})
+                usg, _ = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup, {"MVLT_MAX": 1})
                 extra = {"us_without_few_token_kernel": round(usg, 3)}
             _record("speculative", f"Q6_K 4096x14336 n={n}", "Q6_K", us, alg_bytes("Q6_K", 4096, 14336, n), err, **extra)
         del ws
@@ -234,8 +293,8 @@ def run_configs(which, steps, warmup):
                 us, err = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup)
                 extra = {}
                 if n > 1:
-                    us4, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "0"})
-                    usm, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"NMQ_MVM": "2"})
+                    us4, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"MVM": 0})
+                    usm, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"MVM": 2})
                     extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
                 _record("q4_0", f"Q4_0 {rows}x4096 n={n}", "Q4_0", us, alg_bytes("Q4_0", rows, 4096, n), err, **extra)
             del ws
@@ -263,6 +322,47 @@ def run_configs(which, steps, warmup):
 
     if which in ("moe", "all"):
         run_moe(steps, warmup, threads)
+
+    if which in ("ceiling", "all"):
+        run_ceiling(steps, warmup)
+
+
+CEILING_SHAPES = [(wpc, wgw, u) for wpc in (4, 8, 16, 32) for wgw in (4, 8, 16) for u in (2, 4, 8)
+                  if wpc % wgw == 0]
+
+
+def read_ceiling(n_bytes, steps, warmup, shapes=None):
+    """The pure streaming read (nmq_stream_read) of n_bytes in one launch, rotating over copies larger than
+    twice the last-level cache, for each launch shape (resident waves per CU, waves per workgroup, loads in
+    flight per thread); us per launch back to back (see _timed).  Returns the best shape's
+    record and all timings."""
+    import torch
+    from ggufengine_amd import _native
+    L = _native.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    n_copies = max(2, -(-2 * LLC_BYTES // n_bytes))
+    bufs = [torch.randint(0, 255, (n_bytes,), dtype=torch.uint8, device="cuda") for _ in range(n_copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    table = []
+    for wpc, wgw, u in shapes or CEILING_SHAPES:
+        def go(i, wpc=wpc, wgw=wgw, u=u):
+            rc = L.nmq_stream_read(bufs[i % n_copies].data_ptr(), n_bytes, sink.data_ptr(), wpc, wgw, u, stream)
+            if rc:
+                _native.check(rc)
+        table.append({"waves_per_cu": wpc, "wg_waves": wgw, "unroll": u, "us": round(_events_us(go, steps, warmup), 3)})
+    del bufs
+    best = min(table, key=lambda r: r["us"])
+    gbs = n_bytes / (best["us"] * 1e-6) / 1e9
+    return {"bytes": n_bytes, **best, "GB/s": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2)}, table
+
+
+def run_ceiling(steps, warmup):
+    """Pure-read reference points: the headline's weight bytes (33 MB) and sizes up to 1 GB, every launch
+    shape; one record per size."""
+    for n in (weight_bytes("Q4_K", 14336, 4096), weight_bytes("Q4_K", 4096, 4096), 128 << 20, 512 << 20, 1 << 30):
+        best, table = read_ceiling(n, steps, warmup)
+        print(json.dumps({"config": "ceiling", "case": f"pure read of {n} bytes in one launch", "best": best,
+                          "shapes": table}), flush=True)
 
 
 def run_prefill(L, stream, steps, warmup):
@@ -515,7 +615,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
     ap.add_argument("--config", default="headline",
-                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "offload", "all"),
+                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "offload", "ceiling",
+                             "all"),
                     help="headline (default): the metric line; the others print one record per case of "
                          "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, "
                          "16..112 tokens on the fp16 matrix cores, MoE)")
@@ -558,33 +659,21 @@ def main():
         if rc:
             _native.check(rc)
 
-    for i in range(args.warmup):
-        launch(i)
-    torch.cuda.synchronize()
-    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for i in range(args.steps):
-        launch(i)
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / args.steps
+    timing = _timed(launch, args.steps, args.warmup, pairs=True)
+    ms = timing["us_back_to_back"] * 1e-3
     ab = alg_bytes(fmt, rows, n_in)
     gbs = ab / (ms * 1e-3) / 1e9
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
     # reference point on the same box: the runtime's device copy of the same weight bytes, one launch
     # per copy, source and destination rotating over copies larger than the last-level cache (it reads
     # and writes every byte: its rate counts both)
     dsts = [torch.empty_like(base) for _ in range(copies)]
-    for i in range(20):
-        dsts[i % copies].copy_(ws[(i + 1) % copies])
-    torch.cuda.synchronize()
-    t0.record()
-    for i in range(200):
-        dsts[i % copies].copy_(ws[(i + 1) % copies])
-    t1.record()
-    torch.cuda.synchronize()
-    copy_us = t0.elapsed_time(t1) / 200 * 1e3
+    copy_us = _events_us(lambda i: dsts[i % copies].copy_(ws[(i + 1) % copies]), 200, 20)
     del dsts
+    # reference point: the pure streaming read of the same weight bytes in one launch (best launch shape
+    # of a small sweep; `--config ceiling` sweeps more shapes and sizes)
+    ceiling, _ = read_ceiling(wb, 200, 20, [(wpc, wgw, 4) for wpc, wgw in ((8, 8), (16, 8), (16, 16), (32, 16))])
 
     # parity of the timed kernel's output against the oracle (cheap, full size)
     import oracle
@@ -594,7 +683,12 @@ def main():
     cfg = {"workload": "Q4_K 14336x4096 mat-vec, batch 1 (Llama-3-8B ffn gate/up)", "format": fmt, "rows": rows,
            "n_in": n_in, "batch": 1, "weight_copies": copies, "algorithmic_bytes": ab,
            "us_per_matvec": round(ms * 1e3, 3), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+           "timing": "HIP events around the K launches, queued while a spin kernel holds the GPU so that "
+                     "they run back to back (launch gaps included, the host's launch rate not)",
+           "us_per_matvec_event_pairs": round(timing["us_event_pairs"], 3),
+           "host_us_per_launch": round(timing["host_us_per_step"], 3),
            "max_rel_err_vs_oracle": parity,
+           "pure_read_same_bytes": ceiling,
            "device_copy_same_bytes": {"us": round(copy_us, 3), "bytes_read_and_written": 2 * wb,
                                       "GB/s": round(2 * wb / (copy_us * 1e-6) / 1e9, 1)}}
 
@@ -648,15 +742,7 @@ def main():
 
         reps = max(20, args.steps // 10)
         for how in ("separate", "multi", "values"):
-            for i in range(max(5, args.warmup // 10)):
-                one_layer(i, how)
-            torch.cuda.synchronize()
-            t0.record()
-            for i in range(reps):
-                one_layer(i, how)
-            t1.record()
-            torch.cuda.synchronize()
-            us_layer = t0.elapsed_time(t1) / reps * 1e3
+            us_layer = _events_us(lambda i: one_layer(i, how), reps, max(5, args.warmup // 10))
             if how != "values":
                 cfg[f"us_per_layer_{how}"] = round(us_layer, 3)
         cfg["us_per_layer"] = round(us_layer, 3)
@@ -678,16 +764,9 @@ def main():
             graphs[0].replay()
             torch.cuda.synchronize()
             assert all(torch.equal(eager[n], ys[n]) for n in ys), "graph replay differs from the eager layer"
-            for i in range(max(5, args.warmup // 10)):
-                graphs[i % nl].replay()
-            torch.cuda.synchronize()
             n_rep = max(5, reps // per)
-            t0.record()
-            for i in range(n_rep):
-                graphs[i % nl].replay()
-            t1.record()
-            torch.cuda.synchronize()
-            return round(t0.elapsed_time(t1) / (n_rep * per) * 1e3, 3)
+            us = _events_us(lambda i: graphs[i % nl].replay(), n_rep, max(5, args.warmup // 10))
+            return round(us / per, 3)
 
         cfg["us_per_layer_graph"] = graph_us(lambda j, st: one_layer(j, "values", st))
         cfg["us_per_layer_graph_32_layers"] = graph_us(lambda j, st: one_layer(j, "values", st), 32)
@@ -743,15 +822,7 @@ def main():
                                        *ptrs(eg["act"]), FF, st))
             mv_named(lw, "down", eg["act"], st)
 
-        for i in range(max(5, args.warmup // 10)):
-            step_layer(i)
-        torch.cuda.synchronize()
-        t0.record()
-        for i in range(reps):
-            step_layer(i)
-        t1.record()
-        torch.cuda.synchronize()
-        cfg["us_per_layer_fused_inputs"] = round(t0.elapsed_time(t1) / reps * 1e3, 3)
+        cfg["us_per_layer_fused_inputs"] = round(_events_us(step_layer, reps, max(5, args.warmup // 10)), 3)
         cfg["us_per_layer_fused_inputs_graph"] = graph_us(step_layer)
         cfg["us_per_layer_fused_inputs_graph_32_layers"] = graph_us(step_layer, 32)
         del layers
@@ -767,46 +838,21 @@ def main():
                               ei.xd.data_ptr(), ei.xs.data_ptr(), ys[name].data_ptr(), r, k, 1, stream)
                 if rc:
                     _native.check(rc)
-            for i in range(20):
-                one(i)
-            torch.cuda.synchronize()
-            t0.record()
-            for i in range(reps):
-                one(i)
-            t1.record()
-            torch.cuda.synchronize()
-            us = t0.elapsed_time(t1) / reps * 1e3
+            us = _events_us(one, reps, 20)
             parts[name] = {"format": f, "shape": [r, k], "us": round(us, 3),
                            "pct_hbm_peak": round(100 * alg_bytes(f, r, k) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)}
             del cps
         xq_in = xin["x_attn"]
-        for i in range(20):
-            L.nmq_quant_q8(xq_in.data_ptr(), 1, eg["x_attn"].xq.data_ptr(), eg["x_attn"].xq2.data_ptr(),
-                           eg["x_attn"].xd.data_ptr(), eg["x_attn"].xs.data_ptr(), 4096, stream)
-        torch.cuda.synchronize()
-        t0.record()
-        for i in range(reps):
-            L.nmq_quant_q8(xq_in.data_ptr(), 1, eg["x_attn"].xq.data_ptr(), eg["x_attn"].xq2.data_ptr(),
-                           eg["x_attn"].xd.data_ptr(), eg["x_attn"].xs.data_ptr(), 4096, stream)
-        t1.record()
-        torch.cuda.synchronize()
-        parts["quant_q8_4096"] = {"us": round(t0.elapsed_time(t1) / reps * 1e3, 3)}
-        small = {
+        small = {"quant_q8_4096": lambda: L.nmq_quant_q8(xq_in.data_ptr(), 1, *ptrs(eg["x_attn"]), 4096, stream)}
+        small.update({
             "norm_q8_4096": lambda: L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(),
                                                   nw_s.data_ptr(), 1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E,
                                                   stream),
             "akt_q8_14336": lambda: L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
-                                                 *ptrs(eg["act"]), FF, stream)}
+                                                 *ptrs(eg["act"]), FF, stream)})
         for pname, fn in small.items():
-            for i in range(20):
-                _native.check(fn())
-            torch.cuda.synchronize()
-            t0.record()
-            for i in range(reps):
-                fn()
-            t1.record()
-            torch.cuda.synchronize()
-            parts[pname] = {"us": round(t0.elapsed_time(t1) / reps * 1e3, 3)}
+            _native.check(fn())
+            parts[pname] = {"us": round(_events_us(lambda i, fn=fn: fn(), reps, 20), 3)}
         cfg["layer_parts"] = parts
         del mats
 

@@ -44,6 +44,19 @@ int nmq_abi_version(void);
 /* Text for a return code of any entry point (static storage). */
 const char* nmq_strerror(int code);
 
+/*
+ * Launch-plan overrides for timing runs and tests (no counterpart in the reference, whose kernels
+ * take their launch shape from constants in mmvq.py:25-37 and cudakern.py:31-54).  name: a knob of
+ * the launch planner without or with the "NMQ_" prefix (MV1, MV1_MODE, MV1_HR, MV1_WPC, MV1_W,
+ * MV1_RW, MV1_NBUF, MV1_MAXNIT, MVL, MVL_WPC, MVL_W, MVC_WGPC, MVC_RW, MVC_ROWS, MVT_MAX, MVT_WPC,
+ * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G); value NMQ_TUNE_DEFAULT restores the measured default.
+ * Process-wide, read by every later launch; the environment is never consulted.  NMQ_ERR_ARG for an
+ * unknown name.  nmq_get_tuning writes the override or NMQ_TUNE_DEFAULT.
+ */
+#define NMQ_TUNE_DEFAULT (-2147483647 - 1)
+int nmq_set_tuning(const char* name, int value);
+int nmq_get_tuning(const char* name, int* value);
+
 /* Values and bytes per block of a format; returns NMQ_OK or NMQ_ERR_FORMAT.
  * Replaces the table lookups GGML_TYPES[...] (gguf.py:64-78), mmvq.FORMATE (mmvq.py:25) and
  * cudakern.FORMATE (cudakern.py:42-49) for the five formats of this library. */
@@ -246,6 +259,16 @@ int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, 
  * the unpack step of the PackedLinear fallback (models/common.py:414-428).
  */
 int nmq_dequant_bf16(int fmt, const void* w, uint16_t* out, int64_t n_blocks, void* stream);
+
+/*
+ * Diagnostic: a pure streaming read of n_bytes at src (16-byte aligned, n_bytes % 16 == 0) with 16-byte
+ * loads, `unroll` (1, 2, 4, 8) in flight per thread, waves_per_cu (1..32) resident waves per CU in
+ * workgroups of wg_waves (1..16, dividing waves_per_cu) waves; writes at most one word to sink.  The
+ * reference point for what one launch of that size can read from HBM (the mat-vec kernels read the same
+ * weight bytes plus their input).  No counterpart in the reference.
+ */
+int nmq_stream_read(const void* src, int64_t n_bytes, uint32_t* sink, int waves_per_cu, int wg_waves, int unroll,
+                    void* stream);
 
 /* ---- host-side encoders (CPU, no device involved) -----------------------------------------------
  * Write n values (n % block_values == 0) of fp32 weights into GGUF blocks at out

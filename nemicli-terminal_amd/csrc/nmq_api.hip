@@ -490,6 +490,31 @@ struct DeqK {
     static constexpr auto fn = dequant_bf16_kernel<F>;
 };
 
+// ---- pure streaming read (diagnostic) ----------------------------------------------------------------
+// Reads n16 16-byte words with a grid-stride loop, U loads in flight per thread, and folds them into one
+// value per thread; a lane stores only if its fold equals a constant no real input produces in practice, so
+// the reads cannot be dropped and the kernel writes (almost) nothing.  It is the reference point for what
+// one launch of a given size reads from HBM.
+template <int U>
+__global__ __launch_bounds__(1024) void stream_read_kernel(const u32x4* __restrict__ src, int64_t n16, u32* sink,
+                                                           int nt) {
+    const int64_t stride = (int64_t)gridDim.x * nt;
+    int64_t i = (int64_t)blockIdx.x * nt + threadIdx.x;
+    u32 acc = 0;
+    for (; i + (int64_t)(U - 1) * stride < n16; i += (int64_t)U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = src[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const u32x4 v = src[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+
 }  // namespace nmq
 
 using namespace nmq;
@@ -509,6 +534,25 @@ const char* nmq_strerror(int code) {
         case NMQ_ERR_DEVICE: return "nmq: no usable gfx950 device";
         default: return code > 0 ? hipGetErrorString((hipError_t)code) : "nmq: unknown error";
     }
+}
+
+int nmq_set_tuning(const char* name, int value) {
+    static std::mutex mu;
+    const int k = tune_index(name);
+    if (k < 0) return NMQ_ERR_ARG;
+    std::lock_guard<std::mutex> g(mu);
+    if (!g_tune_ready.load(std::memory_order_acquire)) tune_reset_all();
+    g_tune[k].store(value == NMQ_TUNE_DEFAULT ? TUNE_UNSET : value, std::memory_order_relaxed);
+    return NMQ_OK;
+}
+
+int nmq_get_tuning(const char* name, int* value) {
+    const int k = tune_index(name);
+    if (k < 0 || !value) return NMQ_ERR_ARG;
+    const int v = g_tune_ready.load(std::memory_order_acquire) ? g_tune[k].load(std::memory_order_relaxed)
+                                                               : TUNE_UNSET;
+    *value = v == TUNE_UNSET ? NMQ_TUNE_DEFAULT : v;
+    return NMQ_OK;
 }
 
 int nmq_format_info(int fmt, int* block_values, int* block_bytes) {
@@ -865,6 +909,26 @@ int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, 
     if (blocks > 0x7fffffff) return NMQ_ERR_SHAPE;
     return launch_fmt_kernel<SumsK>(fmt, dim3((unsigned)blocks), (hipStream_t)stream, (const u8*)w, xq, xq2, s1, s2,
                                     n_out, n_in);
+}
+
+int nmq_stream_read(const void* src, int64_t n_bytes, uint32_t* sink, int waves_per_cu, int wg_waves, int unroll,
+                    void* stream) {
+    if (!src || !sink || !aligned(src, 16) || n_bytes % 16) return NMQ_ERR_ARG;
+    if (n_bytes <= 0 || waves_per_cu < 1 || waves_per_cu > 32 || wg_waves < 1 || wg_waves > 16 ||
+        waves_per_cu % wg_waves)
+        return NMQ_ERR_SHAPE;
+    const DeviceInfo di = device_info();
+    const int nt = 64 * wg_waves;
+    const unsigned grid = (unsigned)((int64_t)di.cus * waves_per_cu / wg_waves);
+    const hipStream_t s = (hipStream_t)stream;
+    switch (unroll) {
+        case 1: hipLaunchKernelGGL(stream_read_kernel<1>, dim3(grid), dim3(nt), 0, s, (const u32x4*)src, n_bytes / 16, sink, nt); break;
+        case 2: hipLaunchKernelGGL(stream_read_kernel<2>, dim3(grid), dim3(nt), 0, s, (const u32x4*)src, n_bytes / 16, sink, nt); break;
+        case 4: hipLaunchKernelGGL(stream_read_kernel<4>, dim3(grid), dim3(nt), 0, s, (const u32x4*)src, n_bytes / 16, sink, nt); break;
+        case 8: hipLaunchKernelGGL(stream_read_kernel<8>, dim3(grid), dim3(nt), 0, s, (const u32x4*)src, n_bytes / 16, sink, nt); break;
+        default: return NMQ_ERR_ARG;
+    }
+    return (int)hipGetLastError();
 }
 
 int nmq_dequant_bf16(int fmt, const void* w, uint16_t* out, int64_t n_blocks, void* stream) {

@@ -435,15 +435,15 @@ struct MvmShape {
 template <int F>
 inline MvmShape plan_mvm(int n_out, int n_in, int nc, int cus, int lds_max) {
     MvmShape s{};
-    const int mode = env_int("NMQ_MVM", 1);  // 0: never, 1: from MIN_NC tokens, 2: from 2 tokens
+    const int mode = tune(TUNE_MVM, 1);  // 0: never, 1: from MIN_NC tokens, 2: from 2 tokens
     if (mode == 0 || nc < (mode == 2 ? 2 : Mfma<F>::MIN_NC) || nc > 16 || n_in % 256) return s;
     s.g = nc > 8 ? 2 : 1;
     const int nblk = n_in / 256;
     const int tiles = (n_out + 15) / 16;
-    int tpw = env_int("NMQ_MVM_TPW", 0);
+    int tpw = tune(TUNE_MVM_TPW, 0);
     if (tpw <= 0) tpw = (tiles + cus - 1) / cus;
     if (tpw > 16) tpw = 16;
-    int ks = env_int("NMQ_MVM_KS", 0);
+    int ks = tune(TUNE_MVM_KS, 0);
     if (ks <= 0) {
         ks = 1;
         while (ks * 2 * tpw <= 16 && nblk % (ks * 2) == 0) ks *= 2;

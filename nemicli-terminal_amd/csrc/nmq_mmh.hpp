@@ -282,7 +282,7 @@ constexpr int MMH_MAX_COLS = 64;  // tokens per launch (4 groups of 16)
 // Tiles per workgroup: the most (of 4, 2, 1) that still gives nearly every CU a workgroup.
 inline int plan_mmh_tiles(int n_out, int cus) {
     const int tiles = (n_out + 15) / 16;
-    const int e = env_int("NMQ_MMH_T", 0);
+    const int e = tune(TUNE_MMH_T, 0);
     if (e == 1 || e == 2 || e == 4) return e;
     if ((tiles + 3) / 4 >= cus * 7 / 8) return 4;
     if ((tiles + 1) / 2 >= cus * 7 / 8) return 2;
@@ -307,7 +307,7 @@ int launch_mmh(MmhParams p, hipStream_t stream) {
     p.row_bytes = (int64_t)p.nblk * Mfma<F>::BB;
     const int T = plan_mmh_tiles(p.n_out, di.cus);
     const int ng_all = (p.nc + 15) / 16;
-    const int eg = env_int("NMQ_MMH_G", 0);  // groups of 16 tokens per workgroup
+    const int eg = tune(TUNE_MMH_G, 0);  // groups of 16 tokens per workgroup
     const int ng = eg >= 1 && eg <= ng_all ? eg : ng_all;
     void (*k)(MmhParams) = T == 4 ? pick_mmh_ng<F, 4>(ng) : T == 2 ? pick_mmh_ng<F, 2>(ng) : pick_mmh_ng<F, 1>(ng);
     const int tiles = (p.n_out + 15) / 16;

@@ -17,6 +17,7 @@
 #include <stdlib.h>
 
 #include "nmq_device.hpp"
+#include "nmq_tune.hpp"
 
 namespace nmq {
 
@@ -1351,13 +1352,6 @@ inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf, bool ext, int hr = 0
     }
 }
 
-// Tuning overrides for timing runs (unset in normal use): NMQ_MV1=0 disables the one-token
-// kernel, NMQ_MV1_WPC sets its resident waves per CU, NMQ_MV1_RW its rows per team.
-inline int env_int(const char* name, int dflt) {
-    const char* v = getenv(name);
-    return v && *v ? atoi(v) : dflt;
-}
-
 }  // namespace nmq
 #include "nmq_mfma.hpp"
 #include "nmq_mmh.hpp"
@@ -1371,24 +1365,24 @@ struct Mv1Shape {
 
 inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
     Mv1Shape s{};
-    if (!env_int("NMQ_MV1", 1)) return s;
+    if (!tune(TUNE_MV1, 1)) return s;
     const int U = (n_in + 63) / 64;
     s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     const int nit = (U + s.T - 1) / s.T;
-    if (nit > env_int("NMQ_MV1_MAXNIT", 2)) return s;
+    if (nit > tune(TUNE_MV1_MAXNIT, 2)) return s;
     s.nitm = nit <= 1 ? 1 : (nit <= 2 ? 2 : 4);
-    s.rw = env_int("NMQ_MV1_RW", 1);
+    s.rw = tune(TUNE_MV1_RW, 1);
     s.rw = s.rw == 2 ? 2 : 1;
-    s.nbuf = env_int("NMQ_MV1_NBUF", 3) == 4 && s.nitm * s.rw <= 2 ? 4 : 3;
+    s.nbuf = tune(TUNE_MV1_NBUF, 3) == 4 && s.nitm * s.rw <= 2 ? 4 : 3;
     const int P = 64 / s.T;
     const int64_t steps = ((int64_t)n_out + P * s.rw - 1) / (P * s.rw);  // per instance
     // waves per CU: 16 for one matrix; 8 for gathered experts (many small matrices: fewer, longer-lived
     // waves amortise the input staging; measured on MI355X, MoE layer at one token 21.3 -> 18.6 us)
-    const int wpc = env_int("NMQ_MV1_WPC", n_mats > 1 ? 8 : 16);
+    const int wpc = tune(TUNE_MV1_WPC, n_mats > 1 ? 8 : 16);
     int64_t waves = (int64_t)wpc * di.cus / n_mats;
     if (waves < 1) waves = 1;
     if (waves > steps) waves = steps;
-    int wmax = env_int("NMQ_MV1_W", 8);
+    int wmax = tune(TUNE_MV1_W, 8);
     wmax = wmax < 1 ? 1 : (wmax > 8 ? 8 : wmax);  // launch bound: 512 threads
     s.W = (int)(waves < wmax ? waves : wmax);
     s.grid_x = (int)((waves + s.W - 1) / s.W);
@@ -1411,16 +1405,16 @@ struct MvlShape {
 inline MvlShape plan_mvl(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
     MvlShape s{};
     const int U = (n_in + 63) / 64;
-    if (U <= 128 || U > 256 || !env_int("NMQ_MVL", 1)) return s;
+    if (U <= 128 || U > 256 || !tune(TUNE_MVL, 1)) return s;
     s.nit = U <= 192 ? 3 : 4;
-    int64_t waves_max = (int64_t)env_int("NMQ_MVL_WPC", 16) * di.cus / n_mats;
+    int64_t waves_max = (int64_t)tune(TUNE_MVL_WPC, 16) * di.cus / n_mats;
     if (waves_max < 1) waves_max = 1;
     const int64_t groups = n_out;  // RW = 1
     s.pipe = groups > waves_max;
     int64_t waves = groups < waves_max ? groups : waves_max;
     if (waves < 1) waves = 1;
     const int wcap = s.pipe ? 8 : 16;  // launch bounds: 512 / 1024 threads
-    int wmax = env_int("NMQ_MVL_W", s.pipe ? 8 : 4);  // measured on MI355X: 4-wave workgroups (several
+    int wmax = tune(TUNE_MVL_W, s.pipe ? 8 : 4);  // measured on MI355X: 4-wave workgroups (several
                                                        // per CU) beat one 16-wave workgroup per CU
     wmax = wmax < 1 ? 1 : (wmax > wcap ? wcap : wmax);
     s.W = (int)(waves < wmax ? waves : wmax);
@@ -1530,11 +1524,11 @@ inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di, 
     s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     if (U > s.T) return s;  // one unit per lane only
     const int P = 64 / s.T;
-    const int wg_per_cu = env_int("NMQ_MVC_WGPC", 1);
+    const int wg_per_cu = tune(TUNE_MVC_WGPC, 1);
     int64_t wgs = (int64_t)di.cus * wg_per_cu / n_mats;
     if (wgs < 1) wgs = 1;
     const int64_t R = ((int64_t)n_out + wgs - 1) / wgs;  // rows per workgroup
-    int rw = env_int("NMQ_MVC_RW", 0);
+    int rw = tune(TUNE_MVC_RW, 0);
     if (rw <= 0 && !values && four_rows) {
         rw = 4;  // two-stage input, Q4_K / TQ2_0: 4 rows per team, fewer waves per workgroup (measured on
                  // MI355X: Q4_K 4096x4096 4.1 against 4.7 us, TQ2_0 4.2 against 4.4 us; Q8_0 and IQ2_XXS
@@ -1588,7 +1582,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         // (one unit per lane: rows of up to 4096 values; the NC input slices take about 65 + 34 NC VGPRs
         // (133 for 2 tokens, 174 for 3, 227 for 4), so 4-wave workgroups at 12 waves per CU for 2 tokens,
         // 8 for 3 and 4)
-        if (nc >= 2 && nc <= env_int("NMQ_MVT_MAX", 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
+        if (nc >= 2 && nc <= tune(TUNE_MVT_MAX, 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
             p.n_seg == 0) {
             const int U = (p.n_in + 63) / 64;
             const int T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
@@ -1597,7 +1591,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             const size_t lds = (size_t)nc * ktp * 9 / 4;
             const int W = 4;
             const int64_t steps = ((int64_t)p.n_out + P - 1) / P;
-            int64_t waves = (int64_t)env_int("NMQ_MVT_WPC", nc == 2 ? 12 : 8) * di.cus;
+            int64_t waves = (int64_t)tune(TUNE_MVT_WPC, nc == 2 ? 12 : 8) * di.cus;
             if (waves > steps) waves = steps;
             if (U <= 64 && ktp / 16 <= 64 * W && lds <= (size_t)di.lds_max) {
                 p.ktp = ktp;
@@ -1610,7 +1604,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     }
     if constexpr (F == NMQ_Q6_K) {
         // 2..4 tokens of one matrix with long rows (129..256 units): the long-row loop for all of them
-        if (nc >= 2 && nc <= env_int("NMQ_MVLT_MAX", 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
+        if (nc >= 2 && nc <= tune(TUNE_MVLT_MAX, 4) && nc <= 4 && p.ids == nullptr && p.xv == nullptr &&
             p.n_seg == 0) {
             const int U = (p.n_in + 63) / 64;
             const int ktp = (p.n_in + 127) / 128 * 128;
@@ -1646,8 +1640,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     const int64_t rows_per_cu = ((int64_t)p.n_out * n_mats + di.cus - 1) / di.cus;
     // rows per CU up to which chunk mode runs: 24 for one matrix, 64 for gathered experts (MoE layer at
     // one token, both expert launches in chunk mode: 17.9 against 18.5 us; at 4 tokens both stay above)
-    const int mvc_max = env_int("NMQ_MVC_ROWS", n_mats > 1 ? 64 : 24);
-    const int mode = env_int("NMQ_MV1_MODE", rows_per_cu > mvc_max ? 2 : 1);
+    const int mvc_max = tune(TUNE_MVC_ROWS, n_mats > 1 ? 64 : 24);
+    const int mode = tune(TUNE_MV1_MODE, rows_per_cu > mvc_max ? 2 : 1);
     if (nc == 1 && mode == 1) {
         const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di, p.xv != nullptr, F == NMQ_Q4_K || F == NMQ_TQ2_0);
         if (sc.ok) {
@@ -1677,7 +1671,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             // compiler-scheduled loop)
             int hr = 0;
             if (hand_format(F) && s1.rw == 1 && s1.nbuf == 3 && s1.nitm <= 2 && (F != NMQ_IQ2_XXS || s1.W >= 4) &&
-                env_int("NMQ_MV1_HR", 1) != 0) {
+                tune(TUNE_MV1_HR, 1) != 0) {
                 if (p.xv == nullptr) hr = s1.ktp / 16 <= 64 * s1.W ? 1 : 0;
                 else if (p.x_mode == NMQ_X_F32 || p.x_mode == NMQ_X_F32_BF16) hr = s1.ktp / 4 <= 2 * 64 * s1.W ? 2 : 0;
             }

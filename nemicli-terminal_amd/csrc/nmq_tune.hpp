@@ -1,0 +1,73 @@
+// Launch-plan overrides (timing runs and tests only; unset in normal use).
+//
+// Every knob has a compiled-in default chosen from measurements on MI355X; an override is set through
+// the C ABI (nmq_set_tuning / nmq_get_tuning) and read on the launch path with one relaxed atomic
+// load.  The environment is not consulted: a production process cannot change its kernel choice by
+// an inherited variable, and no launch pays for a getenv.
+#pragma once
+
+#include <atomic>
+#include <climits>
+#include <cstring>
+
+namespace nmq {
+
+enum Tune : int {
+    TUNE_MV1,         // 0 disables the persistent one-token kernel
+    TUNE_MV1_MAXNIT,  // most units per lane of the persistent one-token kernel
+    TUNE_MV1_RW,      // rows per team of the persistent one-token kernel (1, 2)
+    TUNE_MV1_NBUF,    // step buffers of the persistent one-token kernel (3, 4)
+    TUNE_MV1_WPC,     // its resident waves per CU
+    TUNE_MV1_W,       // its waves per workgroup
+    TUNE_MV1_MODE,    // 0: general kernel, 1: chunk kernel, 2: persistent kernel (one token)
+    TUNE_MV1_HR,      // 0: compiler-scheduled reads in the persistent kernel
+    TUNE_MVL,         // 0 disables the long-row kernel
+    TUNE_MVL_WPC,     // long-row kernel: resident waves per CU
+    TUNE_MVL_W,       // long-row kernel: waves per workgroup
+    TUNE_MVC_WGPC,    // chunk kernel: workgroups per CU
+    TUNE_MVC_RW,      // chunk kernel: rows per team
+    TUNE_MVC_ROWS,    // rows per CU up to which one token runs in the chunk kernel
+    TUNE_MVT_MAX,     // most tokens of the few-token Q4_K kernel (1 disables it)
+    TUNE_MVT_WPC,     // few-token Q4_K kernel: resident waves per CU
+    TUNE_MVLT_MAX,    // most tokens of the few-token long-row Q6_K kernel (1 disables it)
+    TUNE_MVM,         // matrix cores for 2..16 tokens: 0 never, 1 from the format's threshold, 2 from 2
+    TUNE_MVM_TPW,     // matrix-core kernel: row tiles per workgroup
+    TUNE_MVM_KS,      // matrix-core kernel: slices of the row
+    TUNE_MMH_T,       // fp16 matrix-core kernel: row tiles per workgroup
+    TUNE_MMH_G,       // fp16 matrix-core kernel: groups of 16 tokens per workgroup
+    TUNE_COUNT
+};
+
+// Names as the C ABI takes them (index = Tune).
+inline const char* const kTuneNames[TUNE_COUNT] = {
+    "MV1",      "MV1_MAXNIT", "MV1_RW",  "MV1_NBUF", "MV1_WPC", "MV1_W",   "MV1_MODE", "MV1_HR",
+    "MVL",      "MVL_WPC",    "MVL_W",   "MVC_WGPC", "MVC_RW",  "MVC_ROWS", "MVT_MAX", "MVT_WPC",
+    "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G"};
+
+constexpr int TUNE_UNSET = INT_MIN;
+
+// One table per process (an inline variable: every translation unit of the library shares it).
+inline std::atomic<int> g_tune[TUNE_COUNT] = {};
+inline std::atomic<bool> g_tune_ready{false};
+
+inline void tune_reset_all() {
+    for (int i = 0; i < TUNE_COUNT; ++i) g_tune[i].store(TUNE_UNSET, std::memory_order_relaxed);
+    g_tune_ready.store(true, std::memory_order_release);
+}
+
+inline int tune_index(const char* name) {
+    if (!name) return -1;
+    if (std::strncmp(name, "NMQ_", 4) == 0) name += 4;  // the prefix is optional
+    for (int i = 0; i < TUNE_COUNT; ++i)
+        if (std::strcmp(name, kTuneNames[i]) == 0) return i;
+    return -1;
+}
+
+// The override of knob k, or dflt when none is set.
+inline int tune(Tune k, int dflt) {
+    if (!g_tune_ready.load(std::memory_order_acquire)) return dflt;
+    const int v = g_tune[k].load(std::memory_order_relaxed);
+    return v == TUNE_UNSET ? dflt : v;
+}
+
+}  // namespace nmq

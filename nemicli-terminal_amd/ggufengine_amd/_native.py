@@ -7,9 +7,11 @@ every launch wrapper raise.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
+from typing import Optional
 
 import torch  # noqa: F401  (loads the HIP runtime first)
 
@@ -60,6 +62,9 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_block_sums.argtypes, L.nmq_block_sums.restype = [i, p, p, p, p, p, i, i, p], i
     L.nmq_dequant_bf16.argtypes, L.nmq_dequant_bf16.restype = [i, p, p, i64, p], i
     L.nmq_encode.argtypes, L.nmq_encode.restype = [i, p, i64, p, i], i64
+    L.nmq_stream_read.argtypes, L.nmq_stream_read.restype = [p, i64, p, i, i, i, p], i
+    L.nmq_set_tuning.argtypes, L.nmq_set_tuning.restype = [ctypes.c_char_p, i], i
+    L.nmq_get_tuning.argtypes, L.nmq_get_tuning.restype = [ctypes.c_char_p, p], i
     return L
 
 
@@ -115,3 +120,34 @@ def stream_ptr(device=None) -> int:
 
 def ptr(t) -> int:
     return 0 if t is None else t.data_ptr()
+
+
+TUNE_DEFAULT = -(1 << 31)
+
+
+def set_tuning(name: str, value: Optional[int]) -> None:
+    """Override a knob of the launch planner (None: back to its measured default)."""
+    rc = lib().nmq_set_tuning(name.encode(), TUNE_DEFAULT if value is None else int(value))
+    if rc:
+        raise ValueError(f"unknown tuning knob {name!r}")
+
+
+def get_tuning(name: str) -> Optional[int]:
+    v = ctypes.c_int(0)
+    if lib().nmq_get_tuning(name.encode(), ctypes.byref(v)):
+        raise ValueError(f"unknown tuning knob {name!r}")
+    return None if v.value == TUNE_DEFAULT else v.value
+
+
+@contextlib.contextmanager
+def tuning(**knobs):
+    """Launch-plan overrides for the duration of a with-block (timing runs and tests), restored after:
+    `with tuning(MVM=2, MVT_MAX=1): ...`."""
+    before = {k: get_tuning(k) for k in knobs}
+    try:
+        for k, v in knobs.items():
+            set_tuning(k, v)
+        yield
+    finally:
+        for k, v in before.items():
+            set_tuning(k, v)

@@ -1,18 +1,28 @@
 """
-Whole matrices streamed from pinned RAM into a ring of VRAM slots: the reference's `Fliessband`
-(models/common.py:295-361), used by `PackedLinear` for weights kept in RAM (`hostmem`).
+Whole matrices streamed from pinned RAM into a ring of VRAM slots (the contract of the reference's
+`Fliessband`, models/common.py:295-361), used by `PackedLinear` for weights kept in RAM (`hostmem`).
 
-Each matrix is copied whole, on a copy stream of its own (default priority), a few matrices ahead
-of its use, so a matrix read more than once (several tokens, prefill) is read from VRAM.  On MI355X
-a lone copy from pinned RAM runs at 54 GB/s and a pass over 8 Q4_K 4096x4096 layers through the ring
-at 44.6 GB/s; kernels reading RAM directly reach 52 GB/s.  Matrices are numbered in the order they are registered, which is their
-order of use in a forward pass; a number not above the previous one starts a new pass.  Ordering is
-by events only (no host synchronisation), so the band also runs inside a HIP graph capture:
+Contract.  Sources are registered in their order of use in a forward pass and numbered from 0.
+`holen(nr)` returns matrix nr's bytes in VRAM and queues the copies of the next matrices (up to PLAETZE
+slots ahead) on a copy stream of default priority; `fertig(nr)` says the computation on nr is queued.
+A number not above the previous one starts a new pass.  Ordering uses events only (no host waits):
 
-  - a copy into a slot waits for the last computation that read the slot (`fertig` records it);
-  - the computation waits for its matrix's copy (`holen` makes the current stream wait);
-  - at the start of a pass the copy stream waits for everything the compute stream has queued, so
-    slots from the previous pass are not overwritten while still being read.
+  - a copy into a slot waits for the last computation of this pass that read the slot;
+  - the computation on nr waits for nr's copy;
+  - a new pass makes the copy stream wait for everything the compute stream queued before, so the
+    previous pass's slots are not overwritten while still being read.
+
+A matrix handed out by `holen` stays lent until `fertig`: a copy that would overwrite it raises
+RuntimeError instead of racing with a computation that may not be queued yet.
+
+HIP graphs: a capture must cover whole passes (a decode step), as in the reference.  The copies a pass
+queues ahead belong to the stream state of that pass, so a pass cannot be split between captures, or
+between a capture and eager calls: `holen` raises RuntimeError when a pass started outside the current
+capture continues inside it, or the other way round.  A capture that ends inside a pass leaves copies
+on the copy stream that were never joined, which the capture's end reports as an error.
+
+Slots are PLAETZE equal views of one allocation whose stride is the largest source rounded up to 256
+bytes, so every slot starts aligned for the kernels' 16-byte weight reads.
 """
 from __future__ import annotations
 
@@ -20,93 +30,109 @@ from typing import List, Optional
 
 import torch
 
-PLAETZE = 4  # VRAM slots of the ring (reference schichten.BAND_PLAETZE)
+PLAETZE = 4          # VRAM slots of the ring (the reference's schichten.BAND_PLAETZE)
+SLOT_ALIGN = 256     # bytes
+
+
+class _Slot:
+    """One ring position: its bytes and what was last done to it."""
+
+    __slots__ = ("data", "holds", "landed", "freed", "read", "lent")
+
+    def __init__(self, data: torch.Tensor):
+        self.data = data
+        self.holds = -1                  # matrix copied (or being copied) into it this pass
+        self.landed = torch.cuda.Event()     # that copy has finished (copy stream)
+        self.freed = torch.cuda.Event()      # its last reader this pass has finished (compute stream)
+        self.read = False                # `freed` was recorded this pass
+        self.lent = -1                   # matrix handed out by holen() and not yet released
+
+    def forget(self) -> None:
+        self.holds, self.read = -1, False
 
 
 class Fliessband:
-    """Ring of `PLAETZE` VRAM slots fed from registered sources (reference common.py:295-361)."""
+    """Ring of PLAETZE VRAM slots fed from registered sources on a copy stream."""
 
     PLAETZE = PLAETZE
 
     def __init__(self, device):
         self.device = torch.device(device)
-        self.quellen: List[torch.Tensor] = []    # flat uint8 sources, in order of use
-        self._ring: Optional[torch.Tensor] = None
-        self._strom: Optional[torch.cuda.Stream] = None
-        self._inhalt: List[int] = []             # matrix held (or being copied) per slot, -1: none
-        self._gelesen: List[bool] = []           # the slot's "done" event belongs to this pass
-        self._ausgegeben: List[int] = []         # matrix handed out by holen() and not yet fertig(), -1: none
-        self._fertig: list = []                  # per slot: the last computation that read it
-        self._bereit: list = []                  # per slot: its copy has landed
-        self._zuletzt = 1 << 62                  # number of the last matrix handed out
+        self.quellen: List[torch.Tensor] = []
+        self._slots: List[_Slot] = []
+        self._copy: Optional[torch.cuda.Stream] = None
+        self._last = None                # number handed out last (None: no pass started)
+        self._pass_captured = False      # the current pass began inside a graph capture
 
     def anmelden(self, quelle: torch.Tensor) -> int:
-        """Register a source (any tensor the copy engine can read: pinned RAM or its GPU view); returns
-        its number.  Registration order is the order of use."""
-        if self._ring is not None:
+        """Register a source (pinned RAM, its GPU view, or device memory); returns its number."""
+        if self._slots:
             raise RuntimeError("Fliessband: sources are registered before the first holen()")
         self.quellen.append(quelle.reshape(-1).view(torch.uint8))
         return len(self.quellen) - 1
 
-    def _anlegen(self) -> None:
-        n = len(self.quellen)
-        if n == 0:
-            raise RuntimeError("Fliessband: no sources registered")
-        groesste = max(q.numel() for q in self.quellen)
-        self._ring = torch.empty(self.PLAETZE, groesste, dtype=torch.uint8, device=self.device)
-        self._strom = torch.cuda.Stream(self.device)
-        self._inhalt = [-1] * self.PLAETZE
-        self._gelesen = [False] * self.PLAETZE
-        self._ausgegeben = [-1] * self.PLAETZE
-        self._fertig = [torch.cuda.Event() for _ in range(self.PLAETZE)]
-        self._bereit = [torch.cuda.Event() for _ in range(self.PLAETZE)]
+    # -- internals -------------------------------------------------------------------------------
+    def _ring(self) -> List[_Slot]:
+        if not self._slots:
+            if not self.quellen:
+                raise RuntimeError("Fliessband: no sources registered")
+            stride = -(-max(q.numel() for q in self.quellen) // SLOT_ALIGN) * SLOT_ALIGN
+            block = torch.empty(self.PLAETZE * stride, dtype=torch.uint8, device=self.device)
+            self._slots = [_Slot(block[i * stride:(i + 1) * stride]) for i in range(self.PLAETZE)]
+            self._copy = torch.cuda.Stream(self.device)
+        return self._slots
 
-    def _laden(self, nr: int) -> None:
-        platz = nr % self.PLAETZE
-        if self._inhalt[platz] == nr:
+    def _new_pass(self, compute: torch.cuda.Stream) -> None:
+        lent = [s.lent for s in self._slots if s.lent >= 0]
+        if lent:
+            raise RuntimeError(f"Fliessband: a new pass starts while matrices {lent} are handed out and not "
+                               f"released by fertig()")
+        self._copy.wait_stream(compute)
+        for s in self._slots:
+            s.forget()
+
+    def _queue_copy(self, nr: int) -> None:
+        slot = self._slots[nr % self.PLAETZE]
+        if slot.holds == nr:
             return
-        if self._ausgegeben[platz] >= 0:         # its computation may not even be queued yet
-            raise RuntimeError(f"Fliessband: matrix {nr} would overwrite matrix {self._ausgegeben[platz]}, "
-                               f"which holen() handed out and fertig() has not released")
-        if self._gelesen[platz]:                 # its reader in this pass must be done first
-            self._strom.wait_event(self._fertig[platz])
-        q = self.quellen[nr]
-        with torch.cuda.stream(self._strom):
-            self._ring[platz, :q.numel()].copy_(q, non_blocking=True)
-            self._bereit[platz].record(self._strom)
-        self._inhalt[platz] = nr
-        self._gelesen[platz] = False
+        if slot.lent >= 0:
+            raise RuntimeError(f"Fliessband: matrix {nr} would overwrite matrix {slot.lent}, which holen() "
+                               f"handed out and fertig() has not released")
+        if slot.read:
+            self._copy.wait_event(slot.freed)
+        src = self.quellen[nr]
+        with torch.cuda.stream(self._copy):
+            slot.data[:src.numel()].copy_(src, non_blocking=True)
+            slot.landed.record(self._copy)
+        slot.holds, slot.read = nr, False
 
+    # -- API -------------------------------------------------------------------------------------
     def holen(self, nr: int) -> torch.Tensor:
-        """The bytes of matrix `nr` in VRAM (the current stream waits for their copy); the copies of the
-        next PLAETZE - 1 matrices are queued behind it.  Every matrix handed out is released with
-        `fertig(nr)` once its computation is queued; a copy that would overwrite a matrix not yet
-        released raises RuntimeError (the band's state is unchanged for that slot)."""
+        """Matrix nr's bytes in its VRAM slot; the current stream waits for their copy, and the copies of
+        the following matrices are queued behind it."""
         if not 0 <= nr < len(self.quellen):
             raise IndexError(f"Fliessband: matrix {nr} of {len(self.quellen)}")
-        if self._ring is None:
-            self._anlegen()
-        rechnen = torch.cuda.current_stream(self.device)
-        if nr <= self._zuletzt:                  # a new pass: nothing queued before may be overwritten early
-            offen = [a for a in self._ausgegeben if a >= 0]
-            if offen:
-                raise RuntimeError(f"Fliessband: a new pass starts at matrix {nr} while matrices {offen} are "
-                                   f"handed out and not released by fertig()")
-            self._strom.wait_stream(rechnen)
-            self._inhalt = [-1] * self.PLAETZE
-            self._gelesen = [False] * self.PLAETZE
+        slots = self._ring()
+        compute = torch.cuda.current_stream(self.device)
+        capturing = torch.cuda.is_current_stream_capturing()
+        if self._last is None or nr <= self._last:
+            self._new_pass(compute)
+            self._pass_captured = capturing
+        elif capturing != self._pass_captured:
+            raise RuntimeError("Fliessband: a pass is split between a graph capture and eager calls; a "
+                               "capture must cover whole passes")
         for k in range(nr, min(nr + self.PLAETZE, len(self.quellen))):
-            self._laden(k)
-        self._zuletzt = nr                       # after the copies: a refused holen() can be retried in its pass
-        platz = nr % self.PLAETZE
-        rechnen.wait_event(self._bereit[platz])
-        self._ausgegeben[platz] = nr
-        return self._ring[platz, :self.quellen[nr].numel()]
+            self._queue_copy(k)
+        self._last = nr                  # set after the copies: a refused call can be retried
+        slot = slots[nr % self.PLAETZE]
+        compute.wait_event(slot.landed)
+        slot.lent = nr
+        return slot.data[:self.quellen[nr].numel()]
 
     def fertig(self, nr: int) -> None:
-        """The computation on matrix `nr` is queued: its slot may be refilled after it."""
-        platz = nr % self.PLAETZE
-        self._fertig[platz].record(torch.cuda.current_stream(self.device))
-        self._gelesen[platz] = True
-        if self._ausgegeben[platz] == nr:
-            self._ausgegeben[platz] = -1
+        """The computation on matrix nr is queued on the current stream: its slot may be refilled after it."""
+        slot = self._slots[nr % self.PLAETZE]
+        slot.freed.record(torch.cuda.current_stream(self.device))
+        slot.read = True
+        if slot.lent == nr:
+            slot.lent = -1

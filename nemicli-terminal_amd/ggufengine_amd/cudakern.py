@@ -21,8 +21,10 @@ from .mmvq import _starten, _werte, eingang_bf16
 
 THREADS = 256
 FORMATE = {"Q4_0": (32, 18), "Q8_0": (32, 34), "Q4_K": (256, 144), "Q6_K": (256, 210), "IQ2_XXS": (256, 66), "TQ2_0": (256, 66)}
-# formats without an int4 path in the reference (qlinear): they always stay in block format
-IMMER_GEPACKT = frozenset(("IQ2_XXS", "TQ2_0"))
+# formats that always stay in their block bytes.  In the reference these are the formats without an int4
+# repack in qlinear; this library repacks nothing, so every format it serves is one (the reference's
+# loader then builds PackedExperts, the gathered kernel, for their expert tensors, models/common.py:215)
+IMMER_GEPACKT = frozenset(FORMATE)
 MM_ZEILEN = 16
 MM_GROESSEN = tuple(range(2, MM_ZEILEN + 1))
 MAX_N_IN = 1 << 20

@@ -25,13 +25,16 @@ from typing import Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from . import _native, cudakern
+from . import _native, cudakern, hostmem
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
 from .mmvq import WERTE_BIS, Eingang, _starten, _werte, eingang_bf16
 
 
 class PackedExperts:
-    """Expert tensor (n_exp, n_out, n_in) kept in its GGUF block format (reference common.py:434-480)."""
+    """All experts of one tensor (n_exp, n_out, n_in) in their GGUF block bytes, multiplied on the device
+    by the expert-id-gathered kernel (the reference's PackedExperts, models/common.py:434-480).  The ids
+    stay on the device, so a captured graph follows new routings.  `adressen` (int64 (n_exp,) on the
+    device), when set, gives each expert's address instead of the `per_expert` stride of `raw`."""
 
     def __init__(self, raw: torch.Tensor, ggml_type: int, n_exp: int, n_out: int, n_in: int,
                  dtype: torch.dtype = torch.bfloat16):
@@ -49,24 +52,61 @@ class PackedExperts:
         self.dtype = dtype
         self.name = name
         self.kernel = True
-        self.adressen: Optional[torch.Tensor] = None   # optional address table (n_exp,) int64 on the GPU
+        self.im_ram = hostmem.abgebildet(raw)          # the bytes sit in pinned host memory
+        self.adressen: Optional[torch.Tensor] = None
+
+    @classmethod
+    def aus_quantlinear(cls, experten, dtype: torch.dtype = torch.bfloat16) -> "PackedExperts":
+        """One expert tensor from a list of qlinear.QuantLinear layers of one format and shape (no bias).
+        Their bytes are used in place when they lie back to back in one allocation (the reference's
+        loader cuts experts out of one tensor that way), else copied together once."""
+        if not experten:
+            raise GGUFError("aus_quantlinear: no experts")
+        first = experten[0]
+        if any(e.ggml_type != first.ggml_type or (e.n_out, e.n_in) != (first.n_out, first.n_in) or e.b is not None
+               for e in experten):
+            raise GGUFError("aus_quantlinear: experts differ in format or shape, or carry a bias")
+        per, n = first.raw.numel(), len(experten)
+        store, off = first.raw.untyped_storage(), first.raw.storage_offset()
+        back_to_back = all(e.raw.untyped_storage().data_ptr() == store.data_ptr() and e.raw.is_contiguous()
+                           and e.raw.storage_offset() == off + i * per for i, e in enumerate(experten))
+        if back_to_back and off + per * n <= store.nbytes():
+            whole = torch.empty(0, dtype=torch.uint8, device=first.raw.device).set_(store, off, (per * n,), (1,))
+        else:
+            whole = torch.cat([e.raw.reshape(-1) for e in experten])
+        return cls(whole, first.ggml_type, len(experten), first.n_out, first.n_in, dtype)
 
     def __len__(self) -> int:
         return self.n_exp
 
-    def matvec(self, ids: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
-        """The experts `ids` (k,) applied to one shared input x (n_in,) -> (k, n_out) float32."""
-        return cudakern.mv(self.name, self.raw, ids, x.reshape(-1), self.n_out, self.n_in, self.adressen)
-
-    def matvec_je(self, ids: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
-        """Expert ids[j] applied to its own input a[j]: (k, n_in) -> (k, n_out) float32."""
-        return cudakern.mv(self.name, self.raw, ids, a.reshape(ids.numel(), -1), self.n_out, self.n_in,
-                           self.adressen)
-
     def _quelle(self, dev):
+        """(tensor, per_expert) for the kernels: the stride of raw, or the address table (per = -1)."""
         if self.adressen is None:
             return self.raw, self.raw.shape[1]
         return self.adressen.to(dev, torch.int64).contiguous(), -1
+
+    def matvec(self, ids: torch.Tensor, x: torch.Tensor) -> torch.Tensor:
+        """ids (k,) on one input x (n_in,) -> float32 (k, n_out), row j from expert ids[j]."""
+        return cudakern.mv(self.name, self.raw, ids, x.reshape(-1), self.n_out, self.n_in, self.adressen)
+
+    def matvec_je(self, ids: torch.Tensor, a: torch.Tensor) -> torch.Tensor:
+        """ids (k,) with one input row each, a (k, n_in) -> float32 (k, n_out): expert ids[j] on a[j]."""
+        return cudakern.mv(self.name, self.raw, ids, a.reshape(ids.numel(), -1), self.n_out, self.n_in,
+                           self.adressen)
+
+    def weights(self, ids: torch.Tensor) -> torch.Tensor:
+        """The experts ids (k,) unpacked on the device: (k, n_out, n_in) in the compute dtype (exact values
+        rounded to bf16 first)."""
+        from .packed import unpack
+        ids = ids.to(self.raw.device, torch.int64).reshape(-1)
+        blocks = self.raw.index_select(0, ids).reshape(-1)
+        w = unpack(self.ggml_type, blocks, ids.numel() * self.n_out, self.n_in)
+        return w.view(-1, self.n_out, self.n_in).to(self.dtype)
+
+    def __getitem__(self, e: int) -> "_OneExpert":
+        if not 0 <= e < self.n_exp:
+            raise IndexError(e)
+        return _OneExpert(self, e)
 
     def matvec_tokens(self, ids: torch.Tensor, x) -> torch.Tensor:
         """ids (L, k), x (L, n_in) or its Eingang: expert ids[t, j] applied to token t's input ->
@@ -97,69 +137,116 @@ class PackedExperts:
         return y
 
 
-class ExpertenLager:
-    """VRAM slots for the most used experts of one layer whose tensors live in pinned RAM (reference
-    models/moe.py:133-192; the RAM side from `hostmem.empty` / `hostmem.abbilden`).
+class _OneExpert:
+    """Expert e of a PackedExperts as a linear layer: x (..., n_in) -> (..., n_out) in the compute dtype,
+    through the gathered kernel for one row and the unpacked weights for more."""
 
-    Every part (gate, up, down ...) gets an address table on the GPU with one entry per expert: its
-    slot in VRAM or its bytes in RAM.  The gathered kernels read through the table, so a HIP graph
-    keeps working when experts move.  `zaehlen(ids)` counts on the GPU how often each expert is
-    chosen (also inside a graph); `umsortieren()` (between steps, never inside a graph) moves the
-    most used ones into the slots, after which the counts fade by half."""
+    def __init__(self, owner: PackedExperts, e: int):
+        self.owner, self.e = owner, e
+        self.n_out, self.n_in = owner.n_out, owner.n_in
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        rows = x.reshape(-1, self.n_in)
+        ids = torch.full((rows.shape[0],), self.e, dtype=torch.int64, device=self.owner.geraet)
+        if rows.shape[0] == 1:
+            y = self.owner.matvec_je(ids, rows).to(self.owner.dtype)
+        else:
+            w = self.owner.weights(ids[:1])[0]
+            y = rows.to(w.dtype) @ w.t()
+        return y.reshape(*x.shape[:-1], self.n_out)
+
+
+class ExpertenLager:
+    """The most chosen experts of one MoE layer, whose tensors live in pinned host memory, held in `plaetze`
+    VRAM slots (the reference's ExpertenLager, models/moe.py:133-192).
+
+    State: `zaehler` (device, fp32) counts how often each expert was chosen, decaying by half at every
+    re-sort; `_slot` (host, int64) maps each expert to its slot or -1.  Each part (gate, up, down ...) owns
+    a slot array `cache[i]` (plaetze x bytes per expert) and an address table `adressen` (device, int64,
+    one entry per expert: its slot or its host bytes) that the gathered kernels read, so captured graphs
+    stay valid while experts move.  Counting (`zaehlen`) is graph-safe; re-sorting (`umsortieren`) copies
+    between steps, never inside a capture."""
 
     def __init__(self, teile, plaetze: int, device):
         self.teile = list(teile)
-        self.n_exp = self.teile[0].n_exp
-        self.plaetze = min(int(plaetze), self.n_exp)
+        n = self.teile[0].n_exp
+        self.n_exp = n
+        self.plaetze = max(0, min(int(plaetze), n))
         self.device = torch.device(device)
-        self.zaehler = torch.zeros(self.n_exp, dtype=torch.float32, device=self.device)
-        self.belegt = list(range(self.plaetze))           # expert held by each slot
+        self.zaehler = torch.zeros(n, dtype=torch.float32, device=self.device)
+        self._eins = torch.ones(0, dtype=torch.float32, device=self.device)
+        self._slot = torch.full((n,), -1, dtype=torch.int64)
+        first = torch.arange(self.plaetze, dtype=torch.int64)
+        self._slot[first] = first                       # experts 0 .. plaetze-1 start in the slots
         self.cache = [torch.empty(self.plaetze, t.raw.shape[1], dtype=torch.uint8, device=self.device)
                       for t in self.teile]
-        for c, t in zip(self.cache, self.teile):
-            c.copy_(t.raw[:self.plaetze], non_blocking=True)
-            t.adressen = torch.empty(self.n_exp, dtype=torch.int64, device=self.device)
+        for t in self.teile:
+            t.adressen = torch.empty(n, dtype=torch.int64, device=self.device)
+        self._einlagern(first, first)
         self.verankern()
 
-    def _tabelle(self, t: PackedExperts, c: torch.Tensor) -> torch.Tensor:
-        per = t.raw.shape[1]
-        table = torch.arange(self.n_exp, dtype=torch.int64) * per + t.raw.data_ptr()
-        if self.plaetze:
-            table[torch.tensor(self.belegt)] = torch.arange(self.plaetze, dtype=torch.int64) * per + c.data_ptr()
-        return table
+    @property
+    def belegt(self) -> list:
+        """Expert held by each slot."""
+        held = torch.nonzero(self._slot >= 0).flatten()
+        out = [-1] * self.plaetze
+        for e, s in zip(held.tolist(), self._slot[held].tolist()):
+            out[s] = e
+        return out
+
+    def _einlagern(self, slots: torch.Tensor, experten: torch.Tensor) -> None:
+        """cache[slot] <- the expert's bytes, for every part, one gather + scatter each."""
+        if slots.numel() == 0:
+            return
+        s = slots.to(self.device)
+        for t, c in zip(self.teile, self.cache):
+            c.index_copy_(0, s, t.raw.index_select(0, experten.to(t.raw.device)).to(self.device, non_blocking=True))
 
     def verankern(self) -> None:
-        """Write the address tables from the current slots (again after the slots moved)."""
+        """Rewrite every part's address table from the current slot map (also after the slots were
+        re-filled from elsewhere)."""
+        held = self._slot >= 0
         for t, c in zip(self.teile, self.cache):
-            t.adressen.copy_(self._tabelle(t, c))
+            per = t.raw.shape[1]
+            host = t.raw.data_ptr() + torch.arange(self.n_exp, dtype=torch.int64) * per
+            if self.plaetze:
+                host = torch.where(held, c.data_ptr() + self._slot.clamp(min=0) * per, host)
+            t.adressen.copy_(host)
 
     def zaehlen(self, ids: torch.Tensor) -> None:
-        """Count the chosen experts (any shape, on the GPU)."""
-        ids = ids.reshape(-1)
-        self.zaehler.index_add_(0, ids, torch.ones(ids.numel(), dtype=torch.float32, device=ids.device))
+        """Add one to the count of every chosen expert (ids of any shape, on the device; graph-safe)."""
+        flat = ids.reshape(-1).to(self.device, torch.int64)
+        if self._eins.numel() < flat.numel():
+            self._eins = torch.ones(flat.numel(), dtype=torch.float32, device=self.device)
+        self.zaehler.scatter_add_(0, flat, self._eins[:flat.numel()])
 
     def treffer(self) -> float:
-        """Share of the counted choices that the slots hold now."""
-        total = float(self.zaehler.sum())
-        return float(self.zaehler[self.belegt].sum()) / total if total and self.plaetze else 0.0
+        """Fraction of the (decayed) counted choices that fall on experts in the slots."""
+        c = self.zaehler.cpu()
+        total = float(c.sum())
+        if not self.plaetze or total == 0.0:
+            return 0.0
+        return float(c[self._slot >= 0].sum()) / total
 
     def umsortieren(self) -> int:
-        """The most used experts into the slots; returns how many moved in."""
+        """Move the `plaetze` most counted experts into the slots (each evicted expert's slot goes to one
+        newcomer); halve the counts.  Returns the number of experts copied in."""
         if not self.plaetze:
             return 0
-        top = self.zaehler.topk(self.plaetze).indices.tolist()
-        held = set(self.belegt)
-        wanted = set(top)
-        free = [p for p, e in enumerate(self.belegt) if e not in wanted]
-        incoming = [e for e in top if e not in held]
-        for p, e in zip(free, incoming):
-            for t, c in zip(self.teile, self.cache):
-                c[p].copy_(t.raw[e], non_blocking=True)
-            self.belegt[p] = e
-        if incoming:
+        want = torch.topk(self.zaehler.cpu(), self.plaetze).indices
+        wanted = torch.zeros(self.n_exp, dtype=torch.bool)
+        wanted[want] = True
+        resident = self._slot >= 0
+        leaving = torch.nonzero(resident & ~wanted).flatten()
+        coming = want[~resident[want]]
+        if coming.numel():
+            slots = self._slot[leaving]
+            self._slot[leaving] = -1
+            self._slot[coming] = slots
+            self._einlagern(slots, coming)
             self.verankern()
         self.zaehler.mul_(0.5)
-        return len(incoming)
+        return int(coming.numel())
 
 
 def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float = 1.0

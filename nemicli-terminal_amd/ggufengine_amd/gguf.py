@@ -1,24 +1,24 @@
 """
-GGUF files for this library: the reference's checked reader (ggufengine/gguf.py:171-369) with its API
-(`GGUFFile`, `TensorInfo`, `GGUFError`, the value-type ids and limits), the upload of a tensor's raw
-block bytes to the GPU the way the reference's weight loader does it (models/common.py:83-116: large
-file reads into a ring of pinned buffers, copies on a copy stream), and a writer for GGUF files (the
-tests and synthetic models build theirs with it).
+GGUF files for this library: a checked reader with the reference's API (`GGUFFile`, `TensorInfo`,
+`GGUFError`, the value-type ids and limits; contract of ggufengine/gguf.py:171-369), the upload of a
+tensor's raw block bytes to the GPU (the reference's weight loader, models/common.py:83-116: large file
+reads into a ring of pinned buffers, copies on a copy stream), and a writer (the tests and synthetic
+models build their files with it).
 
-The reader treats every byte of the file as untrusted: every length and count is bounded before it is
-used, the header is read through one bounds-checked cursor, tensors must be aligned, inside the data
-section and must not overlap, and any violation raises GGUFError (no other exception type, no
-unbounded allocation).  Tensor bytes are served as read-only views of a memory map or read into a
-caller's buffer with plain file reads.
+Every byte of the file is untrusted.  Reading happens in two stages: `_scan` walks the header through one
+bounds-checked cursor (every length and count bounded before use, metadata budgets counted), then
+`_place` turns the tensor records into TensorInfos and checks them in one sweep in offset order
+(aligned, inside the data section, no overlap).  Any violation raises GGUFError and nothing else, and no
+allocation is sized from an unchecked number.  Tensor bytes are read-only views of a memory map or
+positional reads into a caller's buffer.
 """
 from __future__ import annotations
 
 import mmap
 import os
 import struct
-import threading
 from dataclasses import dataclass
-from typing import Any, Dict, List, Optional, Sequence, Tuple
+from typing import Any, Dict, List, NamedTuple, Optional, Sequence, Tuple
 
 from .gguf_types import GGML_ALL_TYPES, GGUFError
 
@@ -146,157 +146,166 @@ class _Header:
         raise GGUFError(f"unknown array element type {etype}")
 
 
+class _Scan(NamedTuple):
+    version: int
+    metadata: Dict[str, Any]
+    records: List[Tuple[str, Tuple[int, ...], int, int]]   # name, dims, ggml type, offset
+    end: int                                                 # first byte after the tensor records
+
+
+def _scan(buf, size: int) -> _Scan:
+    """The header: magic, version, counts, metadata, tensor records, every read bounded."""
+    h = _Header(buf, size)
+    at = h.take(4)
+    if bytes(buf[at:at + 4]) != GGUF_MAGIC:
+        raise GGUFError("bad magic (not a GGUF file)")
+    version = h.fixed("I")
+    if version not in SUPPORTED_VERSIONS:
+        raise GGUFError(f"GGUF version {version} (supported: {SUPPORTED_VERSIONS})")
+    n_tensors, n_kv = h.fixed("Q"), h.fixed("Q")
+    if n_tensors > MAX_TENSORS or n_kv > MAX_KV:
+        raise GGUFError(f"{n_tensors} tensors / {n_kv} metadata entries exceed the limits")
+    meta: Dict[str, Any] = {}
+    for _ in range(n_kv):
+        key = h.text(MAX_NAME)
+        if not key:
+            raise GGUFError("empty metadata key")
+        if key in meta:
+            raise GGUFError(f"metadata key {key!r} appears twice")
+        meta[key] = h.value(h.fixed("I"))
+    records = []
+    for _ in range(n_tensors):
+        name = h.text(MAX_NAME)
+        if not name:
+            raise GGUFError("empty tensor name")
+        n_dims = h.fixed("I")
+        if not 1 <= n_dims <= MAX_DIMS:
+            raise GGUFError(f"tensor {name!r}: {n_dims} dimensions")
+        dims = tuple(h.fixed("Q") for _ in range(n_dims))
+        records.append((name, dims, h.fixed("I"), h.fixed("Q")))
+    return _Scan(version, meta, records, h.pos)
+
+
+def _alignment(meta: Dict[str, Any]) -> int:
+    a = meta.get("general.alignment", DEFAULT_ALIGNMENT)
+    if type(a) is not int or not MIN_ALIGNMENT <= a <= MAX_ALIGNMENT or a & (a - 1):
+        raise GGUFError(f"general.alignment {a!r} is not a power of two in [{MIN_ALIGNMENT}, {MAX_ALIGNMENT}]")
+    return a
+
+
+def _place(records, align: int, data_size: int) -> List[TensorInfo]:
+    """TensorInfos in file order, after one sweep in offset order that checks alignment, extent and
+    overlap and reads a 64-value Q2_0 tensor that only fits the room before the next tensor with
+    128-value blocks as PQ2_0 (a fork's older files)."""
+    infos = [tensor_info(*r) for r in records]
+    seen = set()
+    for ti in infos:
+        if ti.name in seen:
+            raise GGUFError(f"tensor name {ti.name!r} appears twice")
+        seen.add(ti.name)
+    order = sorted(range(len(infos)), key=lambda i: infos[i].offset)
+    end_prev = 0
+    for pos, i in enumerate(order):
+        ti = infos[i]
+        room = (infos[order[pos + 1]].offset if pos + 1 < len(order) else data_size) - ti.offset
+        if ti.ggml_type == Q2_0 and ti.n_bytes > room:
+            wide = tensor_info(ti.name, ti.dims, PQ2_0, ti.offset)
+            if wide.n_bytes <= room:
+                ti = infos[i] = wide
+        if ti.offset % align:
+            raise GGUFError(f"tensor {ti.name!r}: offset {ti.offset} not a multiple of {align}")
+        if ti.offset > data_size or ti.n_bytes > data_size - ti.offset:
+            raise GGUFError(f"tensor {ti.name!r} ({ti.n_bytes} bytes at {ti.offset}) runs past the end of "
+                            f"the data section ({data_size} bytes)")
+        if ti.offset < end_prev:
+            raise GGUFError(f"tensor {ti.name!r} overlaps the tensor before it")
+        end_prev = ti.offset + ti.n_bytes
+    return infos
+
+
 class GGUFFile:
-    """A checked, read-only view of a GGUF file (version 2 or 3)."""
+    """A checked, read-only GGUF file (version 2 or 3): `version`, `alignment`, `metadata`, `tensors`
+    (by name), `tensor_list` (file order), `data_offset`, `file_size`.  Tensor bytes come as read-only
+    views of a memory map (`tensor_bytes`) or as positional reads into a caller's buffer (`read_into`,
+    safe from several threads: no shared file position)."""
 
     def __init__(self, path):
         self.path = os.fspath(path)
-        self._fh = open(self.path, "rb")
-        self._read_lock = threading.Lock()   # read_into: seek + read on the shared handle
         self._mm = None
+        self._fd = os.open(self.path, os.O_RDONLY | getattr(os, "O_CLOEXEC", 0))
         try:
-            self.file_size = os.fstat(self._fh.fileno()).st_size
+            self.file_size = os.fstat(self._fd).st_size
             if self.file_size < 24:
                 raise GGUFError("file too small to be GGUF")
-            self._mm = mmap.mmap(self._fh.fileno(), 0, access=mmap.ACCESS_READ)
-            self.metadata: Dict[str, Any] = {}
-            self.tensors: Dict[str, TensorInfo] = {}
-            self.tensor_list: List[TensorInfo] = []
-            self._parse()
+            self._mm = mmap.mmap(self._fd, 0, access=mmap.ACCESS_READ)
+            head = _scan(self._mm, self.file_size)
+            self.version, self.metadata = head.version, head.metadata
+            self.alignment = _alignment(self.metadata)
+            self.data_offset = -(-head.end // self.alignment) * self.alignment
+            if self.data_offset > self.file_size:
+                raise GGUFError("data section starts past the end of the file")
+            self.tensor_list = _place(head.records, self.alignment, self.file_size - self.data_offset)
+            self.tensors: Dict[str, TensorInfo] = {ti.name: ti for ti in self.tensor_list}
         except BaseException:
             self.close()
             raise
 
-    def _parse(self) -> None:
-        h = _Header(self._mm, self.file_size)
-        at = h.take(4)
-        if bytes(self._mm[at:at + 4]) != GGUF_MAGIC:
-            raise GGUFError("bad magic (not a GGUF file)")
-        self.version = h.fixed("I")
-        if self.version not in SUPPORTED_VERSIONS:
-            raise GGUFError(f"GGUF version {self.version} (supported: {SUPPORTED_VERSIONS})")
-        n_tensors, n_kv = h.fixed("Q"), h.fixed("Q")
-        if n_tensors > MAX_TENSORS or n_kv > MAX_KV:
-            raise GGUFError(f"{n_tensors} tensors / {n_kv} metadata entries exceed the limits")
-        for _ in range(n_kv):
-            key = h.text(MAX_NAME)
-            if not key:
-                raise GGUFError("empty metadata key")
-            if key in self.metadata:
-                raise GGUFError(f"metadata key {key!r} appears twice")
-            self.metadata[key] = h.value(h.fixed("I"))
-        align = self.metadata.get("general.alignment", DEFAULT_ALIGNMENT)
-        if (type(align) is not int or not MIN_ALIGNMENT <= align <= MAX_ALIGNMENT
-                or align & (align - 1)):
-            raise GGUFError(f"general.alignment {align!r} is not a power of two in "
-                            f"[{MIN_ALIGNMENT}, {MAX_ALIGNMENT}]")
-        self.alignment = align
-        infos = []
-        for _ in range(n_tensors):
-            name = h.text(MAX_NAME)
-            if not name:
-                raise GGUFError("empty tensor name")
-            n_dims = h.fixed("I")
-            if not 1 <= n_dims <= MAX_DIMS:
-                raise GGUFError(f"tensor {name!r}: {n_dims} dimensions")
-            dims = [h.fixed("Q") for _ in range(n_dims)]
-            ggml_type, offset = h.fixed("I"), h.fixed("Q")
-            infos.append(tensor_info(name, dims, ggml_type, offset))
-        self.data_offset = -(-h.pos // align) * align
-        if self.data_offset > self.file_size:
-            raise GGUFError("data section starts past the end of the file")
-        data_size = self.file_size - self.data_offset
-        infos = self._wide_q2_0(infos, data_size)
-        for ti in infos:
-            if ti.name in self.tensors:
-                raise GGUFError(f"tensor name {ti.name!r} appears twice")
-            if ti.offset % align:
-                raise GGUFError(f"tensor {ti.name!r}: offset {ti.offset} not a multiple of {align}")
-            if ti.offset > data_size or ti.n_bytes > data_size - ti.offset:
-                raise GGUFError(f"tensor {ti.name!r} ({ti.n_bytes} bytes at {ti.offset}) runs past the end "
-                                f"of the data section ({data_size} bytes)")
-            self.tensors[ti.name] = ti
-            self.tensor_list.append(ti)
-        last_end = 0
-        for ti in sorted(infos, key=lambda t: t.offset):
-            if ti.offset < last_end:
-                raise GGUFError(f"tensor {ti.name!r} overlaps the tensor before it")
-            last_end = ti.offset + ti.n_bytes
-
-    @staticmethod
-    def _wide_q2_0(infos: List[TensorInfo], data_size: int) -> List[TensorInfo]:
-        """Q2_0 blocks hold 64 values; older files of a fork used the same id for 128-value blocks (now
-        PQ2_0, gguf.py:272-290).  A Q2_0 tensor that does not fit in the room up to the next tensor at
-        64 values per block but does at 128 is read as PQ2_0."""
-        if all(ti.ggml_type != Q2_0 for ti in infos):
-            return infos
-        by_offset = sorted(infos, key=lambda t: t.offset)
-        room = {}
-        for i, ti in enumerate(by_offset):
-            nxt = by_offset[i + 1].offset if i + 1 < len(by_offset) else data_size
-            room[ti.name, ti.offset] = nxt - ti.offset
-        out = []
-        for ti in infos:
-            space = room[ti.name, ti.offset]
-            if ti.ggml_type == Q2_0 and ti.n_bytes > space:
-                wide = tensor_info(ti.name, ti.dims, PQ2_0, ti.offset)
-                if wide.n_bytes <= space:
-                    ti = wide
-            out.append(ti)
-        return out
-
-    # ---- access ---------------------------------------------------------------------------------
-    @property
-    def architecture(self) -> str:
-        arch = self.metadata.get("general.architecture")
-        if not isinstance(arch, str):
-            raise GGUFError("general.architecture missing")
-        return arch
-
+    # ---- metadata ------------------------------------------------------------------------------
     def get(self, key: str, default=None):
         return self.metadata.get(key, default)
 
     def require(self, key: str):
-        if key not in self.metadata:
-            raise GGUFError(f"required metadata key {key!r} missing")
-        return self.metadata[key]
+        try:
+            return self.metadata[key]
+        except KeyError:
+            raise GGUFError(f"required metadata key {key!r} missing") from None
 
-    def tensor_bytes(self, ti: TensorInfo) -> memoryview:
-        """Read-only view of the tensor's bytes in the memory map (no copy)."""
-        start = self.data_offset + ti.offset
-        if start + ti.n_bytes > self.file_size:
-            raise GGUFError("tensor out of bounds")
-        return memoryview(self._mm)[start:start + ti.n_bytes]
+    @property
+    def architecture(self) -> str:
+        arch = self.metadata.get("general.architecture")
+        if isinstance(arch, str):
+            return arch
+        raise GGUFError("general.architecture missing or not a string")
 
-    def read_into(self, ti: TensorInfo, out, start: int = 0) -> int:
-        """Copy tensor bytes [start, start + len(out)) into the writable buffer `out` with plain file
-        reads (large sequential requests instead of page faults on the map); stops at the tensor's
-        end and returns the number of bytes read."""
-        view = memoryview(out).cast("B")
-        if not 0 <= start <= ti.n_bytes:
-            raise GGUFError("read outside the tensor")
-        n = min(view.nbytes, ti.n_bytes - start)
+    # ---- tensor bytes --------------------------------------------------------------------------
+    def _span(self, ti: TensorInfo, start: int, n: int) -> int:
         pos = self.data_offset + ti.offset + start
         if pos + n > self.file_size:
             raise GGUFError("tensor out of bounds")
-        with self._read_lock:
-            self._fh.seek(pos)
-            done = 0
-            while done < n:
-                k = self._fh.readinto(view[done:n])
-                if not k:
-                    raise GGUFError("unexpected end of file")
-                done += k
+        return pos
+
+    def tensor_bytes(self, ti: TensorInfo) -> memoryview:
+        """Read-only view of the tensor's bytes in the memory map (no copy)."""
+        pos = self._span(ti, 0, ti.n_bytes)
+        return memoryview(self._mm)[pos:pos + ti.n_bytes]
+
+    def read_into(self, ti: TensorInfo, out, start: int = 0) -> int:
+        """Read tensor bytes [start, start + len(out)) into the writable buffer `out` with positional
+        reads (large sequential requests instead of page faults on the map), stopping at the tensor's
+        end; returns the number of bytes read."""
+        if not 0 <= start <= ti.n_bytes:
+            raise GGUFError("read outside the tensor")
+        dst = memoryview(out).cast("B")
+        n = min(dst.nbytes, ti.n_bytes - start)
+        pos = self._span(ti, start, n)
+        done = 0
+        while done < n:
+            got = os.preadv(self._fd, [dst[done:n]], pos + done)
+            if got <= 0:
+                raise GGUFError("unexpected end of file")
+            done += got
         return n
 
     def close(self) -> None:
-        try:
-            if self._mm is not None:
-                self._mm.close()
-        except BufferError:            # a view is still alive: the map closes with it
-            pass
-        finally:
-            self._fh.close()
+        mm, self._mm = self._mm, None
+        if mm is not None:
+            try:
+                mm.close()
+            except BufferError:        # a tensor still views the map; it is unmapped with the last view
+                pass
+        fd, self._fd = self._fd, -1
+        if fd >= 0:
+            os.close(fd)
 
     def __enter__(self):
         return self

@@ -1,143 +1,167 @@
 """
-Pinned host memory of exactly the requested size, mapped for the GPU: the reference's hostmem.py
-(ggufengine/hostmem.py:1-125) on HIP.  Weights that stay in RAM (MoE experts that do not fit, offloaded
-layers) are allocated with hipHostMalloc(portable | mapped) instead of torch's caching host allocator
-(which rounds every pinned block up to a power of two and keeps freed blocks).  On MI355X the GPU sees
-such a block at the same address (checked with hipHostGetDevicePointer; a different address is an
-error, no kernel is handed the pointer then), so the gathered mat-vec kernels read experts from RAM
-over PCIe through their address table (cudakern.mv `adressen`).
+Pinned host memory of exactly the requested size, mapped into the GPU's address space: the contract of
+the reference's ggufengine/hostmem.py (`empty`, `abbilden`, `abgebildet`, `flush`, `pending`,
+`ram_reicht`, `RAM_REST`), built on HIP for MI355X.
 
-A block is freed only in `flush()`, never by the garbage collector: freeing waits for the device and
-must neither disturb a graph capture nor pull the memory from under a copy still queued.
+Why not torch's pinned allocator: it rounds every block up to a power of two (300 MB -> 512 MB) and keeps
+freed blocks cached.  Weights that stay in RAM (MoE experts that do not fit in VRAM, offloaded layers)
+come from `hipHostMalloc(portable | mapped)` instead.  On MI355X the GPU sees such a block at its host
+address; `empty()` checks that with `hipHostGetDevicePointer` and refuses the block otherwise, so a
+kernel is never handed an address the GPU cannot use.  The gathered mat-vec kernels then read experts
+over PCIe through their address tables (cudakern.mv `adressen`).
+
+Lifetime: the block's memory is the buffer of a ctypes array; every CPU tensor and every GPU view made
+from it holds that array through torch's buffer reference.  When the last view dies, a finalizer puts the
+address on a retirement queue (no lock, no runtime call: finalizers run at arbitrary points).  Retired
+blocks are freed only by `flush()`, after a device synchronisation and never during a graph capture, so
+a copy or kernel still queued on the device never loses its memory.
 """
 from __future__ import annotations
 
+import bisect
+import collections
 import ctypes
 import os
 import threading
-from typing import Dict, List
+import types
+import weakref
 
-import numpy as np
 import torch
 
-_PORTABLE = 0x1      # hipHostMallocPortable: pinned for every device context
-_MAPPED = 0x2        # hipHostMallocMapped: kernels read it over PCIe
+RAM_REST = 8 << 30        # RAM that must stay free after pinning (else the caller keeps ordinary RAM)
 
-RAM_REST = 8 << 30              # RAM left free after pinning (else the caller keeps ordinary RAM)
-
-_pending: List[int] = []        # pointers of dead blocks, freed in flush()
-_ranges: Dict[int, int] = {}    # start -> end of the live blocks (the same addresses on the GPU)
-_lock = threading.Lock()
-_hip_lib = None
+_FLAG_PORTABLE = 0x1      # hipHostMallocPortable: pinned for every device
+_FLAG_MAPPED = 0x2        # hipHostMallocMapped: visible to kernels
 
 
-def _hip() -> ctypes.CDLL:
-    """The HIP runtime torch has loaded (the one libnmq.so binds to as well)."""
-    global _hip_lib
-    if _hip_lib is None:
-        path = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
-        L = ctypes.CDLL(path if os.path.exists(path) else "libamdhip64.so.7")
-        pp, p, sz, u = ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint
-        L.hipHostMalloc.argtypes, L.hipHostMalloc.restype = [pp, sz, u], ctypes.c_int
-        L.hipHostGetDevicePointer.argtypes, L.hipHostGetDevicePointer.restype = [pp, p, u], ctypes.c_int
-        L.hipHostFree.argtypes, L.hipHostFree.restype = [p], ctypes.c_int
-        _hip_lib = L
-    return _hip_lib
+class _Runtime:
+    """The three HIP host-memory calls, bound on first use from the runtime torch loaded."""
+
+    def __init__(self):
+        here = os.path.join(os.path.dirname(torch.__file__), "lib", "libamdhip64.so")
+        lib = ctypes.CDLL(here if os.path.exists(here) else "libamdhip64.so.7")
+        vpp = ctypes.POINTER(ctypes.c_void_p)
+        self.malloc = lib.hipHostMalloc
+        self.malloc.argtypes, self.malloc.restype = [vpp, ctypes.c_size_t, ctypes.c_uint], ctypes.c_int
+        self.device_pointer = lib.hipHostGetDevicePointer
+        self.device_pointer.argtypes = [vpp, ctypes.c_void_p, ctypes.c_uint]
+        self.device_pointer.restype = ctypes.c_int
+        self.free = lib.hipHostFree
+        self.free.argtypes, self.free.restype = [ctypes.c_void_p], ctypes.c_int
 
 
-class _Block:
-    """Owns one hipHostMalloc allocation; numpy (and through it every torch view) keeps it alive."""
+class PinnedHeap:
+    """Live pinned blocks (sorted start addresses for lookups) and the queue of retired ones."""
 
-    def __init__(self, ptr: int, n: int):
-        self.ptr = ptr
-        self.__array_interface__ = {"shape": (n,), "typestr": "|u1", "data": (ptr, False), "version": 3}
+    def __init__(self):
+        self._starts: list = []
+        self._end: dict = {}
+        self._retired: collections.deque = collections.deque()
+        self._lock = threading.Lock()
+        self._rt = None
 
-    def __del__(self):
-        try:
-            _pending.append(self.ptr)        # atomic under the GIL; no lock in a finaliser
-        except Exception:                    # interpreter shutdown: the process frees it
-            pass
+    def runtime(self) -> _Runtime:
+        if self._rt is None:
+            self._rt = _Runtime()
+        return self._rt
+
+    def allocate(self, n_bytes: int, device) -> torch.Tensor:
+        self.release()
+        if not ram_reicht(n_bytes):
+            raise RuntimeError(f"pinning {n_bytes} bytes would leave less than {RAM_REST >> 30} GB of RAM free")
+        torch.zeros(1, device=torch.device(device))        # makes the device's context current
+        rt = self.runtime()
+        size = max(1, int(n_bytes))
+        host = ctypes.c_void_p()
+        err = rt.malloc(ctypes.byref(host), size, _FLAG_PORTABLE | _FLAG_MAPPED)
+        if err or not host.value:
+            raise RuntimeError(f"hipHostMalloc({n_bytes}): HIP error {err}")
+        seen = ctypes.c_void_p()
+        err = rt.device_pointer(ctypes.byref(seen), host, 0)
+        if err or seen.value != host.value:
+            rt.free(host)
+            raise RuntimeError(f"the GPU does not see pinned RAM at its host address (error {err}, "
+                               f"{seen.value!r} against {host.value:#x})")
+        start = host.value
+        with self._lock:
+            bisect.insort(self._starts, start)
+            self._end[start] = start + size
+        buf = (ctypes.c_ubyte * int(n_bytes)).from_address(start) if n_bytes else (ctypes.c_ubyte * 1).from_address(start)
+        weakref.finalize(buf, self._retired.append, start)
+        t = torch.frombuffer(buf, dtype=torch.uint8)
+        return t[:0] if not n_bytes else t
+
+    def owns(self, addr: int) -> bool:
+        with self._lock:
+            i = bisect.bisect_right(self._starts, addr) - 1
+            return i >= 0 and addr < self._end[self._starts[i]]
+
+    def release(self) -> None:
+        if not self._retired or torch.cuda.is_current_stream_capturing():
+            return
+        torch.cuda.synchronize()
+        rt = self.runtime()
+        while True:
+            try:
+                start = self._retired.popleft()
+            except IndexError:
+                break
+            with self._lock:
+                i = bisect.bisect_left(self._starts, start)
+                if i < len(self._starts) and self._starts[i] == start:
+                    del self._starts[i]
+                self._end.pop(start, None)
+            rt.free(ctypes.c_void_p(start))
+
+    def waiting(self) -> int:
+        return len(self._retired)
+
+
+_heap = PinnedHeap()
 
 
 def ram_reicht(n_bytes: int) -> bool:
-    """Would RAM_REST stay free after pinning n_bytes?  Without psutil: yes."""
+    """True when RAM_REST would stay free after pinning n_bytes (True when psutil is missing)."""
     try:
         import psutil
-        return psutil.virtual_memory().available - int(n_bytes) >= RAM_REST
-    except Exception:
+    except ImportError:
         return True
+    return psutil.virtual_memory().available - int(n_bytes) >= RAM_REST
 
 
 def empty(n_bytes: int, device) -> torch.Tensor:
-    """uint8 CPU tensor of n_bytes in pinned RAM, mapped for the GPU at the same address.
-    RuntimeError if the runtime cannot pin that much, if less than RAM_REST would stay free, or if the
-    GPU would see the block at another address."""
-    flush()
-    if not ram_reicht(n_bytes):
-        raise RuntimeError(f"pinning {n_bytes} bytes would leave less than {RAM_REST >> 30} GB of RAM free")
-    device = torch.device(device)
-    torch.zeros(1, device=device)            # a current device context for the runtime calls
-    L = _hip()
-    n = max(1, int(n_bytes))
-    ptr = ctypes.c_void_p()
-    err = L.hipHostMalloc(ctypes.byref(ptr), n, _PORTABLE | _MAPPED)
-    if err or not ptr.value:
-        raise RuntimeError(f"hipHostMalloc({n_bytes}): HIP error {err}")
-    dptr = ctypes.c_void_p()
-    err = L.hipHostGetDevicePointer(ctypes.byref(dptr), ptr, 0)
-    if err or dptr.value != ptr.value:
-        L.hipHostFree(ptr)
-        raise RuntimeError(f"the GPU does not see pinned RAM at the host address (error {err}, "
-                           f"{dptr.value!r} vs {ptr.value:#x})")
-    with _lock:
-        _ranges[ptr.value] = ptr.value + n
-    return torch.from_numpy(np.asarray(_Block(ptr.value, int(n_bytes))))
-
-
-class _GpuView:
-    """__cuda_array_interface__ of a host block; torch keeps this object (and through it the block)
-    alive as long as the GPU tensor lives."""
-
-    def __init__(self, host: torch.Tensor):
-        self.host = host
-        self.__cuda_array_interface__ = {"shape": (host.numel(),), "typestr": "|u1", "strides": None,
-                                         "data": (host.data_ptr(), False), "version": 3}
+    """uint8 CPU tensor of exactly n_bytes in pinned RAM that the GPU sees at the same address.
+    RuntimeError when the runtime cannot pin that much, when less than RAM_REST would stay free, or
+    when the GPU would see the block elsewhere."""
+    return _heap.allocate(n_bytes, device)
 
 
 def abbilden(host: torch.Tensor, device) -> torch.Tensor:
-    """A block from `empty()` as a GPU tensor at the same address: kernels, copies and graphs read it
-    over PCIe, nothing is held in VRAM."""
+    """The GPU tensor at the address of a block from `empty()` (or a part of one): kernels, copies and
+    graphs read it over PCIe; nothing is held in VRAM.  The view keeps the block alive."""
     if not abgebildet(host):
-        raise ValueError("only blocks from hostmem.empty() can be mapped")
-    view = torch.as_tensor(_GpuView(host.view(-1)), device=torch.device(device))
-    if view.data_ptr() != host.data_ptr():
+        raise ValueError("only memory from hostmem.empty() can be mapped")
+    flat = host.reshape(-1)
+    holder = types.SimpleNamespace(host=flat, __cuda_array_interface__={
+        "shape": (flat.numel(),), "typestr": "|u1", "strides": None, "data": (flat.data_ptr(), False),
+        "version": 3})
+    gpu = torch.as_tensor(holder, device=torch.device(device))
+    if gpu.data_ptr() != flat.data_ptr():
         raise RuntimeError("no unified addressing: the GPU sees the block at another address")
-    return view
+    return gpu
 
 
 def abgebildet(t: torch.Tensor) -> bool:
-    """t lies in a live block from `empty()` (also as the GPU tensor from `abbilden`)."""
-    p = t.data_ptr()
-    with _lock:
-        return any(a <= p < e for a, e in _ranges.items())
+    """t starts inside a live block from `empty()` (as the CPU tensor or as its GPU view)."""
+    return _heap.owns(t.data_ptr())
 
 
 def flush() -> None:
-    """Free the blocks no tensor uses any more, once the device has finished all work."""
-    if not _pending or torch.cuda.is_current_stream_capturing():
-        return
-    torch.cuda.synchronize()
-    L = _hip()
-    while _pending:
-        try:
-            ptr = _pending.pop()
-        except IndexError:                   # emptied by another thread
-            break
-        with _lock:
-            _ranges.pop(ptr, None)
-        L.hipHostFree(ctypes.c_void_p(ptr))
+    """Free the retired blocks (no tensor uses them any more) once the device has finished its work;
+    nothing happens during a graph capture."""
+    _heap.release()
 
 
 def pending() -> int:
-    """Dead blocks waiting for `flush()`."""
-    return len(_pending)
+    """Retired blocks waiting for `flush()`."""
+    return _heap.waiting()

@@ -23,6 +23,23 @@ def pytest_collection_modifyitems(config, items):
     pass
 
 
+@pytest.fixture
+def tune():
+    """Launch-plan overrides for one test (nmq_set_tuning), restored to the defaults afterwards:
+    tune(MVM=2, MVT_MAX=1)."""
+    from ggufengine_amd import _native
+    touched = set()
+
+    def set_knobs(**knobs):
+        for name, value in knobs.items():
+            touched.add(name)
+            _native.set_tuning(name, value)
+
+    yield set_knobs
+    for name in touched:
+        _native.set_tuning(name, None)
+
+
 @pytest.fixture(scope="session")
 def oracle():
     import oracle as O

@@ -145,3 +145,32 @@ def test_python_api_without_gpu():
         mmvq.Eingang(n=33, device="cpu")
     assert qlinear.quantizable(12, 4096, 4096) and not qlinear.quantizable(16, 4096, 4096)
     assert not mmvq.schritt_moeglich("cpu", 32, 8, 128)
+
+
+def test_tuning_knobs_set_get_and_reset(L):
+    """Launch-plan overrides go through nmq_set_tuning only (no environment variable is read): a value
+    set is read back, NMQ_TUNE_DEFAULT restores the default, unknown names are refused."""
+    from ggufengine_amd import _native
+    assert _native.get_tuning("MVM") is None
+    with _native.tuning(MVM=2, NMQ_MVT_MAX=1):
+        assert _native.get_tuning("MVM") == 2 and _native.get_tuning("MVT_MAX") == 1
+        assert _native.get_tuning("NMQ_MVM") == 2
+    assert _native.get_tuning("MVM") is None and _native.get_tuning("MVT_MAX") is None
+    with pytest.raises(ValueError):
+        _native.set_tuning("NOT_A_KNOB", 1)
+    assert L.nmq_set_tuning(None, 1) == _native.NMQ_ERR_ARG
+    os.environ["NMQ_MVM"] = "0"
+    try:
+        assert _native.get_tuning("MVM") is None      # the environment changes nothing
+    finally:
+        del os.environ["NMQ_MVM"]
+
+
+def test_quantlinear_has_no_int4_planes_and_every_format_stays_packed():
+    """models/moe.py `_StapelTeil` stacks QuantLinear.mats for torch's int4 kernel: this library's
+    QuantLinear has none and says so; its expert tensors take the gathered path instead, because every
+    format is in cudakern.IMMER_GEPACKT (the reference loader's `packed_type`)."""
+    from ggufengine_amd import cudakern, qlinear
+    with pytest.raises(TypeError, match="aus_quantlinear"):
+        qlinear.QuantLinear.mats.fget(object())
+    assert cudakern.IMMER_GEPACKT == frozenset(cudakern.FORMATE)

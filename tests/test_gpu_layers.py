@@ -572,3 +572,119 @@ def test_expert_layer_with_experts_in_pinned_ram(nmq, L):
     lager.zaehlen(idx)
     lager.umsortieren()
     assert torch.equal(ram(x, idx, w), want)
+
+
+# ---- QuantLinear (the reference's "QLinear forward", qlinear.py:222-239) ------------------------------------
+
+@pytest.mark.parametrize("fmt", ["Q8_0", "Q4_0", "Q4_K", "Q6_K"])
+@pytest.mark.parametrize("M", [1, 8, 64, 300])
+def test_quant_linear_call(nmq, oracle, fmt, M):
+    """QuantLinear.__call__: x cast to bf16, the route for M rows (mat-vec kernels, matrix cores, or the
+    unpack to bf16 + GEMM at 300 rows), the result in bf16, the bias added in bf16.  Against dequantise +
+    matmul in fp64 on the bf16-rounded x, with the bias: the bf16 output rounding (2^-9 relative) bounds
+    the difference; tolerance 8e-3 of the row maximum."""
+    from ggufengine_amd import qlinear
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out, n_in = 320, 1024
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=201 + M)
+    rng = np.random.default_rng(202 + M)
+    x = rng.standard_normal((M, n_in)).astype(np.float32)
+    b = (rng.standard_normal(n_out) * 0.5).astype(np.float32)
+    say("QuantLinear", fmt, M)
+    ql = qlinear.build_quant_linear(dev(raw), TYPE_ID[fmt], n_out, n_in, bias=dev(b))
+    y = ql(dev(x).view(M, 1, n_in))
+    assert y.dtype == torch.bfloat16 and y.shape == (M, 1, n_out)
+    got = y.float().reshape(M, n_out).cpu().numpy()
+    xb = oracle.round_bf16(x)
+    ref = oracle.mv_deq(fmt, raw, n_out, n_in, xb) + oracle.round_bf16(b).astype(np.float64)
+    err = oracle.rel_err_rows(got, ref)
+    assert err.max() <= 8e-3, (fmt, M, ql.route(M), float(err.max()))
+    # before the bf16 cast: the kernels' fp32 result on the same bf16 x within the mat-vec bar
+    kind = ql.route(M)
+    assert kind == {1: "mmvq.mv" if fmt in ("Q4_K", "Q6_K") else "cudakern.mv"}.get(M, kind)
+    if kind != "unpack":
+        f32 = ql._layer.forward_raw(dev(xb), ql._layer.raw, torch.float32).cpu().numpy()
+        assert oracle.rel_err_rows(f32, ref - oracle.round_bf16(b)).max() <= 1e-3
+    assert ql.bf16_weight().shape == (n_out, n_in)
+
+
+def test_quant_linear_experts_as_packed_experts(nmq, oracle):
+    """QuantLinear experts cut back to back out of one tensor (the reference loader's way) become one
+    PackedExperts in place; the gathered kernel on them equals each expert's own QuantLinear call on the
+    same bf16 input."""
+    from ggufengine_amd import experts, qlinear
+    n_exp, n_out, n_in = 6, 128, 1024
+    raw = random_blocks("Q4_K", n_exp * n_out * n_in // 256, seed=211)
+    whole = dev(raw)
+    per = raw.size // n_exp
+    qls = [qlinear.build_quant_linear(whole[e * per:(e + 1) * per], 12, n_out, n_in) for e in range(n_exp)]
+    pe = experts.PackedExperts.aus_quantlinear(qls)
+    assert pe.raw.data_ptr() == whole.data_ptr() and pe.n_exp == n_exp
+    x = dev(np.random.default_rng(212).standard_normal(n_in).astype(np.float32))
+    ids = torch.tensor([5, 0, 3, 3], device="cuda")
+    say("QuantLinear experts")
+    y = pe.matvec(ids, x)
+    for j, e in enumerate(ids.tolist()):
+        one = qls[e]._layer.forward_raw(x.to(torch.bfloat16).view(1, -1), qls[e]._layer.raw, torch.float32)
+        assert torch.allclose(y[j], one[0], rtol=1e-6, atol=1e-6 * float(one.abs().max())), (j, e)
+    # copied together when the experts are separate allocations
+    pe2 = experts.PackedExperts.aus_quantlinear([qlinear.build_quant_linear(whole[e * per:(e + 1) * per].clone(), 12,
+                                                                             n_out, n_in) for e in range(n_exp)])
+    assert pe2.raw.data_ptr() != whole.data_ptr() and torch.equal(pe2.matvec(ids, x), y)
+    # unpacked experts and one expert as a layer
+    w = pe.weights(ids[:2])
+    assert w.shape == (2, n_out, n_in)
+    ref = oracle.round_bf16(oracle.dequant("Q4_K", raw.reshape(n_exp, -1)[5])).reshape(n_out, n_in)
+    assert np.array_equal(w[0].float().cpu().numpy(), ref)
+    one5 = pe[5](x.view(1, -1)).float().view(-1)
+    assert torch.allclose(one5, y[0].to(torch.bfloat16).float(), rtol=1e-2, atol=1e-2 * float(y[0].abs().max()))
+
+
+def test_band_slots_aligned_for_any_largest_source(nmq):
+    """The largest source is a 5-row TQ2_0 matrix of 1320 bytes (not a multiple of 16); Q4_K matrices after
+    it land in slots 1..3, which start at 256-byte multiples, and compute the VRAM results bit for bit."""
+    from ggufengine_amd import band, hostmem, packed
+    specs = [("TQ2_0", 35, 5, 1024), ("Q4_K", 12, 8, 256), ("Q4_K", 12, 4, 512), ("Q4_K", 12, 2, 1024),
+             ("Q6_K", 14, 3, 512), ("Q4_K", 12, 6, 256)]
+    fl = band.Fliessband("cuda")
+    vram, ram, xs = [], [], []
+    rng = np.random.default_rng(221)
+    say("band alignment")
+    for i, (fmt, tid, n_out, n_in) in enumerate(specs):
+        raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=222 + i)
+        vram.append(packed.PackedLinear(dev(raw), tid, n_out, n_in, dtype=torch.float32))
+        host = hostmem.empty(raw.size, "cuda")
+        host.numpy()[:] = raw
+        lay = packed.PackedLinear(hostmem.abbilden(host, "cuda"), tid, n_out, n_in, dtype=torch.float32)
+        lay.band, lay.nr = fl, fl.anmelden(host)
+        ram.append(lay)
+        xs.append(dev(rng.standard_normal((1, n_in)).astype(np.float32)))
+    for _ in range(2):
+        for i, (a, b, x) in enumerate(zip(ram, vram, xs)):
+            assert torch.equal(a(x), b(x)), i
+    torch.cuda.synchronize()
+    assert all(s.data.data_ptr() % 256 == 0 for s in fl._slots)
+
+
+def test_band_refuses_a_pass_split_across_a_capture(nmq):
+    """A pass begun by eager calls cannot continue inside a graph capture (its queued copies are not part
+    of the capture): holen raises before touching any stream, and the pass then finishes eagerly."""
+    from ggufengine_amd import band
+    fl = band.Fliessband("cuda")
+    src = [torch.full((512,), i, dtype=torch.uint8, device="cuda") for i in range(3)]
+    for t in src:
+        fl.anmelden(t)
+    say("band split pass")
+    fl.holen(0)
+    fl.fertig(0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with pytest.raises(RuntimeError, match="whole passes"):
+        with torch.cuda.graph(g, stream=s):
+            fl.holen(1)
+    torch.cuda.current_stream().wait_stream(s)
+    got = fl.holen(1)
+    assert bool((got == 1).all())
+    fl.fertig(1)
+    torch.cuda.synchronize()

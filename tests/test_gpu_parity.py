@@ -132,12 +132,12 @@ def test_mv_one_token(nmq, oracle, fmt, shape):
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("n_in", [10240, 14336, 16384])
 @pytest.mark.parametrize("pipelined", [False, True])
-def test_mv_one_token_long_rows(nmq, oracle, monkeypatch, fmt, n_in, pipelined):
+def test_mv_one_token_long_rows(nmq, oracle, tune, fmt, n_in, pipelined):
     """One token on rows of 160..256 units of 64 values (the Llama down projection has 224): one row
     per wave, and (with fewer resident waves than rows) the variant that cycles two row buffers."""
     n_out = 300
     if pipelined:
-        monkeypatch.setenv("NMQ_MVL_WPC", "1")   # 1 wave per CU: fewer waves than rows
+        tune(MVL_WPC=1)   # 1 wave per CU: fewer waves than rows
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=81)
     x = np.random.default_rng(82).standard_normal((1, n_in)).astype(np.float32)
     x[0, 5] = 25.0
@@ -176,7 +176,7 @@ def test_mv_tokens(nmq, oracle, fmt, nc):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("split", [(1, 16), (1, 8), (1, 4), (1, 2), (1, 1), (2, 4), (4, 4), (3, 2)])
-def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
+def test_mv_tokens_matrix_core_splits(nmq, oracle, tune, fmt, split):
     """2..16 tokens on the matrix cores (one or two groups of 8 per launch) with every (tiles per
     workgroup, K slices) split: slices of 16, 8, 4, 2 and 1 blocks (held whole or cycled through
     buffers), a partial last tile, and workgroups whose last tiles lie past the matrix."""
@@ -184,10 +184,10 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, monkeypatch, fmt, split):
     n_out, n_in = 200, 4096
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=61 + ks)
     from ggufengine_amd.gguf_types import TYPE_ID
-    monkeypatch.setenv("NMQ_MVM", "2")   # the matrix-core path from 2 tokens on, whatever the format
-    monkeypatch.setenv("NMQ_MVT_MAX", "1")   # (not the few-token Q4_K kernel)
-    monkeypatch.setenv("NMQ_MVM_TPW", str(tpw))
-    monkeypatch.setenv("NMQ_MVM_KS", str(ks))
+    tune(MVM=2)   # the matrix-core path from 2 tokens on, whatever the format
+    tune(MVT_MAX=1)   # (not the few-token Q4_K kernel)
+    tune(MVM_TPW=tpw)
+    tune(MVM_KS=ks)
     for nc in (2, 7, 8, 12, 16):
         x = np.random.default_rng(62 + nc).standard_normal((nc, n_in)).astype(np.float32)
         x[:, 7] = 30.0
@@ -294,15 +294,15 @@ def _mm_run(nmq, fmt, raw_d, x_np, n_out, n_in):
 
 @pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K"])
 @pytest.mark.parametrize("tiles,groups", [("1", "0"), ("2", "0"), ("4", "0"), ("4", "1"), ("2", "3")])
-def test_mm_tokens(nmq, oracle, monkeypatch, fmt, tiles, groups):
+def test_mm_tokens(nmq, oracle, tune, fmt, tiles, groups):
     """1..112 tokens (1..4 groups of 16 per launch, launches of 64) with 1, 2 and 4 row tiles per
     workgroup and all, one or three token groups per workgroup (three: the last workgroup of 4 groups
     repeats the last one, unstored): against the dequantised weights times the same two-stage input
     (only the order of the fp32 sums differs) and times the exact input.  Shapes: partial tiles and
     workgroups whose tiles lie past the matrix (200, 37 rows), one block per row (256: three of the
     four K quarters empty), an odd number of blocks per quarter (1280)."""
-    monkeypatch.setenv("NMQ_MMH_T", tiles)
-    monkeypatch.setenv("NMQ_MMH_G", groups)
+    tune(MMH_T=int(tiles))
+    tune(MMH_G=int(groups))
     for n_out, n_in in ((200, 1280), (37, 256), (64, 4096)):
         raw = random_blocks(fmt, n_out * n_in // 256, seed=103)
         raw_d = dev(raw)
@@ -343,14 +343,14 @@ def test_mm_mirror_112_tokens(nmq, oracle, fmt):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_mv_tokens_dot4_kernel(nmq, oracle, monkeypatch, fmt):
+def test_mv_tokens_dot4_kernel(nmq, oracle, tune, fmt):
     """2..8 tokens on the dot4 kernel (the path below each format's matrix-core threshold), forced for
     every token count."""
     n_out, n_in = 200, 4096
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=71)
     from ggufengine_amd.gguf_types import TYPE_ID
-    monkeypatch.setenv("NMQ_MVM", "0")
-    monkeypatch.setenv("NMQ_MVT_MAX", "1")
+    tune(MVM=0)
+    tune(MVT_MAX=1)
     for nc in (2, 5, 8, 13):                   # 13: launches of 8 and 5
         x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
         e = quant_dev(dev(x))
@@ -627,12 +627,12 @@ def test_experts_values(nmq, oracle, two):
 
 @pytest.mark.parametrize("nc", [2, 3, 4])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 4096), (1000, 2048), (513, 1024), (37, 256)])
-def test_few_tokens_equal_one_by_one(nmq, oracle, monkeypatch, shape, nc):
+def test_few_tokens_equal_one_by_one(nmq, oracle, tune, shape, nc):
     """2..4 tokens of Q4_K (speculative verification) in one launch of the few-token kernel (enabled up to
     4 tokens here): each token's output equals the one-token launch on that token bit for bit (the same
     decode and combine expression, one weight read for all), and the oracle within tolerance.  Covers
     64, 32 and 16 lanes per row and row counts that leave the last steps partial."""
-    monkeypatch.setenv("NMQ_MVT_MAX", "4")
+    tune(MVT_MAX=4)
     n_out, n_in = shape
     raw = random_blocks("Q4_K", n_out * n_in // 256, seed=131 + n_in)
     x = np.random.default_rng(132 + n_out + nc).standard_normal((nc, n_in)).astype(np.float32)

@@ -243,6 +243,26 @@ int nmq_mv_experts2(int fmt, const void* w_a, const void* w_b, const int64_t* id
 int nmq_moe_combine(const float* y, const float* w, int L, int k, int E, float* out, void* stream);
 
 /*
+ * The down projection of an expert layer fused with the weighted combine:
+ *   out[t][r] = sum_{j<k} wts[t*k + j] * (W_{ids[t*k + j]}[r,:] . x_(t*k + j)),   t < L, r < n_out,
+ * each slot's product exactly as nmq_mv_experts_x forms it (x_group = 1: slot t*k + j reads input row
+ * t*k + j of x, mode x_mode, x2 for NMQ_X_SILU_MUL_BF16), the slots summed in order j = 0..k-1 with fp32
+ * fused multiply-adds (bit for bit nmq_moe_combine on those products).  ids: L*k int64 on the device;
+ * wts: L*k fp32; out: fp32 L x n_out; w, per_expert as in nmq_mv_experts; n_in <= NMQ_X_MAX_N_IN.
+ * Rows of up to 4096 values and k <= 16: one launch, each workgroup computing a block of rows for all k
+ * slots of one token and summing them in LDS (no workspace: nmq_moe_down_work_bytes reports 0).  Other
+ * shapes: the gathered launch writes the L*k slot results into `work` (nmq_moe_down_work_bytes bytes,
+ * 256-byte aligned) and a second launch sums them; calls that overlap in time must not share it.
+ * NMQ_ERR_SHAPE when work_bytes is too small.
+ * Replaces the down call of Experten.__call__ plus its weighted combine (models/moe.py:264-277, 319-320;
+ * cudakern.mv with ids, cudakern.py:756-774).
+ */
+int nmq_moe_down_work_bytes(int fmt, int L, int k, int n_out, int n_in, int64_t* bytes);
+int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                 int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, void* work,
+                 int64_t work_bytes, void* stream);
+
+/*
  * Diagnostic: the int32 sums the mat-vec kernels form, per 16 weights, for one token:
  *   s1[r][g] = sum_{j<16} w_int(r, 16g+j) * xq[16g+j],  s2 likewise with xq2,
  * where w_int is the format's integer weight (Q4_K nibble, Q6_K q-32, Q8_0 qs, TQ2_0 code-1,

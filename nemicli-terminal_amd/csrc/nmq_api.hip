@@ -452,6 +452,27 @@ extern template int launch_mv<NMQ_IQ2_XXS>(MvParams, int, int, hipStream_t);
 extern template int launch_mv<NMQ_TQ2_0>(MvParams, int, int, hipStream_t);
 
 template <int F>
+int launch_moe_down(MvParams p, Combine c, int L, hipStream_t stream);
+extern template int launch_moe_down<NMQ_Q4_0>(MvParams, Combine, int, hipStream_t);
+extern template int launch_moe_down<NMQ_Q8_0>(MvParams, Combine, int, hipStream_t);
+extern template int launch_moe_down<NMQ_Q4_K>(MvParams, Combine, int, hipStream_t);
+extern template int launch_moe_down<NMQ_Q6_K>(MvParams, Combine, int, hipStream_t);
+extern template int launch_moe_down<NMQ_IQ2_XXS>(MvParams, Combine, int, hipStream_t);
+extern template int launch_moe_down<NMQ_TQ2_0>(MvParams, Combine, int, hipStream_t);
+
+static int launch_moe_down_any(int fmt, const MvParams& p, const Combine& c, int L, hipStream_t s) {
+    switch (fmt) {
+        case NMQ_Q4_0: return launch_moe_down<NMQ_Q4_0>(p, c, L, s);
+        case NMQ_Q8_0: return launch_moe_down<NMQ_Q8_0>(p, c, L, s);
+        case NMQ_Q4_K: return launch_moe_down<NMQ_Q4_K>(p, c, L, s);
+        case NMQ_Q6_K: return launch_moe_down<NMQ_Q6_K>(p, c, L, s);
+        case NMQ_IQ2_XXS: return launch_moe_down<NMQ_IQ2_XXS>(p, c, L, s);
+        case NMQ_TQ2_0: return launch_moe_down<NMQ_TQ2_0>(p, c, L, s);
+        default: return NMQ_ERR_FORMAT;
+    }
+}
+
+template <int F>
 int launch_mmh(MmhParams p, hipStream_t stream);
 extern template int launch_mmh<NMQ_Q4_K>(MmhParams, hipStream_t);
 extern template int launch_mmh<NMQ_Q6_K>(MmhParams, hipStream_t);
@@ -895,6 +916,73 @@ int nmq_mv_experts_x(int fmt, const void* w_a, const void* w_b, const int64_t* i
     p.x_group = x_group;
     p.n_ids = n_ids;
     return launch_any(fmt, p, 1, w_b ? 2 * n_ids : n_ids, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+// ---- expert down projection fused with the weighted combine ---------------------------------------------
+// One launch of moe_down_kernel where it takes the shape (no workspace).  Otherwise the slots go through the
+// plain gathered launch into a workspace of L*k x n_out fp32 and moe_combine_kernel sums them.
+static int64_t moe_work_bytes(int L, int k, int n_out, int n_in) {
+    return plan_moe_down(n_out, n_in, L, k, device_info()).ok ? 0 : (int64_t)L * k * n_out * 4;
+}
+
+static int moe_check(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                     int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in) {
+    int e = check_w(fmt, w, out, n_out, n_in);
+    if (e) return e;
+    if ((e = check_values(x, x_mode, x2, n_in))) return e;
+    if (!ids || !wts || !aligned(wts, 4) || L < 1 || k < 1 || (int64_t)L * k > 65535) return NMQ_ERR_ARG;
+    return check_experts(fmt, w, L * k, per_expert, 1, n_out, n_in);
+}
+
+// The checked call on a workspace of at least moe_work_bytes(...) bytes at `work`.
+static int moe_launch(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                      int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, float* work,
+                      hipStream_t s) {
+    MvParams p{};
+    p.w = (const u8*)w;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xv = x;
+    p.xv2 = x2;
+    p.x_mode = x_mode;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    p.x_group = 1;
+    p.n_ids = L * k;
+    const Combine c{wts, out, k, 0};
+    const int e = launch_moe_down_any(fmt, p, c, L, s);
+    if (e != NMQ_ERR_SHAPE) return e;
+    p.y = work;
+    const int e2 = launch_any(fmt, p, 1, L * k, s);
+    if (e2) return e2;
+    const int64_t blocks = ((int64_t)L * n_out + 255) / 256;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, wts, L, k,
+                       n_out, out);
+    return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int nmq_moe_down_work_bytes(int fmt, int L, int k, int n_out, int n_in, int64_t* bytes) {
+    int bv, bb;
+    if (!bytes || L < 1 || k < 1 || n_out < 1 || n_in < 1) return NMQ_ERR_ARG;
+    if (nmq_format_info(fmt, &bv, &bb)) return NMQ_ERR_FORMAT;
+    *bytes = moe_work_bytes(L, k, n_out, n_in);
+    return NMQ_OK;
+}
+
+int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                 int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, void* work,
+                 int64_t work_bytes, void* stream) {
+    const int e = moe_check(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in);
+    if (e) return e;
+    const int64_t need = moe_work_bytes(L, k, n_out, n_in);
+    if (need > 0 && (!work || !aligned(work, 256))) return NMQ_ERR_ARG;
+    if (work_bytes < need) return NMQ_ERR_SHAPE;
+    return moe_launch(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in, (float*)work,
+                      (hipStream_t)stream);
 }
 
 int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2, int n_out,

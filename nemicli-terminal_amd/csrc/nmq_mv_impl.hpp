@@ -851,11 +851,10 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
     }
 }
 
+// The team's RW row sums of one step (every lane of the team holds them after the team reduction).
 template <int F, int T, int RW, int NITM>
-__device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, const XSlice (&x)[NITM], int r0,
-                                            const RowMap& rm, int lt, int U, const u64* tab,
-                                            const LaneConst& lc) {
-    float acc[RW];
+__device__ __forceinline__ void mv1_dots(const Mv1Step<F, T, RW, NITM>& st, const XSlice (&x)[NITM], int lt, int U,
+                                         const u64* tab, const LaneConst& lc, float (&acc)[RW]) {
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) {
         acc[rr] = 0.f;
@@ -868,6 +867,14 @@ __device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, c
     }
 #pragma unroll
     for (int rr = 0; rr < RW; ++rr) acc[rr] = team_sum<T>(acc[rr]);
+}
+
+template <int F, int T, int RW, int NITM>
+__device__ __forceinline__ void mv1_compute(const Mv1Step<F, T, RW, NITM>& st, const XSlice (&x)[NITM], int r0,
+                                            const RowMap& rm, int lt, int U, const u64* tab,
+                                            const LaneConst& lc) {
+    float acc[RW];
+    mv1_dots<F, T, RW, NITM>(st, x, lt, U, tab, lc, acc);
     if (lt == 0) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
@@ -1193,8 +1200,7 @@ __global__ __launch_bounds__(PIPE ? 512 : 1024) void mvl_kernel(MvParams p) {
 // arrives.  Used when the matrix fits in the resident waves of one launch (then every
 // weight byte of the matvec is in flight at once, the shape a streaming read needs at this size).
 template <int F, int T, int RW, bool EXT>
-__global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
-    args_early<EXT>(p);
+__device__ __forceinline__ void mvc_body(const MvParams& p) {
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
@@ -1214,6 +1220,69 @@ __global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
     const LaneConst lc = lane_const<F, T, 1>(lt);
     mv1_compute<F, T, RW, 1>(a, x, r0, rm, lt, U, tab, lc);
+}
+
+template <int F, int T, int RW, bool EXT>
+__global__ __launch_bounds__(RW >= 8 ? 512 : 1024) void mvc_kernel(MvParams p) {
+    args_early<EXT>(p);
+    mvc_body<F, T, RW, EXT>(p);
+}
+
+// The down projection of an expert layer with the weighted combine in the same workgroup (MoE, one
+// token per blockIdx.y): workgroup (x, t) computes rows [x*R, (x+1)*R) of all k slots of token t -- slot j
+// (instance t*k + j, expert ids[t*k + j]) on waves j*WS .. j*WS + WS - 1, each wave one chunk of P*RW rows
+// like the chunk kernel -- keeps the k*R sums in LDS and then forms
+//   out[t][r] = sum_j w[t*k + j] * y_j[r]   (fp32 fused multiply-adds in slot order),
+// bit for bit the plain gathered launch followed by nmq_moe_combine, with no global intermediate and no
+// ordering between workgroups.  The k slots' inputs are consecutive rows of values (x_group = 1), staged
+// as one row of k*n_in values: slot j's unit u is unit j*U + u of that row.
+struct Combine {
+    const float* w;  // L*k slot weights
+    float* out;      // L x n_out
+    int k;           // slots per token
+    int ws;          // waves per slot
+};
+
+template <int F, int T, int RW>
+__global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
+    args_early<true>(p);
+    using FM = Fmt<F>;
+    constexpr int P = 64 / T;
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int team = lane / T, lt = lane % T;
+    const int t = blockIdx.y, j = wave / c.ws, wj = wave % c.ws;
+    const int R = c.ws * P * RW;  // rows per workgroup
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, t * c.k + j, xrow);
+    const RowMap rm = row_map<false>(p, wbase, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    const int lr = (wj * P + team) * RW;  // the team's first row in the block
+    const int r0 = blockIdx.x * R + lr;
+    Mv1Step<F, T, RW, 1> a;
+    MvParams q = p;  // the token's k input rows as one row of k*n_in values
+    q.n_in = p.n_in * c.k;
+    stage1_around<F, true, 1>(lds, tab, q, t, [&] { a.load(rm, r0, lt, U, r0); });
+    XSlice x[1];
+    read_slice<FM::STRIDED>(lds, p.ktp, j * U + min(lt, U - 1), x[0]);
+    const LaneConst lc = lane_const<F, T, 1>(lt);
+    float acc[RW];
+    mv1_dots<F, T, RW, 1>(a, x, lt, U, tab, lc, acc);
+    float* res = (float*)(lds + p.ktp * 9 / 4);  // k x R sums
+    if (lt == 0) {
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) res[j * R + lr + rr] = acc[rr];
+    }
+    lds_barrier();
+    const float* wt = c.w + (int64_t)t * c.k;
+    for (int r = (int)threadIdx.x; r < R; r += p.nt) {
+        const int row = blockIdx.x * R + r;
+        if (row >= p.n_out) break;
+        float sum = 0.f;
+        for (int s = 0; s < c.k; ++s) sum = fmaf(wt[s], res[s * R + r], sum);
+        gpw<float>(c.out)[(int64_t)t * p.n_out + row] = sum;
+    }
 }
 
 // ---- host side --------------------------------------------------------------------------------
@@ -1702,6 +1771,65 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     MvKernel k = pick_kernel<F>(nc, s.rw, s.T);
     p.nt = 64 * s.W;
     hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x, (unsigned)n_mats), dim3(p.nt), s.lds, stream, p);
+    return (int)hipGetLastError();
+}
+
+
+// ---- the expert down projection with the weighted combine (moe_down_kernel) --------------------------
+typedef void (*MoeDownKernel)(MvParams, Combine);
+
+template <int F, int T>
+inline MoeDownKernel pick_moe_down_rw(int rw) {
+    switch (rw) {
+        case 1: return moe_down_kernel<F, T, 1>;
+        case 2: return moe_down_kernel<F, T, 2>;
+        default: return moe_down_kernel<F, T, 4>;
+    }
+}
+
+struct MoeDownShape {
+    bool ok;
+    int T, rw, ws, W, R, grid_x, ktp;
+    size_t lds;
+};
+
+// Waves per slot WS (W = k*WS <= 16) and rows per team RW: about 256 workgroups per launch when the rows
+// allow it (R = WS*P*RW rows per workgroup), one unit per lane (rows of up to T*64 values).
+inline MoeDownShape plan_moe_down(int n_out, int n_in, int L, int k, const DeviceInfo& di) {
+    MoeDownShape s{};
+    const int U = (n_in + 63) / 64;
+    s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    if (U > s.T || k < 1 || k > 16) return s;
+    const int P = 64 / s.T;
+    s.ws = 16 / k >= 2 ? 2 : 1;
+    if (s.ws > 16 / k) return s;
+    s.W = k * s.ws;
+    int64_t R = ((int64_t)n_out * L + di.cus - 1) / di.cus;  // rows per workgroup for ~one per CU
+    s.rw = 1;
+    while (s.rw < 4 && R > (int64_t)s.ws * P * s.rw) s.rw *= 2;
+    s.R = s.ws * P * s.rw;
+    s.grid_x = (n_out + s.R - 1) / s.R;
+    s.ktp = (n_in * k + 127) / 128 * 128;
+    s.lds = (size_t)s.ktp * 9 / 4 + (size_t)k * s.R * 4;
+    s.ok = s.lds <= (size_t)di.lds_max && n_in % 64 == 0;
+    return s;
+}
+
+// One launch (value input, x_group = 1).  NMQ_ERR_SHAPE when the kernel does not take the shape.
+template <int F>
+int launch_moe_down(MvParams p, Combine c, int L, hipStream_t stream) {
+    using FM = Fmt<F>;
+    const DeviceInfo di = device_info();
+    const MoeDownShape sh = plan_moe_down(p.n_out, p.n_in, L, c.k, di);
+    if (!sh.ok) return NMQ_ERR_SHAPE;
+    p.nblk = p.n_in / FM::BV;
+    p.row_bytes = (int64_t)p.nblk * FM::BB;
+    p.ktp = sh.ktp;
+    p.nt = 64 * sh.W;
+    c.ws = sh.ws;
+    const MoeDownKernel kern = sh.T == 16 ? pick_moe_down_rw<F, 16>(sh.rw)
+                             : sh.T == 32 ? pick_moe_down_rw<F, 32>(sh.rw) : pick_moe_down_rw<F, 64>(sh.rw);
+    hipLaunchKernelGGL(kern, dim3((unsigned)sh.grid_x, (unsigned)L), dim3(p.nt), sh.lds, stream, p, c);
     return (int)hipGetLastError();
 }
 

@@ -11,15 +11,17 @@ The reference's expert path around the gathered mat-vec, on this library's kerne
     pinned RAM (`hostmem`), read by the kernels through per-part address tables.
   - `Experten` (models/moe.py:252-321): y = sum_j w_j * down_j(silu(gate_j(x)) * up_j(x)).  Every
     (token, slot) pair on its own, in (token, slot) order (the reference's one-token and graph paths),
-    the weighted sum per token in slot order.  Three launches: gate and up in one gathered launch
+    the weighted sum per token in slot order.  Two launches: gate and up in one gathered launch
     reading each token's input through its k slots (x_group = k), the input rounded to bf16 (as
     cudakern.mv does) and quantised inside the launch; down on each slot's own activation
-    bf16(silu(gate) * up), also formed and quantised inside its launch; the combine.
+    bf16(silu(gate) * up), also formed and quantised inside its launch, whose last workgroup per
+    (token, row block) adds the slots' results in slot order (nmq_moe_down).
 
 Every expert product runs on libnmq's HIP kernels; without the library the constructor raises.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Optional, Tuple
 
 import torch
@@ -270,6 +272,7 @@ class Experten:
             raise GGUFError("Experten: gate/up/down shapes do not fit together")
         self.gate, self.up, self.down = gate, up, down
         self.n_exp = gate.n_exp
+        self._work: dict = {}
 
     @staticmethod
     def _gu(h_gate: torch.Tensor, h_up: torch.Tensor) -> torch.Tensor:
@@ -281,9 +284,9 @@ class Experten:
 
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights.
-        Three launches: gate and up together on every (token, slot), each token's input rounded to bf16
+        Two launches: gate and up together on every (token, slot), each token's input rounded to bf16
         and quantised in the launch; down on every slot, its input bf16(silu(gate) * up) formed and
-        quantised in the launch; the weighted combine.  (Rows longer than WERTE_BIS values, or a gate
+        quantised in the launch, with the weighted combine in the same launch (nmq_moe_down).  (Rows longer than WERTE_BIS values, or a gate
         and up of different layout: the input quantisations as launches of their own.)"""
         L_, E = x.shape
         k = idx.shape[1]
@@ -300,14 +303,26 @@ class Experten:
         (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
         _starten("mv_experts2", L.nmq_mv_experts_x, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
                  flat.data_ptr(), n, per, xc.data_ptr(), _native.X_F32_BF16, None, k, gu.data_ptr(), FF, E, st)
-        y = torch.empty(n, E, dtype=torch.float32, device=dev)
         wd, perd = self.down._quelle(dev)
-        _starten("mv_experts", L.nmq_mv_experts_x, TYPE_ID[self.down.name], wd.data_ptr(), None, flat.data_ptr(), n,
-                 perd, gu.data_ptr(), _native.X_SILU_MUL_BF16, gu[n:].data_ptr(), 1, y.data_ptr(), E, FF, st)
         out = torch.empty(L_, E, dtype=torch.float32, device=dev)
         wf = w.to(dev, torch.float32).contiguous()
-        _starten("moe_combine", L.nmq_moe_combine, y.data_ptr(), wf.data_ptr(), L_, k, E, out.data_ptr(), st)
+        work = self._arbeitsplatz(L_, k, dev)
+        _starten("moe_down", L.nmq_moe_down, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), L_, k, perd,
+                 gu.data_ptr(), _native.X_SILU_MUL_BF16, gu[n:].data_ptr(), wf.data_ptr(), out.data_ptr(), E, FF,
+                 work.data_ptr(), work.numel(), st)
         return out
+
+    def _arbeitsplatz(self, L_: int, k: int, dev) -> torch.Tensor:
+        """The fused down launch's workspace for L_ tokens of k slots: kept per layer and device, grown
+        when needed, zeroed once when made (the launch leaves its counters zero)."""
+        need = ctypes.c_int64(0)
+        _native.check(_native.lib().nmq_moe_down_work_bytes(TYPE_ID[self.down.name], L_, k, self.down.n_out,
+                                                            self.down.n_in, ctypes.byref(need)))
+        have = self._work.get(dev)
+        if have is None or have.numel() < need.value:
+            have = torch.zeros(max(need.value, 256), dtype=torch.uint8, device=dev)
+            self._work[dev] = have
+        return have
 
     def _aufgeteilt(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """The same layer with the inputs quantised by launches of their own (five launches when gate

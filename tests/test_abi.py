@@ -174,3 +174,31 @@ def test_quantlinear_has_no_int4_planes_and_every_format_stays_packed():
     with pytest.raises(TypeError, match="aus_quantlinear"):
         qlinear.QuantLinear.mats.fget(object())
     assert cudakern.IMMER_GEPACKT == frozenset(cudakern.FORMATE)
+
+
+def test_moe_down_checks_without_launching(L):
+    """nmq_moe_down sizes its workspace and refuses bad arguments before anything is launched."""
+    from ggufengine_amd import _native
+    need = ctypes.c_int64(0)
+    assert L.nmq_moe_down_work_bytes(14, 4, 8, 2048, 768, ctypes.byref(need)) == 0
+    assert need.value == 0                                       # one launch, the sums in LDS
+    assert L.nmq_moe_down_work_bytes(14, 4, 8, 2048, 5120, ctypes.byref(need)) == 0
+    assert need.value == 4 * 8 * 2048 * 4                        # rows too long: slots through a workspace
+    assert L.nmq_moe_down_work_bytes(14, 0, 8, 2048, 768, ctypes.byref(need)) == _native.NMQ_ERR_ARG
+    assert L.nmq_moe_down_work_bytes(13, 1, 8, 2048, 768, ctypes.byref(need)) == _native.NMQ_ERR_FORMAT
+    buf = ctypes.create_string_buffer(1 << 16)
+    a = (ctypes.addressof(buf) + 255) // 256 * 256
+    args = dict(fmt=14, w=a, ids=a, L=1, k=8, per=2048 * 3 * 210, x=a, mode=_native.X_SILU_MUL_BF16, x2=a, wts=a,
+                out=a, n_out=2048, n_in=768, work=a, work_bytes=1 << 14)
+
+    def call(**kw):
+        v = {**args, **kw}
+        return L.nmq_moe_down(v["fmt"], v["w"], v["ids"], v["L"], v["k"], v["per"], v["x"], v["mode"], v["x2"],
+                              v["wts"], v["out"], v["n_out"], v["n_in"], v["work"], v["work_bytes"], None)
+    assert call(ids=None) == _native.NMQ_ERR_ARG
+    assert call(wts=None) == _native.NMQ_ERR_ARG
+    assert call(k=0) == _native.NMQ_ERR_ARG
+    long = dict(n_in=5120, per=2048 * 20 * 210)
+    assert call(work=a + 16, **long) == _native.NMQ_ERR_ARG       # not 256-byte aligned
+    assert call(work_bytes=16, **long) == _native.NMQ_ERR_SHAPE   # too small
+    assert call(n_in=700) == _native.NMQ_ERR_SHAPE                # not whole blocks

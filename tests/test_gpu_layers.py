@@ -688,3 +688,101 @@ def test_band_refuses_a_pass_split_across_a_capture(nmq):
     assert bool((got == 1).all())
     fl.fertig(1)
     torch.cuda.synchronize()
+
+
+# ---- down projection fused with the weighted combine (nmq_moe_down) ----------------------------------------
+
+def _moe_down_case(nmq, fmt, L, k, E, FF, n_exp, seed):
+    from ggufengine_amd.gguf_types import TYPE_ID
+    raw = random_blocks(fmt, n_exp * E * FF // BV[fmt], seed=seed)
+    w = dev(raw)
+    rng = np.random.default_rng(seed + 1)
+    gu = dev(rng.standard_normal((2 * L * k, FF)).astype(np.float32))
+    return TYPE_ID[fmt], w, raw.size // n_exp, gu, rng
+
+
+def _moe_down_unfused(nmq, t, w, per, ids, gu, wts, L, k, E, FF):
+    n = L * k
+    y = torch.empty(n, E, dtype=torch.float32, device="cuda")
+    out = torch.empty(L, E, dtype=torch.float32, device="cuda")
+    Lb = nmq.lib()
+    nmq.check(Lb.nmq_mv_experts_x(t, w.data_ptr(), None, ids.data_ptr(), n, per, gu.data_ptr(), nmq.X_SILU_MUL_BF16,
+                                  gu[n:].data_ptr(), 1, y.data_ptr(), E, FF, nmq.stream_ptr()))
+    nmq.check(Lb.nmq_moe_combine(y.data_ptr(), wts.data_ptr(), L, k, E, out.data_ptr(), nmq.stream_ptr()))
+    return out
+
+
+def _moe_down_work(nmq, t, L, k, E, FF):
+    import ctypes
+    need = ctypes.c_int64(0)
+    nmq.check(nmq.lib().nmq_moe_down_work_bytes(t, L, k, E, FF, ctypes.byref(need)))
+    return torch.zeros(max(need.value, 0), dtype=torch.uint8, device="cuda")
+
+
+def _moe_down_fused(nmq, t, w, per, ids, gu, wts, L, k, E, FF, work, out=None):
+    n = L * k
+    out = torch.empty(L, E, dtype=torch.float32, device="cuda") if out is None else out
+    nmq.check(nmq.lib().nmq_moe_down(t, w.data_ptr(), ids.data_ptr(), L, k, per, gu.data_ptr(), nmq.X_SILU_MUL_BF16,
+                                     gu[n:].data_ptr(), wts.data_ptr(), out.data_ptr(), E, FF, work.data_ptr(),
+                                     work.numel(), nmq.stream_ptr()))
+    return out
+
+
+@pytest.mark.parametrize("fmt,L,k,E,FF", [("Q6_K", 1, 8, 2048, 768), ("Q6_K", 4, 8, 2048, 768),
+                                          ("Q4_K", 3, 2, 1024, 512), ("Q8_0", 2, 8, 640, 1024),
+                                          ("IQ2_XXS", 5, 4, 512, 1024), ("TQ2_0", 1, 8, 2048, 768),
+                                          ("Q6_K", 2, 8, 256, 5120)])
+def test_moe_down_fused_equals_unfused(nmq, fmt, L, k, E, FF):
+    """nmq_moe_down (each workgroup computes a row block of all k slots of one token and sums them in LDS;
+    n_in 5120: the plain gathered launch into the workspace + the combine launch) equals nmq_mv_experts_x +
+    nmq_moe_combine bit for bit, over three calls in a row with new routings."""
+    n_exp = 16
+    t, w, per, gu, rng = _moe_down_case(nmq, fmt, L, k, E, FF, n_exp, 231 + L * k)
+    work = _moe_down_work(nmq, t, L, k, E, FF)
+    say("moe_down", fmt, L, k, E, FF, work.numel())
+    for call in range(3):
+        ids = torch.from_numpy(rng.integers(0, n_exp, L * k)).cuda()
+        wts = dev(rng.random((L, k)).astype(np.float32))
+        want = _moe_down_unfused(nmq, t, w, per, ids, gu, wts, L, k, E, FF)
+        got = _moe_down_fused(nmq, t, w, per, ids, gu, wts, L, k, E, FF, work)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (fmt, L, k, call)
+    assert (work.numel() == 0) == (FF <= 4096)      # a workspace only where the one-launch kernel does not fit
+
+
+def test_moe_down_refuses_a_small_workspace(nmq):
+    t, w, per, gu, rng = _moe_down_case(nmq, "Q6_K", 2, 8, 512, 5120, 4, 241)
+    work = _moe_down_work(nmq, t, 2, 8, 512, 5120)
+    assert work.numel() == 2 * 8 * 512 * 4
+    ids = torch.zeros(16, dtype=torch.int64, device="cuda")
+    wts = torch.ones(2, 8, device="cuda")
+    with pytest.raises(ValueError):
+        _moe_down_fused(nmq, t, w, per, ids, gu, wts, 2, 8, 512, 5120, work[:work.numel() - 256])
+
+
+def test_moe_down_graph_replays(nmq):
+    """One nmq_moe_down call captured in a HIP graph and replayed with new ids and weights written into its
+    input tensors between replays (eager work in between): every replay equals the unfused launches."""
+    L, k, E, FF, n_exp = 2, 8, 2048, 768, 16
+    t, w, per, gu, rng = _moe_down_case(nmq, "Q6_K", L, k, E, FF, n_exp, 251)
+    work = _moe_down_work(nmq, t, L, k, E, FF)
+    ids = torch.from_numpy(rng.integers(0, n_exp, L * k)).cuda()
+    wts = dev(rng.random((L, k)).astype(np.float32))
+    out = torch.empty(L, E, device="cuda")
+    say("moe_down graph")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _moe_down_fused(nmq, t, w, per, ids, gu, wts, L, k, E, FF, work, out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _moe_down_fused(nmq, t, w, per, ids, gu, wts, L, k, E, FF, work, out)
+    for rep in range(4):
+        ids.copy_(torch.from_numpy(rng.integers(0, n_exp, L * k)))
+        wts.copy_(torch.from_numpy(rng.random((L, k)).astype(np.float32)))
+        g.replay()
+        torch.cuda.synchronize()
+        want = _moe_down_unfused(nmq, t, w, per, ids, gu, wts, L, k, E, FF)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep

@@ -263,6 +263,19 @@ int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64
                  int64_t work_bytes, void* stream);
 
 /*
+ * nmq_moe_down without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid allocation); no counterpart in the reference.
+ * The two-launch form keeps its slot results in a device array inside the library, one per GPU, of
+ * NMQ_MOE_SCRATCH_BYTES bytes (held until the process ends): shapes whose L*k x n_out fp32 results do not
+ * fit are refused with NMQ_ERR_SHAPE.  It allocates nothing.  Calls that overlap in time on one GPU share
+ * that array and race; nothing needs clearing between calls (a call reads only what it wrote).
+ * Otherwise identical to nmq_moe_down (results bit for bit equal).
+ */
+#define NMQ_MOE_SCRATCH_BYTES (8 << 20)
+int nmq_moe_down_static(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                        int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, void* stream);
+
+/*
  * Diagnostic: the int32 sums the mat-vec kernels form, per 16 weights, for one token:
  *   s1[r][g] = sum_{j<16} w_int(r, 16g+j) * xq[16g+j],  s2 likewise with xq2,
  * where w_int is the format's integer weight (Q4_K nibble, Q6_K q-32, Q8_0 qs, TQ2_0 code-1,

@@ -936,6 +936,30 @@ static int moe_check(int fmt, const void* w, const int64_t* ids, int L, int k, i
     return check_experts(fmt, w, L * k, per_expert, 1, n_out, n_in);
 }
 
+// Device memory of nmq_moe_down_static: the slot results of the two-launch form (one copy per GPU the
+// library runs on, held until the process ends).  Host code never passes `scratch` itself to a kernel (on
+// the host it names a stand-in, not the device address): the address comes from hipGetSymbolAddress, taken
+// once per device with that device current.  Every element a call reads was written by the same call, so
+// nothing needs clearing between calls.
+static __device__ __align__(256) unsigned char scratch[NMQ_MOE_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_at[64];
+
+static int scratch_address(void** at) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NMQ_ERR_DEVICE;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_at[dev]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress((void**)&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!ptr) return NMQ_ERR_DEVICE;
+        g_scratch_at[dev] = ptr;
+    }
+    *at = g_scratch_at[dev];
+    return NMQ_OK;
+}
+
 // The checked call on a workspace of at least moe_work_bytes(...) bytes at `work`.
 static int moe_launch(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
                       int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, float* work,
@@ -981,6 +1005,18 @@ int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64
     const int64_t need = moe_work_bytes(L, k, n_out, n_in);
     if (need > 0 && (!work || !aligned(work, 256))) return NMQ_ERR_ARG;
     if (work_bytes < need) return NMQ_ERR_SHAPE;
+    return moe_launch(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in, (float*)work,
+                      (hipStream_t)stream);
+}
+
+int nmq_moe_down_static(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
+                        int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, void* stream) {
+    int e = moe_check(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in);
+    if (e) return e;
+    const int64_t need = moe_work_bytes(L, k, n_out, n_in);
+    if (need > NMQ_MOE_SCRATCH_BYTES) return NMQ_ERR_SHAPE;
+    void* work = nullptr;
+    if ((e = scratch_address(&work))) return e;
     return moe_launch(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in, (float*)work,
                       (hipStream_t)stream);
 }

@@ -359,7 +359,9 @@ def read_ceiling(n_bytes, steps, warmup, shapes=None):
 def run_ceiling(steps, warmup):
     """Pure-read reference points: the headline's weight bytes (33 MB) and sizes up to 1 GB, every launch
     shape; one record per size."""
-    for n in (weight_bytes("Q4_K", 14336, 4096), weight_bytes("Q4_K", 4096, 4096), 128 << 20, 512 << 20, 1 << 30):
+    sizes = (weight_bytes("TQ2_0", 4096, 4096), weight_bytes("Q4_K", 4096, 4096), weight_bytes("TQ2_0", 12288, 4096),
+             weight_bytes("Q4_K", 14336, 4096), weight_bytes("Q6_K", 4096, 14336), 128 << 20, 512 << 20, 1 << 30)
+    for n in sizes:
         best, table = read_ceiling(n, steps, warmup)
         print(json.dumps({"config": "ceiling", "case": f"pure read of {n} bytes in one launch", "best": best,
                           "shapes": table}), flush=True)

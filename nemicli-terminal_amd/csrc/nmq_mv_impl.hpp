@@ -824,8 +824,58 @@ struct HandStep<NMQ_Q4_K, NITM> : Q4kStepAsm<NITM> {
 constexpr bool hand_format(int f) { return f == NMQ_Q4_K || f == NMQ_TQ2_0 || f == NMQ_IQ2_XXS; }
 
 // Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
+// TQ2_0 on the raw 2-bit codes c (value c - 1).  Run r of a unit (16 values, one xd) holds its codes at bit
+// offset 2r of the unit's four code dwords, so q & (3 << 2r) is the run's codes times 4^r as bytes; run 3
+// is shifted right by 2 first, (q >> 2) & 0x30303030 = 16 c, so that every byte stays <= 32 and the signed
+// dot4 is exact.  With the run's scale f (1, 4, 16, 16), S1' = sum f c xq and S2' = sum f c xq2:
+//   f (254 sum (c - 1) xq + sum (c - 1) xq2) = 254 S1' + S2' - f (254 X1 + X2),
+// X1, X2 the run's input sums.  The xq2 chain starts at -f (254 X1 + X2) (a lane constant, formed once from
+// the lane's input slice), one 24-bit multiply-add joins the stages, an exact arithmetic shift removes f, and
+// the run adds (that integer, |.| < 2^20: exact in fp32) times xd / 254; the block scale d multiplies the
+// unit's sum.  About half the VALU instructions of unpacking every code to a signed byte.
+struct Tq2Lane {
+    int k[4];    // xq2 chain start per run
+    float e[4];  // xd / 254 per run
+};
+
+__device__ __forceinline__ Tq2Lane tq2_lane(const XSlice& x) {
+    Tq2Lane c;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        int x1 = 0, x2 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x1 = dot4(0x01010101u, x.q[4 * r + k], x1);
+            x2 = dot4(0x01010101u, x.q2[4 * r + k], x2);
+        }
+        const int f = r == 0 ? 1 : (r == 1 ? 4 : 16);
+        c.k[r] = -f * (254 * x1 + x2);
+        c.e[r] = x.d[r] * FEIN;
+    }
+    return c;
+}
+
+__device__ __forceinline__ float tq2_dot1(const Fmt<NMQ_TQ2_0>::Raw& raw, const XSlice& x, const Tq2Lane& c) {
+    const u32 q[4] = {raw.q.x, raw.q.y, raw.q.z, raw.q.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        int a = 0, b = c.k[r];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32 w = r == 3 ? ((q[k] >> 2) & 0x30303030u) : (q[k] & (0x03030303u << (2 * r)));
+            a = dot4(w, x.q[4 * r + k], a);
+            b = dot4(w, x.q2[4 * r + k], b);
+        }
+        const int t = (__mul24(a, 254) + b) >> (r == 0 ? 0 : (r == 1 ? 2 : 4));  // |a| <= 16*32*127: 24-bit
+        acc = fmaf((float)t, c.e[r], acc);
+    }
+    return acc * h2f(raw.d);
+}
+
 struct LaneConst {
     Q4kLane q4k[4];  // Q4_K: the unit's scale/min selection
+    Tq2Lane tq2[4];  // TQ2_0 (kernels that hold their input slices): the unit's input constants
 };
 
 template <int F, int T, int NITM>
@@ -836,7 +886,19 @@ __device__ __forceinline__ LaneConst lane_const(int lt) {
     return c;
 }
 
-template <int F>
+// Kernels that keep the lane's input slices in registers for all their rows: also the per-slice constants.
+template <int F, int T, int NITM>
+__device__ __forceinline__ LaneConst lane_const(int lt, const XSlice (&x)[NITM]) {
+    LaneConst c = lane_const<F, T, NITM>(lt);
+    if constexpr (F == NMQ_TQ2_0) {
+#pragma unroll
+        for (int it = 0; it < NITM && it < 4; ++it) c.tq2[it] = tq2_lane(x[it]);
+    }
+    return c;
+}
+
+// HELD: the slice constants of lane_const(lt, x) are present (TQ2_0 then takes the raw-code path).
+template <int F, bool HELD = false>
 __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int u, const u64* tab, const XSlice& x,
                                            const LaneConst& lc, int it) {
     using FM = Fmt<F>;
@@ -844,6 +906,8 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
         return q4k_dot1(raw, x, lc.q4k[it]);
     } else if constexpr (F == NMQ_Q6_K) {
         return q6k_dot1(raw, x, u);
+    } else if constexpr (F == NMQ_TQ2_0 && HELD) {
+        return tq2_dot1(raw, x, lc.tq2[it]);
     } else {
         WUnit wu;
         FM::decode(raw, u, tab, wu);
@@ -861,7 +925,7 @@ __device__ __forceinline__ void mv1_dots(const Mv1Step<F, T, RW, NITM>& st, cons
 #pragma unroll
         for (int it = 0; it < NITM; ++it) {
             const int u = lt + it * T;
-            const float v = unit_dot1<F>(st.raw[rr][it], min(u, U - 1), tab, x[it], lc, it);
+            const float v = unit_dot1<F, true>(st.raw[rr][it], min(u, U - 1), tab, x[it], lc, it);
             acc[rr] += u < U ? v : 0.f;
         }
     }
@@ -937,7 +1001,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
         if (u < U) read_slice<FM::STRIDED>(lds, p.ktp, u, x[it]);
     }
 
-    const LaneConst lc = lane_const<F, T, NITM>(lt);
+    const LaneConst lc = lane_const<F, T, NITM>(lt, x);
     if constexpr (HR) {
         float res = 0.f;
         int k = 0, first = base;
@@ -955,7 +1019,7 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
 #pragma unroll
                 for (int it = 0; it < NITM; ++it) {
                     const int u = lt + it * T;
-                    const float v = unit_dot1<F>(hb[i].raw[it], min(u, U - 1), tab, x[it], lc, it);
+                    const float v = unit_dot1<F, true>(hb[i].raw[it], min(u, U - 1), tab, x[it], lc, it);
                     acc += u < U ? v : 0.f;
                 }
                 acc = team_sum<T>(acc);
@@ -1218,7 +1282,7 @@ __device__ __forceinline__ void mvc_body(const MvParams& p) {
     stage1_around<F, EXT, 1>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
-    const LaneConst lc = lane_const<F, T, 1>(lt);
+    const LaneConst lc = lane_const<F, T, 1>(lt, x);
     mv1_compute<F, T, RW, 1>(a, x, r0, rm, lt, U, tab, lc);
 }
 
@@ -1266,7 +1330,7 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
     stage1_around<F, true, 1>(lds, tab, q, t, [&] { a.load(rm, r0, lt, U, r0); });
     XSlice x[1];
     read_slice<FM::STRIDED>(lds, p.ktp, j * U + min(lt, U - 1), x[0]);
-    const LaneConst lc = lane_const<F, T, 1>(lt);
+    const LaneConst lc = lane_const<F, T, 1>(lt, x);
     float acc[RW];
     mv1_dots<F, T, RW, 1>(a, x, lt, U, tab, lc, acc);
     float* res = (float*)(lds + p.ktp * 9 / 4);  // k x R sums
@@ -1400,19 +1464,20 @@ inline MvKernel pick_mv1_ext(int nitm) {
 // hr: the Q4_K variant with hand-issued weight reads and register-held results (one row per team,
 // 3 buffers)
 template <int F, int T, bool EXT, int HR>
-inline MvKernel pick_mv1_hr(int nitm) {
+inline MvKernel pick_mv1_hr(int nitm, int nbuf) {
     if constexpr (!hand_format(F)) return nullptr;
-    else return nitm == 1 ? mv1_kernel<F, T, 1, 1, 3, EXT, HR> : mv1_kernel<F, T, 1, 2, 3, EXT, HR>;
+    else if (nitm == 1) return nbuf == 4 ? mv1_kernel<F, T, 1, 1, 4, EXT, HR> : mv1_kernel<F, T, 1, 1, 3, EXT, HR>;
+    else return mv1_kernel<F, T, 1, 2, 3, EXT, HR>;
 }
 template <int F, bool EXT, int HR>
-inline MvKernel pick_mv1_hr_t(int T, int nitm) {
-    return T == 16 ? pick_mv1_hr<F, 16, EXT, HR>(nitm)
-                   : (T == 32 ? pick_mv1_hr<F, 32, EXT, HR>(nitm) : pick_mv1_hr<F, 64, EXT, HR>(nitm));
+inline MvKernel pick_mv1_hr_t(int T, int nitm, int nbuf) {
+    return T == 16 ? pick_mv1_hr<F, 16, EXT, HR>(nitm, nbuf)
+                   : (T == 32 ? pick_mv1_hr<F, 32, EXT, HR>(nitm, nbuf) : pick_mv1_hr<F, 64, EXT, HR>(nitm, nbuf));
 }
 template <int F>
 inline MvKernel pick_mv1(int T, int rw, int nitm, int nbuf, bool ext, int hr = 0) {
-    if (hr == 2) return pick_mv1_hr_t<F, true, 2>(T, nitm);
-    if (hr == 1) return ext ? pick_mv1_hr_t<F, true, 1>(T, nitm) : pick_mv1_hr_t<F, false, 1>(T, nitm);
+    if (hr == 2) return pick_mv1_hr_t<F, true, 2>(T, nitm, nbuf);
+    if (hr == 1) return ext ? pick_mv1_hr_t<F, true, 1>(T, nitm, nbuf) : pick_mv1_hr_t<F, false, 1>(T, nitm, nbuf);
     if (ext) return T == 16 ? pick_mv1_ext<F, 16>(nitm) : (T == 32 ? pick_mv1_ext<F, 32>(nitm) : pick_mv1_ext<F, 64>(nitm));
     switch (T) {
         case 16: return pick_mv1_rw<F, 16>(rw, nitm, nbuf);
@@ -1432,7 +1497,7 @@ struct Mv1Shape {
     size_t lds;
 };
 
-inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) {
+inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di, bool values = false) {
     Mv1Shape s{};
     if (!tune(TUNE_MV1, 1)) return s;
     const int U = (n_in + 63) / 64;
@@ -1445,13 +1510,16 @@ inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     s.nbuf = tune(TUNE_MV1_NBUF, 3) == 4 && s.nitm * s.rw <= 2 ? 4 : 3;
     const int P = 64 / s.T;
     const int64_t steps = ((int64_t)n_out + P * s.rw - 1) / (P * s.rw);  // per instance
-    // waves per CU: 16 for one matrix; 8 for gathered experts (many small matrices: fewer, longer-lived
-    // waves amortise the input staging; measured on MI355X, MoE layer at one token 21.3 -> 18.6 us)
-    const int wpc = tune(TUNE_MV1_WPC, n_mats > 1 ? 8 : 16);
+    // 8 resident waves per CU in 4-wave workgroups (two per CU), 8-wave workgroups with value input (the
+    // hand-issued staging of 4096 fp32 values needs 512 threads).  Measured on MI355X against 16 waves per CU
+    // in 8-wave workgroups: Q4_K 14336x4096 8.37 -> 7.43 us, TQ2_0 12288x4096 6.21 -> 5.82, Q6_K 14336x4096
+    // 13.37 -> 11.60, Q8_0 14336x4096 16.25 -> 14.02, gate|up in one launch 13.39 -> 13.10; more step
+    // buffers per wave, or 4 to 6 waves per CU, were not faster overall.
+    const int wpc = tune(TUNE_MV1_WPC, 8);
     int64_t waves = (int64_t)wpc * di.cus / n_mats;
     if (waves < 1) waves = 1;
     if (waves > steps) waves = steps;
-    int wmax = tune(TUNE_MV1_W, 8);
+    int wmax = tune(TUNE_MV1_W, values ? 8 : 4);
     wmax = wmax < 1 ? 1 : (wmax > 8 ? 8 : wmax);  // launch bound: 512 threads
     s.W = (int)(waves < wmax ? waves : wmax);
     s.grid_x = (int)((waves + s.W - 1) / s.W);
@@ -1732,14 +1800,15 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         }
     }
     if (nc == 1 && mode != 0) {
-        const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di);
+        const Mv1Shape s1 = plan_mv1(p.n_out, p.n_in, n_mats, di, p.xv != nullptr);
         if (s1.ok) {
             p.ktp = s1.ktp;
             // Q4_K, TQ2_0, IQ2_XXS (with at least 256 threads: the grid table) with the two-stage input
             // staged in one round, or fp32 values in at most two: hand-issued reads (NMQ_MV1_HR=0 for the
             // compiler-scheduled loop)
             int hr = 0;
-            if (hand_format(F) && s1.rw == 1 && s1.nbuf == 3 && s1.nitm <= 2 && (F != NMQ_IQ2_XXS || s1.W >= 4) &&
+            if (hand_format(F) && s1.rw == 1 && (s1.nbuf == 3 || s1.nitm == 1) && s1.nitm <= 2 &&
+                (F != NMQ_IQ2_XXS || s1.W >= 4) &&
                 tune(TUNE_MV1_HR, 1) != 0) {
                 if (p.xv == nullptr) hr = s1.ktp / 16 <= 64 * s1.W ? 1 : 0;
                 else if (p.x_mode == NMQ_X_F32 || p.x_mode == NMQ_X_F32_BF16) hr = s1.ktp / 4 <= 2 * 64 * s1.W ? 2 : 0;

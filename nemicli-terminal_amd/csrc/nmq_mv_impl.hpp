@@ -1510,12 +1510,13 @@ inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di, 
     s.nbuf = tune(TUNE_MV1_NBUF, 3) == 4 && s.nitm * s.rw <= 2 ? 4 : 3;
     const int P = 64 / s.T;
     const int64_t steps = ((int64_t)n_out + P * s.rw - 1) / (P * s.rw);  // per instance
-    // 8 resident waves per CU in 4-wave workgroups (two per CU), 8-wave workgroups with value input (the
-    // hand-issued staging of 4096 fp32 values needs 512 threads).  Measured on MI355X against 16 waves per CU
-    // in 8-wave workgroups: Q4_K 14336x4096 8.37 -> 7.43 us, TQ2_0 12288x4096 6.21 -> 5.82, Q6_K 14336x4096
-    // 13.37 -> 11.60, Q8_0 14336x4096 16.25 -> 14.02, gate|up in one launch 13.39 -> 13.10; more step
-    // buffers per wave, or 4 to 6 waves per CU, were not faster overall.
-    const int wpc = tune(TUNE_MV1_WPC, 8);
+    // Two-stage input: 8 resident waves per CU in 4-wave workgroups (two per CU).  Measured on MI355X against
+    // 16 waves per CU in 8-wave workgroups: Q4_K 14336x4096 8.37 -> 7.43 us, TQ2_0 12288x4096 6.21 -> 5.82,
+    // Q6_K 14336x4096 13.37 -> 11.60, Q8_0 14336x4096 16.25 -> 14.02, gate|up in one launch 13.39 -> 13.10;
+    // more step buffers per wave, or 4 to 6 waves per CU, were not faster overall.  Value input: 16 waves per
+    // CU in 8-wave workgroups (the hand-issued staging of 4096 fp32 values needs 512 threads; at 8 waves per
+    // CU the gate|up launch of the Llama-3-8B layer was faster alone but the layer 1.4 us slower).
+    const int wpc = tune(TUNE_MV1_WPC, values ? 16 : 8);
     int64_t waves = (int64_t)wpc * di.cus / n_mats;
     if (waves < 1) waves = 1;
     if (waves > steps) waves = steps;
@@ -1562,6 +1563,105 @@ inline MvlShape plan_mvl(int n_out, int n_in, int n_mats, const DeviceInfo& di) 
     return s;
 }
 
+// ---- one token, long rows split along K over the waves of a workgroup ------------------------------------
+// The input slice of unit u straight from global memory, in the register layout read_slice forms from LDS
+// (contiguous formats: values 64u .. 64u+63; strided formats: the 16-value runs 128h + 32k + 16j of block b).
+template <bool STRIDED>
+__device__ __forceinline__ void load_slice(const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int u,
+                                           XSlice& x) {
+    if (!STRIDED) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 a = *gp<u32x4>(xq + 64 * u + 16 * k);
+            const u32x4 b = *gp<u32x4>(xq2 + 64 * u + 16 * k);
+            x.q[4 * k] = a.x; x.q[4 * k + 1] = a.y; x.q[4 * k + 2] = a.z; x.q[4 * k + 3] = a.w;
+            x.q2[4 * k] = b.x; x.q2[4 * k + 1] = b.y; x.q2[4 * k + 2] = b.z; x.q2[4 * k + 3] = b.w;
+        }
+        const u32x2 dd = *gp<u32x2>(xd + 2 * u);
+        const u32x2 ss = *gp<u32x2>(xs + 2 * u);
+        x.d[0] = __uint_as_float(dd.x); x.d[1] = __uint_as_float(dd.y); x.d[2] = 0.f; x.d[3] = 0.f;
+        x.s[0] = __uint_as_float(ss.x); x.s[1] = __uint_as_float(ss.y);
+    } else {
+        const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+        const int v0 = 256 * b + 128 * h + 16 * j;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const u32x4 a = *gp<u32x4>(xq + v0 + 32 * k);
+            const u32x4 c = *gp<u32x4>(xq2 + v0 + 32 * k);
+            x.q[4 * k] = a.x; x.q[4 * k + 1] = a.y; x.q[4 * k + 2] = a.z; x.q[4 * k + 3] = a.w;
+            x.q2[4 * k] = c.x; x.q2[4 * k + 1] = c.y; x.q2[4 * k + 2] = c.z; x.q2[4 * k + 3] = c.w;
+        }
+        const u32x4 dd = *gp<u32x4>(xd + 8 * b + 4 * h);
+        x.d[0] = __uint_as_float(dd.x); x.d[1] = __uint_as_float(dd.y);
+        x.d[2] = __uint_as_float(dd.z); x.d[3] = __uint_as_float(dd.w);
+        x.s[0] = x.s[1] = 0.f;
+    }
+}
+
+// Rows of 65..256 units (one token, two-stage input): a workgroup of KS = ceil(U / 64) waves walks the rows
+// blockIdx.x, blockIdx.x + G, ... (G = gridDim.x); wave w takes units 64w .. 64w+63 of every row, one per lane,
+// with that unit's input slice read straight from global memory into registers once (no LDS staging) and the
+// weight reads of the next NBUF - 1 rows in flight.  Each step's wave sum (team_sum over the 64 lanes) is kept
+// in register lane k for the wave's k-th row; every 64 rows and at the end the KS partial sums of each row
+// meet in LDS and are added in slice order starting from zero, ((0 + p_0) + p_1) + ..., which is how the
+// few-token long-row kernel forms each token's sum.
+template <int F, int KS, int NBUF>
+__global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
+    args_early<false>(p);
+    using FM = Fmt<F>;
+    static_assert(F != NMQ_IQ2_XXS, "the grid table is staged by the LDS kernels only");
+    __shared__ float part[KS][64];
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const RowMap rm = row_map<false>(p, p.w, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    const int u = 64 * w + lane, uc = min(u, U - 1);
+    const int G = gridDim.x;
+    XSlice x[1];
+    load_slice<FM::STRIDED>(p.xq, p.xq2, p.xd, p.xs, uc, x[0]);
+    Mv1Step<F, 64, 1, 1> buf[NBUF];
+    int r = blockIdx.x;
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i) buf[i].load(rm, r + i * G, u, U, r);
+    const LaneConst lc = lane_const<F, 64, 1>(u);
+    const u64* tab = nullptr;
+    float res = 0.f;
+    int k = 0, first = r;
+    for (;;) {
+#pragma unroll
+        for (int i = 0; i < NBUF; ++i) {
+            const bool more = r < p.n_out;  // workgroup-uniform
+            if (more) {
+                buf[(i + NBUF - 1) % NBUF].load(rm, r + (NBUF - 1) * G, u, U, r);
+                const float v = unit_dot1<F>(buf[i].raw[0][0], uc, tab, x[0], lc, 0);
+                const float ws = team_sum<64>(u < U ? v : 0.f);
+                res = lane == k ? ws : res;
+                ++k;
+                r += G;
+            }
+            if (k == 64 || (!more && k > 0)) {  // flush a batch of rows
+                part[w][lane] = res;
+                lds_barrier();
+                if (threadIdx.x < (unsigned)k) {
+                    float sum = 0.f;
+#pragma unroll
+                    for (int q = 0; q < KS; ++q) sum += part[q][threadIdx.x];
+                    *gpw<float>(rm.out(first + (int)threadIdx.x * G)) = sum;
+                }
+                lds_barrier();
+                k = 0;
+                first = r;
+            }
+            if (!more) return;
+        }
+    }
+}
+
+template <int F>
+inline MvKernel pick_mvk(int ks) {
+    if constexpr (F == NMQ_IQ2_XXS) return nullptr;
+    else return ks == 2 ? mvk_kernel<F, 2, 3> : (ks == 3 ? mvk_kernel<F, 3, 3> : mvk_kernel<F, 4, 3>);
+}
+
 // ---- 2..4 tokens, long rows (Q6_K: the layer's down projection) ---------------------------------------
 // The long-row kernel for NC tokens: one row per wave in 16-wave workgroups (one per CU with the NC
 // staged inputs, 32 KB each for 14336 values), all of the row's weights requested at once, every token's
@@ -1597,6 +1697,8 @@ __global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
     float acc[NC];
 #pragma unroll
     for (int t = 0; t < NC; ++t) acc[t] = 0.f;
+    // each 64-unit slice's sum over the wave first, then the slices in order from zero: the order of the
+    // one-token K-split kernel (mvk_kernel), so every token's output equals the one-token launch
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const int u = lane + it * 64;
@@ -1604,12 +1706,10 @@ __global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
 #pragma unroll
         for (int t = 0; t < NC; ++t) {
             const float v = q6k_dot1_lds(a.raw[0][it], lds + t * tok, p.ktp, uc);
-            acc[t] += u < U ? v : 0.f;
+            acc[t] += team_sum<64>(u < U ? v : 0.f);
         }
         __builtin_amdgcn_sched_barrier(0);  // one unit's input slices live at a time
     }
-#pragma unroll
-    for (int t = 0; t < NC; ++t) acc[t] = team_sum<64>(acc[t]);
     if (lane == 0) {
 #pragma unroll
         for (int t = 0; t < NC; ++t) gpw<float>(p.y)[(int64_t)t * p.n_out + row] = acc[t];
@@ -1786,6 +1886,21 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             MvKernel k = pick_mvc<F>(sc.T, sc.rw, ext);
             p.nt = 64 * sc.W;
             hipLaunchKernelGGL(k, dim3((unsigned)sc.grid_x, (unsigned)n_mats), dim3(p.nt), sc.lds, stream, p);
+            return (int)hipGetLastError();
+        }
+    }
+    if constexpr (F != NMQ_IQ2_XXS) {
+        // one token over rows of 129..256 units from the two-stage input: the K-split kernel (the long-row
+        // kernel below stays for value input, segments, experts and IQ2_XXS)
+        const int U = (p.n_in + 63) / 64;
+        if (nc == 1 && U > 128 && U <= 256 && p.ids == nullptr && p.xv == nullptr && p.n_seg == 0 &&
+            tune(TUNE_MVK, 1) != 0) {
+            const int ks = (U + 63) / 64;
+            int64_t g = (int64_t)tune(TUNE_MVK_WPC, 8) * di.cus / ks;
+            if (g < 1) g = 1;
+            if (g > p.n_out) g = p.n_out;
+            p.nt = 64 * ks;
+            hipLaunchKernelGGL(pick_mvk<F>(ks), dim3((unsigned)g), dim3(p.nt), 0, stream, p);
             return (int)hipGetLastError();
         }
     }

@@ -130,18 +130,22 @@ def test_mv_one_token(nmq, oracle, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("n_in", [10240, 14336, 16384])
-@pytest.mark.parametrize("pipelined", [False, True])
-def test_mv_one_token_long_rows(nmq, oracle, tune, fmt, n_in, pipelined):
-    """One token on rows of 160..256 units of 64 values (the Llama down projection has 224): one row
-    per wave, and (with fewer resident waves than rows) the variant that cycles two row buffers."""
+@pytest.mark.parametrize("n_in", [8448, 10240, 14336, 16384])
+@pytest.mark.parametrize("kernel", ["ksplit", "longrow", "longrow_pipelined"])
+def test_mv_one_token_long_rows(nmq, oracle, tune, fmt, n_in, kernel):
+    """One token on rows of 132..256 units of 64 values (the Llama down projection has 224): the K-split
+    kernel (3 or 4 waves per row, input slices from global memory; IQ2_XXS always takes the long-row
+    kernel), and the long-row kernel with one row per wave and (with fewer resident waves than rows) the
+    variant that cycles two row buffers."""
     n_out = 300
-    if pipelined:
+    if kernel != "ksplit":
+        tune(MVK=0)
+    if kernel == "longrow_pipelined":
         tune(MVL_WPC=1)   # 1 wave per CU: fewer waves than rows
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=81)
     x = np.random.default_rng(82).standard_normal((1, n_in)).astype(np.float32)
     x[0, 5] = 25.0
-    say("mv long rows", fmt, n_in, pipelined)
+    say("mv long rows", fmt, n_in, kernel)
     e = quant_dev(dev(x))
     y = torch.full((1, n_out), float("nan"), device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID

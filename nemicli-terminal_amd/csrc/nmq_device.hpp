@@ -353,31 +353,71 @@ struct Fmt<NMQ_Q6_K> {
     }
 };
 
-// Q6_K unit (one token): decode and reduce one 16-value group at a time (the same sums and fp32
-// operations, in the same order, as decode() + unit_dot(), with a quarter of the decoded registers).
-__device__ __forceinline__ float q6k_dot1(const Fmt<NMQ_Q6_K>::Raw& r, const XSlice& x, int u) {
+// Q6_K unit (one token) on the raw 6-bit codes c (0..63, signed bytes as they are; value c - 32), one
+// 16-value group g at a time: with S1' = sum c xq and S2' = sum c xq2 over the group,
+//   254 sum (c - 32) xq + sum (c - 32) xq2 = 254 S1' + S2' - 32 (254 X1 + X2),
+// X1, X2 the group's input sums.  The xq2 chain starts at the group's input constant -32 (254 X1 + X2)
+// (Q6kLane, formed once per input slice), one 24-bit multiply-add joins the stages (|S1'| <= 16*63*127),
+// the integer (|.| < 2^24, exact in fp32) is weighted by the int8 sub-block scale times xd / 254, and the
+// block scale d multiplies the unit's sum.  Every kernel forms each group's term with this expression, so
+// the one-token and few-token kernels agree bit for bit.
+struct Q6kLane {
+    int k[4];    // xq2 chain start per 16-value group
+    float e[4];  // xd / 254 per group
+};
+
+__device__ __forceinline__ int q6k_group_const(u32 q0, u32 q1, u32 q2, u32 q3, u32 r0, u32 r1, u32 r2, u32 r3) {
+    int x1 = dot4(0x01010101u, q0, 0), x2 = dot4(0x01010101u, r0, 0);
+    x1 = dot4(0x01010101u, q1, x1); x2 = dot4(0x01010101u, r1, x2);
+    x1 = dot4(0x01010101u, q2, x1); x2 = dot4(0x01010101u, r2, x2);
+    x1 = dot4(0x01010101u, q3, x1); x2 = dot4(0x01010101u, r3, x2);
+    return -32 * (254 * x1 + x2);
+}
+
+__device__ __forceinline__ Q6kLane q6k_lane(const XSlice& x) {
+    Q6kLane c;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        c.k[g] = q6k_group_const(x.q[4 * g], x.q[4 * g + 1], x.q[4 * g + 2], x.q[4 * g + 3], x.q2[4 * g],
+                                 x.q2[4 * g + 1], x.q2[4 * g + 2], x.q2[4 * g + 3]);
+        c.e[g] = x.d[g] * FEIN;
+    }
+    return c;
+}
+
+// Group g's term: the chains from the raw codes and the group constant, joined and scaled.
+template <int G>
+__device__ __forceinline__ float q6k_group(const u32 (&lo)[4], const u32 (&qh)[4], const u32 (&xa)[4],
+                                           const u32 (&xc)[4], int k0, float sc_e, float acc) {
+    int a = 0, b = k0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const u32 c = q6k_codes<G>(lo[k], qh[k]);
+        a = dot4(c, xa[k], a);
+        b = dot4(c, xc[k], b);
+    }
+    return fmaf((float)(__mul24(a, 254) + b), sc_e, acc);
+}
+
+__device__ __forceinline__ float q6k_dot1(const Fmt<NMQ_Q6_K>::Raw& r, const XSlice& x, int u, const Q6kLane& c) {
     const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
     const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
     const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    const float d = h2f(r.d);
     const u32 sh = 8u * (u32)(u & 1);
+    float sc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sc[g] = (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        int s1 = 0, s2 = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const u32 lo = (g & 1) ? lb[k] : la[k];
-            const u32 c = g == 0 ? q6k_codes<0>(lo, qh[k])
-                                 : (g == 1 ? q6k_codes<1>(lo, qh[k]) : (g == 2 ? q6k_codes<2>(lo, qh[k]) : q6k_codes<3>(lo, qh[k])));
-            const u32 w = sub32x4(c);
-            s1 = dot4(w, x.q[4 * g + k], s1);
-            s2 = dot4(w, x.q2[4 * g + k], s2);
-        }
-        const float ws = d * (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
-        acc += ws * x.d[g] * ((float)s1 + FEIN * (float)s2);
+        const u32 xa[4] = {x.q[4 * g], x.q[4 * g + 1], x.q[4 * g + 2], x.q[4 * g + 3]};
+        const u32 xc[4] = {x.q2[4 * g], x.q2[4 * g + 1], x.q2[4 * g + 2], x.q2[4 * g + 3]};
+        const float se = sc[g] * c.e[g];
+        acc = g == 0 ? q6k_group<0>(la, qh, xa, xc, c.k[0], se, acc)
+            : g == 1 ? q6k_group<1>(lb, qh, xa, xc, c.k[1], se, acc)
+            : g == 2 ? q6k_group<2>(la, qh, xa, xc, c.k[2], se, acc) : q6k_group<3>(lb, qh, xa, xc, c.k[3], se, acc);
     }
-    return acc;
+    return acc * h2f(r.d);
 }
 
 // Q8_0, 34-byte blocks (quant.py:46-50, cudakern.py:307-313): unit u = blocks 2u and 2u+1 (68

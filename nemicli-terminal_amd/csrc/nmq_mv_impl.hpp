@@ -876,6 +876,7 @@ __device__ __forceinline__ float tq2_dot1(const Fmt<NMQ_TQ2_0>::Raw& raw, const 
 struct LaneConst {
     Q4kLane q4k[4];  // Q4_K: the unit's scale/min selection
     Tq2Lane tq2[4];  // TQ2_0 (kernels that hold their input slices): the unit's input constants
+    Q6kLane q6k[4];  // Q6_K (likewise)
 };
 
 template <int F, int T, int NITM>
@@ -894,10 +895,15 @@ __device__ __forceinline__ LaneConst lane_const(int lt, const XSlice (&x)[NITM])
 #pragma unroll
         for (int it = 0; it < NITM && it < 4; ++it) c.tq2[it] = tq2_lane(x[it]);
     }
+    if constexpr (F == NMQ_Q6_K) {
+#pragma unroll
+        for (int it = 0; it < NITM && it < 4; ++it) c.q6k[it] = q6k_lane(x[it]);
+    }
     return c;
 }
 
-// HELD: the slice constants of lane_const(lt, x) are present (TQ2_0 then takes the raw-code path).
+// HELD: the slice constants of lane_const(lt, x) are present; otherwise TQ2_0 and Q6_K form them from the
+// slice on the spot (the same integers: both give the same bits).
 template <int F, bool HELD = false>
 __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int u, const u64* tab, const XSlice& x,
                                            const LaneConst& lc, int it) {
@@ -905,9 +911,9 @@ __device__ __forceinline__ float unit_dot1(const typename Fmt<F>::Raw& raw, int 
     if constexpr (F == NMQ_Q4_K) {
         return q4k_dot1(raw, x, lc.q4k[it]);
     } else if constexpr (F == NMQ_Q6_K) {
-        return q6k_dot1(raw, x, u);
-    } else if constexpr (F == NMQ_TQ2_0 && HELD) {
-        return tq2_dot1(raw, x, lc.tq2[it]);
+        return HELD ? q6k_dot1(raw, x, u, lc.q6k[it]) : q6k_dot1(raw, x, u, q6k_lane(x));
+    } else if constexpr (F == NMQ_TQ2_0) {
+        return HELD ? tq2_dot1(raw, x, lc.tq2[it]) : tq2_dot1(raw, x, tq2_lane(x));
     } else {
         WUnit wu;
         FM::decode(raw, u, tab, wu);
@@ -1153,11 +1159,12 @@ inline void (*pick_mvt(int T))(MvParams) {
 // q6k_dot1 with the group's 2 x 16 input bytes and its xd read just before use.  (Unsigned codes with a
 // per-group offset -32 (sum xq + sum xq2 / 254) formed once per workgroup took 14 % fewer VALU
 // instructions but an extra LDS pass and barrier: 14.2 against 13.8 us for 4096x14336, not kept.)
+// q6k_dot1 with the unit's input read from the staged LDS copy and its group constants formed on the spot
+// (the same integers and fp32 operations: results equal q6k_dot1's bit for bit).
 __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const u8* base, int ktp, int u) {
     const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
     const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
     const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
-    const float d = h2f(r.d);
     const u32 sh = 8u * (u32)(u & 1);
     const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
     const float4 xd = *(const float4*)((const float*)(base + 2 * ktp) + 8 * b + 4 * h);
@@ -1165,25 +1172,18 @@ __device__ __forceinline__ float q6k_dot1_lds(const Fmt<NMQ_Q6_K>::Raw& r, const
     float acc = 0.f;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-        const int ch = 16 * b + 8 * h + 2 * g + j;
-        const int ph = swz<true>(ch);
+        const int ph = swz<true>(16 * b + 8 * h + 2 * g + j);
         const u32x4 a = *(const u32x4*)(base + 16 * ph);
         const u32x4 c = *(const u32x4*)(base + ktp + 16 * ph);
         const u32 xa[4] = {a.x, a.y, a.z, a.w};
         const u32 xc[4] = {c.x, c.y, c.z, c.w};
-        int s1 = 0, s2 = 0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const u32 lo = (g & 1) ? lb[k] : la[k];
-            const u32 w = g == 0 ? q6k_codes<0>(lo, qh[k])
-                                 : (g == 1 ? q6k_codes<1>(lo, qh[k]) : (g == 2 ? q6k_codes<2>(lo, qh[k]) : q6k_codes<3>(lo, qh[k])));
-            s1 = dot4(sub32x4(w), xa[k], s1);
-            s2 = dot4(sub32x4(w), xc[k], s2);
-        }
-        const float ws = d * (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
-        acc += ws * xdg[g] * ((float)s1 + FEIN * (float)s2);
+        const int k0 = q6k_group_const(a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w);
+        const float se = (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8) * (xdg[g] * FEIN);
+        acc = g == 0 ? q6k_group<0>(la, qh, xa, xc, k0, se, acc)
+            : g == 1 ? q6k_group<1>(lb, qh, xa, xc, k0, se, acc)
+            : g == 2 ? q6k_group<2>(la, qh, xa, xc, k0, se, acc) : q6k_group<3>(lb, qh, xa, xc, k0, se, acc);
     }
-    return acc;
+    return acc * h2f(r.d);
 }
 
 template <int F, int RW, int NIT>
@@ -1198,11 +1198,13 @@ __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, c
     for (int it = 0; it < NIT; ++it) {
         const int u = lane + it * 64;
         const int uc = min(u, U - 1);
+        // each 64-unit slice summed over the wave, the slices added in order from zero: the K-split
+        // kernel's order, so value input (staged here) and the two-stage input give the same bits
         if constexpr (F == NMQ_Q6_K) {
 #pragma unroll
             for (int rr = 0; rr < RW; ++rr) {
                 const float v = q6k_dot1_lds(st.raw[rr][it], lds, ktp, uc);
-                acc[rr] += u < U ? v : 0.f;
+                acc[rr] += team_sum<64>(u < U ? v : 0.f);
             }
         } else {
             XSlice x;
@@ -1210,13 +1212,11 @@ __device__ __forceinline__ void mvl_compute(const Mv1Step<F, 64, RW, NIT>& st, c
 #pragma unroll
             for (int rr = 0; rr < RW; ++rr) {
                 const float v = unit_dot1<F>(st.raw[rr][it], uc, tab, x, lc, it);
-                acc[rr] += u < U ? v : 0.f;
+                acc[rr] += team_sum<64>(u < U ? v : 0.f);
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // one input slice live at a time
     }
-#pragma unroll
-    for (int rr = 0; rr < RW; ++rr) acc[rr] = team_sum<64>(acc[rr]);
     if (lane == 0) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr)
@@ -1605,14 +1605,16 @@ __device__ __forceinline__ void load_slice(const int8_t* xq, const int8_t* xq2, 
 // in register lane k for the wave's k-th row; every 64 rows and at the end the KS partial sums of each row
 // meet in LDS and are added in slice order starting from zero, ((0 + p_0) + p_1) + ..., which is how the
 // few-token long-row kernel forms each token's sum.
-template <int F, int KS, int NBUF>
+// EXT: rows of several matrices scheduled as one (segments, nmq_mv_multi), each output as a launch of its
+// matrix alone gives it.
+template <int F, int KS, int NBUF, bool EXT>
 __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
-    args_early<false>(p);
+    args_early<EXT>(p);
     using FM = Fmt<F>;
     static_assert(F != NMQ_IQ2_XXS, "the grid table is staged by the LDS kernels only");
     __shared__ float part[KS][64];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const RowMap rm = row_map<false>(p, p.w, p.y);
+    const RowMap rm = row_map<EXT>(p, p.w, p.y);
     const int U = (p.n_in + 63) >> 6;
     const int u = 64 * w + lane, uc = min(u, U - 1);
     const int G = gridDim.x;
@@ -1622,7 +1624,7 @@ __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
     int r = blockIdx.x;
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) buf[i].load(rm, r + i * G, u, U, r);
-    const LaneConst lc = lane_const<F, 64, 1>(u);
+    const LaneConst lc = lane_const<F, 64, 1>(u, x);
     const u64* tab = nullptr;
     float res = 0.f;
     int k = 0, first = r;
@@ -1632,7 +1634,7 @@ __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
             const bool more = r < p.n_out;  // workgroup-uniform
             if (more) {
                 buf[(i + NBUF - 1) % NBUF].load(rm, r + (NBUF - 1) * G, u, U, r);
-                const float v = unit_dot1<F>(buf[i].raw[0][0], uc, tab, x[0], lc, 0);
+                const float v = unit_dot1<F, true>(buf[i].raw[0][0], uc, tab, x[0], lc, 0);
                 const float ws = team_sum<64>(u < U ? v : 0.f);
                 res = lane == k ? ws : res;
                 ++k;
@@ -1656,10 +1658,14 @@ __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
     }
 }
 
+template <int F, bool EXT>
+inline MvKernel pick_mvk_e(int ks) {
+    return ks == 2 ? mvk_kernel<F, 2, 3, EXT> : (ks == 3 ? mvk_kernel<F, 3, 3, EXT> : mvk_kernel<F, 4, 3, EXT>);
+}
 template <int F>
-inline MvKernel pick_mvk(int ks) {
+inline MvKernel pick_mvk(int ks, bool ext) {
     if constexpr (F == NMQ_IQ2_XXS) return nullptr;
-    else return ks == 2 ? mvk_kernel<F, 2, 3> : (ks == 3 ? mvk_kernel<F, 3, 3> : mvk_kernel<F, 4, 3>);
+    else return ext ? pick_mvk_e<F, true>(ks) : pick_mvk_e<F, false>(ks);
 }
 
 // ---- 2..4 tokens, long rows (Q6_K: the layer's down projection) ---------------------------------------
@@ -1891,16 +1897,15 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     }
     if constexpr (F != NMQ_IQ2_XXS) {
         // one token over rows of 129..256 units from the two-stage input: the K-split kernel (the long-row
-        // kernel below stays for value input, segments, experts and IQ2_XXS)
+        // kernel below stays for value input, experts and IQ2_XXS)
         const int U = (p.n_in + 63) / 64;
-        if (nc == 1 && U > 128 && U <= 256 && p.ids == nullptr && p.xv == nullptr && p.n_seg == 0 &&
-            tune(TUNE_MVK, 1) != 0) {
+        if (nc == 1 && U > 128 && U <= 256 && p.ids == nullptr && p.xv == nullptr && tune(TUNE_MVK, 1) != 0) {
             const int ks = (U + 63) / 64;
             int64_t g = (int64_t)tune(TUNE_MVK_WPC, 8) * di.cus / ks;
             if (g < 1) g = 1;
             if (g > p.n_out) g = p.n_out;
             p.nt = 64 * ks;
-            hipLaunchKernelGGL(pick_mvk<F>(ks), dim3((unsigned)g), dim3(p.nt), 0, stream, p);
+            hipLaunchKernelGGL(pick_mvk<F>(ks, p.n_seg > 0), dim3((unsigned)g), dim3(p.nt), 0, stream, p);
             return (int)hipGetLastError();
         }
     }

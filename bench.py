@@ -262,10 +262,13 @@ def run_configs(which, steps, warmup):
                 extra = {}
                 if n > 1:
                     us4, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
-                                      {"MVM": 0, "MVT_MAX": 1})
+                                      {"MVM": 0, "MVT_MAX": 1, "MVD": 0})
                     usm, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
-                                      {"MVM": 2, "MVT_MAX": 1})
-                    extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
+                                      {"MVM": 2, "MVT_MAX": 1, "MVD": 0})
+                    usd, _ = _mv_case(L, stream, "Q4_K", ws, raw, rows, 4096, X[:n], steps, warmup,
+                                      {"MVD_MIN": 2, "MVT_MAX": 1})
+                    extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3),
+                             "us_dense_matrix_core_kernel": round(usd, 3)}
                 _record("speculative", f"Q4_K {rows}x4096 n={n}", "Q4_K", us, alg_bytes("Q4_K", rows, 4096, n), err,
                         **extra)
             del ws

@@ -419,7 +419,265 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     }
 }
 
+// ---- Q4_K, 5..8 tokens: dense reads straight into LDS ----------------------------------------------
+// mvm_kernel reads, per instruction, 8 bytes of each of 16 rows per lane group: 16 short pieces per read.
+// A CU issuing those for 16 waves stalls for longer than HBM takes to deliver the bytes (per-wave time
+// stamps: 10 us until the last wave has issued its reads, against 6 us with dense reads of the same
+// bytes).  mvd_kernel keeps mvm_kernel's work split and arithmetic, but every read is dense (16 bytes per
+// lane, consecutive lanes on consecutive bytes), and weights and input move with global_load_lds_dwordx4
+// (lane l's 16 bytes land at the LDS address of the instruction + 16 l, no registers in between):
+//   - the input rows (xq, xq2 of each token) row-major, 16 + n_in bytes apart, so that the 16 rows' A
+//     operands of a step (8 bytes at row n, 32 step + 8 k-block) fall on distinct banks;
+//   - the weights, per wave in chunks of 2 blocks x 16 rows: slot u = 64 j + lane of instruction j holds
+//     piece u % 19 of row u / 19 (18 pieces of 16 bytes per row, slot 18 a padding copy of piece 17, so
+//     rows are 304 bytes apart and the 16 rows' operands fall on distinct banks).
+// (xd / 254, xs) per step and token are read densely into registers and stored as mvm_kernel stores them.
+// A wave holds one chunk buffer: chunk c + 1 is requested as soon as chunk c's operands are in registers,
+// and streams in while chunk c is computed.
+constexpr int MVD_ROW = 304;            // LDS bytes per row of a chunk buffer
+constexpr int MVD_BUF = 16 * MVD_ROW;   // bytes per wave
+typedef __attribute__((address_space(3))) void lds_void;
+
+// global_load_lds_dwordx4 issued by hand, its address a wave-uniform base (SGPR pair) plus an unsigned
+// 32-bit per-lane offset: the compiler neither counts it nor sees its LDS write, so it adds no waits of
+// its own (with the builtin it waits for every outstanding read before each later LDS access, since it
+// cannot tell the buffers apart).  The kernel waits with vm_wait<N> (memory clobber: no LDS access moves
+// across the wait).  M0 is set inside the statement; nothing else in the kernel uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // M0 is reserved: clobbering it is the point here
+__device__ __forceinline__ void dma16s(const void* base, u32 off, void* lds_dst) {
+    const u32 m = (u32)(uintptr_t)(lds_void*)lds_dst;
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Per-lane offsets of the chunk reads (the same for every chunk), from the chunk's first byte in row
+// rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % 19, 17) of row
+// min(row0 + u / 19, n_out - 1) >= rb0, so every offset is non-negative, also for tiles past the matrix.
+struct ChunkOffsets {
+    u32 o[5];
+};
+__device__ __forceinline__ ChunkOffsets mvd_offsets(const MvmParams& p, int row0, int lane) {
+    ChunkOffsets c;
+    const int rb0 = min(row0, p.n_out - 1);
+#pragma unroll
+    for (int j = 0; j < 5; ++j) {
+        const int u = 64 * j + lane;
+        const int r = min(row0 + u / 19, p.n_out - 1) - rb0, k = min(u % 19, 17);
+        c.o[j] = (u32)(r * (int)p.row_bytes + 16 * k);
+    }
+    return c;
+}
+
+// chunk of blocks blk, blk + 1 of rows row0 .. row0 + 15 into buf (5 instructions; the last one with 48 lanes)
+__device__ __forceinline__ void mvd_chunk(u8* buf, const MvmParams& p, const ChunkOffsets& co, int row0, int blk,
+                                          int lane) {
+    const u8* base = p.w + (int64_t)min(row0, p.n_out - 1) * p.row_bytes + (int64_t)blk * Mfma<NMQ_Q4_K>::BB;
+#pragma unroll
+    for (int j = 0; j < 5; ++j)
+        if (j < 4 || lane < 48) dma16s(base, co.o[j], buf + 1024 * j);
+}
+
+// Mfma<Q4_K>::load from the chunk buffer: block bb (0, 1) of the chunk, the lane's row n and k-block kb.
+__device__ __forceinline__ void mvd_frag(Mfma<NMQ_Q4_K>::Raw& r, const u8* buf, int bb, int n, int kb) {
+    const u8* b = buf + n * MVD_ROW + Mfma<NMQ_Q4_K>::BB * bb;
+    r.h = *(const u32x4*)b;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.q[i] = *(const u32x2*)(b + 16 + 32 * i + 8 * kb);
+}
+
+// One 256-value block (8 steps, one 32-value group each) of the lane's weight row into its sums of
+// tokens 2 kb and 2 kb + 1, A operands read from the row-major input (arow: the lane's input row n at
+// k-block kb; block b's steps 32 bytes apart).  The block's scales d, dmin apply once per block:
+//   y += d * sum_g (sc_g (254 S1 + S2)) (xd_g / 254)  -  dmin * sum_g m_g xs_g
+// with sc_g (254 S1 + S2) an exact int32 (|.| <= 63 * 254 * 32 * 127 * 15 * 1.004 < 2^31) rounded once to
+// fp32, where mvm_block forms d sc_g and dmin m_g per group.
+__device__ __forceinline__ void mvd_block(const Mfma<NMQ_Q4_K>::Raw& cur, int b, const u8* arow, const float2* xsc,
+                                          int kb, float (&acc)[2]) {
+    using M = Mfma<NMQ_Q4_K>;
+    const u8* ab = arow + 256 * b;
+    const float2* xb = xsc + 64 * b + 2 * kb;
+    // 6-bit scales and mins of groups 0..3 (bytes of lo) and 4..7 (bytes of hi): get_scale_min_k4
+    const u32 sc_lo = cur.h.y & 0x3f3f3f3fu, m_lo = cur.h.z & 0x3f3f3f3fu;
+    const u32 sc_hi = (cur.h.w & 0x0f0f0f0fu) | ((cur.h.y >> 2) & 0x30303030u);
+    const u32 m_hi = ((cur.h.w >> 4) & 0x0f0f0f0fu) | ((cur.h.z >> 2) & 0x30303030u);
+    float sd0 = 0.f, sd1 = 0.f, sm0 = 0.f, sm1 = 0.f;
+    u64 xv[2];
+    float4 xf[2];
+    xv[0] = *(const u64*)ab;
+    xf[0] = *(const float4*)xb;
+#pragma unroll
+    for (int s = 0; s < M::STEPS; ++s) {
+        if (s + 1 < M::STEPS) {
+            xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+            xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const u64 wv = M::frag(cur, s);
+        const u64 x = xv[s & 1];
+        const float4 f = xf[s & 1];
+        i32x4 c = {0, 0, 0, 0};
+        c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+        const u32 scw = s < 4 ? sc_lo : sc_hi, mw = s < 4 ? m_lo : m_hi;
+        const int sc = (int)((scw >> (8 * (s & 3))) & 0xffu), sc254 = 254 * sc;
+        const float mf = (float)((mw >> (8 * (s & 3))) & 0xffu);
+        // sc (254 S1 + S2) as 24-bit products (|S1|, |S2| <= 32 * 127 * 15, sc254 <= 16002)
+        sd0 = fmaf((float)(__mul24(c[0], sc254) + __mul24(c[1], sc)), f.x, sd0);
+        sd1 = fmaf((float)(__mul24(c[2], sc254) + __mul24(c[3], sc)), f.z, sd1);
+        sm0 = fmaf(mf, f.y, sm0);
+        sm1 = fmaf(mf, f.w, sm1);
+    }
+    const float d = h2f(cur.h.x), dm = h2f(cur.h.x >> 16);
+    acc[0] = fmaf(d, sd0, fmaf(-dm, sm0, acc[0]));
+    acc[1] = fmaf(d, sd1, fmaf(-dm, sm1, acc[1]));
+}
+
+// LDS: input rows 16 x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
+__host__ __device__ constexpr size_t mvd_lds(int n_in, int W) {
+    return (size_t)16 * (n_in + 16) + (size_t)2 * n_in + (size_t)W * MVD_BUF;
+}
+
+template <int NCH>
+__global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
+    using M = Mfma<NMQ_Q4_K>;
+    asm volatile("" ::"s"(p.w), "s"(p.xq), "s"(p.xq2), "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in),
+                 "s"(p.nc), "s"(p.ks), "s"(p.tpw), "s"(p.row_bytes), "s"(p.nblk));
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int W = p.ks * p.tpw, nt = 64 * W;
+    const int S = p.n_in / 32, RS = p.n_in + 16;
+    const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
+    const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
+    const int n = lane & 15, kb = lane >> 4;
+    const int b0 = slice * 2 * NCH;
+    float2* xsc = (float2*)(lds + 16 * RS);
+    u8* buf = lds + 16 * RS + 2 * p.n_in + wave * MVD_BUF;
+
+    // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2 (absent tokens re-read xq's first
+    // bytes), 1 KB per instruction, instruction i = row i / MB, kilobyte i % MB, over the waves
+    for (int r = wave; r < 16; r += W) {
+        const int t = r >> 1;
+        const int8_t* row = t < p.nc ? ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in : p.xq;
+        for (int m = 0; 1024 * m < p.n_in; ++m)
+            if (1024 * m + 16 * lane < p.n_in) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
+    }
+    // (xd, xs): piece i < 4 S = 4 consecutive steps (of S / 4 groups of 4) of token i & 7 of xd
+    // (i / 8 < S / 4) or xs, read by hand.  Every thread issues both reads (threads past the pieces and
+    // absent tokens re-read xd's first bytes): the code from the reads to their wait is straight-line,
+    // so the compiler has no join at which it would copy a register whose read is still outstanding.
+    u32x4 xv[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
+        const bool ok = i < 4 * S && t < p.nc;
+        xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * S + 4 * m : p.xd);
+    }
+    // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
+    // request order, so input requested after another wave's weights would wait for them (the barrier
+    // waits for issue only: the reads are not counted by the compiler's waits)
+    const ChunkOffsets co = mvd_offsets(p, row0, lane);
+    lds_barrier();
+    mvd_chunk(buf, p, co, row0, b0, lane);
+    asm volatile("s_waitcnt vmcnt(5)" : "+v"(xv[0]), "+v"(xv[1]) : : "memory");
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
+        if (i < 4 * S) {
+            const float v[4] = {__uint_as_float(xv[k].x), __uint_as_float(xv[k].y), __uint_as_float(xv[k].z),
+                                __uint_as_float(xv[k].w)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                ((float*)xsc)[((4 * m + e) * 8 + t) * 2 + a] = t < p.nc ? (a ? v[e] : v[e] * FEIN) : 0.f;
+        }
+    }
+    lds_barrier();
+
+    const u8* arow = lds + n * RS + 8 * kb;
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+        vm_wait<0>();  // chunk c in the buffer
+        typename M::Raw r0, r1;
+        mvd_frag(r0, buf, 0, n, kb);
+        mvd_frag(r1, buf, 1, n, kb);
+        if (c + 1 < NCH) {
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the operands read before the buffer is refilled
+            mvd_chunk(buf, p, co, row0, b0 + 2 * (c + 1), lane);
+        }
+        mvd_block(r0, b0 + 2 * c, arow, xsc, kb, acc);
+        mvd_block(r1, b0 + 2 * c + 1, arow, xsc, kb, acc);
+    }
+
+    // add the KS slices of each tile (as mvm_kernel)
+    float* red = (float*)lds;
+    lds_barrier();
+    red[(wave * 64 + lane) * 2] = acc[0];
+    red[(wave * 64 + lane) * 2 + 1] = acc[1];
+    lds_barrier();
+    if (slice == 0) {
+        const int r = row0 + n;
+        float s0 = 0.f, s1 = 0.f;
+        for (int q = 0; q < p.ks; ++q) {
+            const int ri = ((tile_in_wg * p.ks + q) * 64 + lane) * 2;
+            s0 += red[ri];
+            s1 += red[ri + 1];
+        }
+        const int t = 2 * kb;
+        if (r < p.n_out) {
+            if (t < p.nc) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = s0;
+            if (t + 1 < p.nc) gpw<float>(p.y)[(int64_t)(t + 1) * p.n_out + r] = s1;
+        }
+    }
+}
+
 // ---- host side ------------------------------------------------------------------------------------
+
+struct MvdShape {
+    bool ok;
+    int ks, tpw, grid_x, nch;
+    size_t lds;
+};
+
+// Q4_K, MVD_MIN (5) .. 8 tokens, rows of 512 .. 4096 values (a multiple of 512): tiles of 16 rows, about
+// one workgroup of 4 .. 16 waves per CU, K slices of 2 or 4 blocks (1 or 2 chunks).
+inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max) {
+    MvdShape s{};
+    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, 5) || nc > 8 || n_in % 512 || n_in > 4096) return s;
+    const int nblk = n_in / 256;
+    const int tiles = (n_out + 15) / 16;
+    int tpw = tune(TUNE_MVD_TPW, 0);
+    if (tpw <= 0) tpw = std::min((tiles + cus - 1) / cus, 8);
+    int ks = tune(TUNE_MVD_KS, 0);
+    if (ks <= 0) {
+        ks = 1;
+        while (ks * 2 * tpw <= 16 && nblk % (ks * 4) == 0) ks *= 2;  // slices of at least 2 blocks
+    }
+    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || nblk % ks || (nblk / ks) % 2) return s;
+    s.nch = nblk / ks / 2;
+    if (s.nch != 1 && s.nch != 2) return s;
+    s.ks = ks;
+    s.tpw = tpw;
+    s.grid_x = (tiles + tpw - 1) / tpw;
+    s.lds = mvd_lds(n_in, ks * tpw);
+    s.ok = s.lds + 4096 <= (size_t)lds_max;
+    return s;
+}
+
+inline void (*pick_mvd(const MvdShape& s))(MvmParams) {
+    return s.nch == 1 ? mvd_kernel<1> : mvd_kernel<2>;
+}
+
+inline int launch_mvd(const MvdShape& s, MvmParams p, hipStream_t stream) {
+    p.ks = s.ks;
+    p.tpw = s.tpw;
+    hipLaunchKernelGGL(pick_mvd(s), dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
+    return (int)hipGetLastError();
+}
 
 struct MvmShape {
     bool ok;

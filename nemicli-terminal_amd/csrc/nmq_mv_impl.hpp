@@ -685,6 +685,34 @@ __device__ __forceinline__ float team_sum(float v) {
     return v;
 }
 
+// team_sum<64> of N values, level by level so that the N chains interleave (no wait states between a
+// DPP add and the one that reads its result); each result equals team_sum<64> of that value bit for bit.
+template <int N>
+__device__ __forceinline__ void team_sum64_n(float (&v)[N]) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0xB1, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x4E, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x141, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), 0x140, 0xF, 0xF, false));
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i]), false, false);
+        v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+}
+
 template <int F, int T, int RW, int NITM>
 struct Mv1Step {
     using FM = Fmt<F>;
@@ -1669,22 +1697,91 @@ inline MvKernel pick_mvk(int ks, bool ext) {
 }
 
 // ---- 2..4 tokens, long rows (Q6_K: the layer's down projection) ---------------------------------------
+// LDS bytes per token of the few-token long-row kernel: xq and xq2 (ktp each, stage1_store's strided
+// layout), xd / 254 per 32-value group (ktp / 32 floats), the xq2 chain start -32 (254 X1 + X2) of every
+// 16-value group (ktp / 16 ints, the four of a unit together).
+__host__ __device__ constexpr int q6k_tok_bytes(int ktp) { return 2 * ktp + ktp / 8 + ktp / 4; }
+
+// One token's staging round in that layout.  The thread holding chunk i (values 16i .. 16i + 15, one
+// Q6_K group: i = 16b + 8h + 2g + j for group g of unit u = 4b + 2h + j) forms its group constant from
+// the registers it is about to store, so the constants cost no LDS pass of their own.
+__device__ __forceinline__ void stage_q6k_store(const XRound& r, u8* lds, int n_in, int ktp) {
+    const int i = threadIdx.x;
+    if (i < ktp / 16) {
+        const bool ok = 16 * i < n_in;
+        const u32x4 a = ok ? r.a : u32x4{0u, 0u, 0u, 0u}, b = ok ? r.b : u32x4{0u, 0u, 0u, 0u};
+        const int ph = swz<true>(i);
+        *(u32x4*)(lds + 16 * ph) = a;
+        *(u32x4*)(lds + ktp + 16 * ph) = b;
+        const int u = ((i >> 4) << 2) | (((i >> 3) & 1) << 1) | (i & 1);
+        ((int*)(lds + 2 * ktp + ktp / 8))[4 * u + ((i >> 1) & 3)] =
+            q6k_group_const(a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w);
+    }
+    if (i < ktp / 32) ((float*)(lds + 2 * ktp))[i] = i < n_in / 32 ? r.d * FEIN : 0.f;
+}
+
+// Q6_K unit u for NC tokens staged by stage_q6k_store: the 64 codes and the four scales decoded once,
+// each token's groups formed with q6k_dot1's integers and fp32 operations in its order, so v[t] equals
+// q6k_dot1 on token t bit for bit.
+template <int NC>
+__device__ __forceinline__ void q6k_dotn_lds(const Fmt<NMQ_Q6_K>::Raw& r, const u8* lds, int tok, int ktp, int u,
+                                             float (&v)[NC]) {
+    const u32 la[4] = {r.la.x, r.la.y, r.la.z, r.la.w};
+    const u32 lb[4] = {r.lb.x, r.lb.y, r.lb.z, r.lb.w};
+    const u32 qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
+    u32 c[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        c[0][k] = q6k_codes<0>(la[k], qh[k]);
+        c[1][k] = q6k_codes<1>(lb[k], qh[k]);
+        c[2][k] = q6k_codes<2>(la[k], qh[k]);
+        c[3][k] = q6k_codes<3>(lb[k], qh[k]);
+    }
+    const u32 sh = 8u * (u32)(u & 1);
+    float sc[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) sc[g] = (float)(int8_t)bfe(g < 2 ? r.sc.x : r.sc.y, sh + 16u * (u32)(g & 1), 8);
+    const float d = h2f(r.d);
+    const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+#pragma unroll
+    for (int t = 0; t < NC; ++t) {
+        const u8* base = lds + t * tok;
+        const float4 xd = *(const float4*)((const float*)(base + 2 * ktp) + 8 * b + 4 * h);
+        const u32x4 kc = *(const u32x4*)((const int*)(base + 2 * ktp + ktp / 8) + 4 * u);
+        const float e[4] = {xd.x, xd.y, xd.z, xd.w};
+        const int k0[4] = {(int)kc.x, (int)kc.y, (int)kc.z, (int)kc.w};
+        float acc = 0.f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int ph = swz<true>(16 * b + 8 * h + 2 * g + j);
+            const u32x4 xa = *(const u32x4*)(base + 16 * ph);
+            const u32x4 xc = *(const u32x4*)(base + ktp + 16 * ph);
+            int s1 = dot4(c[g][0], xa.x, 0), s2 = dot4(c[g][0], xc.x, k0[g]);
+            s1 = dot4(c[g][1], xa.y, s1); s2 = dot4(c[g][1], xc.y, s2);
+            s1 = dot4(c[g][2], xa.z, s1); s2 = dot4(c[g][2], xc.z, s2);
+            s1 = dot4(c[g][3], xa.w, s1); s2 = dot4(c[g][3], xc.w, s2);
+            acc = fmaf((float)(__mul24(s1, 254) + s2), sc[g] * e[g], acc);
+        }
+        v[t] = acc * d;
+    }
+}
+
 // The long-row kernel for NC tokens: one row per wave in 16-wave workgroups (one per CU with the NC
-// staged inputs, 32 KB each for 14336 values), all of the row's weights requested at once, every token's
-// input staged in LDS (one round each, read before the weight reads, stored after them), and each
-// token's sum formed exactly as the one-token long-row kernel forms it (q6k_dot1_lds per unit, added in
-// unit order, team_sum): every output equals the one-token launch on that token bit for bit.
+// staged inputs, 34 KB each for 14336 values), all of the row's weights requested at once, every token's
+// input staged in LDS (one round each, read before the weight reads, stored after them), each unit's
+// codes decoded once for all tokens, and each token's sum formed exactly as the one-token K-split kernel
+// forms it (q6k_dot1's terms per unit, team_sum per 64-unit slice, slices added in order from zero):
+// every output equals the one-token launch on that token bit for bit.
 template <int NC, int NIT>
 __global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
     args_early<false>(p);
     constexpr int F = NMQ_Q6_K;
-    using FM = Fmt<F>;
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), W = p.nt >> 6;
     const RowMap rm = row_map<false>(p, p.w, p.y);
     const int U = (p.n_in + 63) >> 6;
     const int row = blockIdx.x * W + wave;
-    const int tok = p.ktp * 9 / 4;  // LDS bytes per token
+    const int tok = q6k_tok_bytes(p.ktp);
     Mv1Step<F, 64, 1, NIT> a;
     {
         XRound r[NC];
@@ -1696,7 +1793,7 @@ __global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
         a.load(rm, row, lane, U, row);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int t = 0; t < NC; ++t) stage1_store<FM::STRIDED>(r[t], 0, lds + t * tok, p.n_in, p.ktp, p.nt);
+        for (int t = 0; t < NC; ++t) stage_q6k_store(r[t], lds + t * tok, p.n_in, p.ktp);
         lds_barrier();
     }
     if (row >= p.n_out) return;  // wave-uniform, after the workgroup's last barrier
@@ -1709,12 +1806,14 @@ __global__ __launch_bounds__(1024) void mvlt_kernel(MvParams p) {
     for (int it = 0; it < NIT; ++it) {
         const int u = lane + it * 64;
         const int uc = min(u, U - 1);
+        float v[NC];
+        q6k_dotn_lds<NC>(a.raw[0][it], lds, tok, p.ktp, uc, v);
 #pragma unroll
-        for (int t = 0; t < NC; ++t) {
-            const float v = q6k_dot1_lds(a.raw[0][it], lds + t * tok, p.ktp, uc);
-            acc[t] += team_sum<64>(u < U ? v : 0.f);
-        }
-        __builtin_amdgcn_sched_barrier(0);  // one unit's input slices live at a time
+        for (int t = 0; t < NC; ++t) v[t] = u < U ? v[t] : 0.f;
+        team_sum64_n<NC>(v);
+#pragma unroll
+        for (int t = 0; t < NC; ++t) acc[t] += v[t];
+        __builtin_amdgcn_sched_barrier(0);  // one unit's codes live at a time
     }
     if (lane == 0) {
 #pragma unroll
@@ -1851,7 +1950,7 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             p.n_seg == 0) {
             const int U = (p.n_in + 63) / 64;
             const int ktp = (p.n_in + 127) / 128 * 128;
-            const size_t lds = (size_t)nc * ktp * 9 / 4;
+            const size_t lds = (size_t)nc * q6k_tok_bytes(ktp);
             const int W = 16;
             if (U > 128 && U <= 256 && ktp / 16 <= 64 * W && lds + 4096 <= (size_t)di.lds_max_big) {
                 p.ktp = ktp;
@@ -1862,6 +1961,19 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
                                      : (n3 ? mvlt_kernel<4, 3> : mvlt_kernel<4, 4>);
                 hipLaunchKernelGGL(k, dim3((unsigned)((p.n_out + W - 1) / W)), dim3(p.nt), lds, stream, p);
                 return (int)hipGetLastError();
+            }
+        }
+    }
+    if constexpr (F == NMQ_Q4_K) {
+        if (nc >= 2 && p.ids == nullptr) {
+            const MvdShape sd = plan_mvd(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
+            if (sd.ok) {
+                MvmParams q{};
+                q.w = p.w; q.xq = p.xq; q.xq2 = p.xq2; q.xd = p.xd; q.xs = p.xs; q.y = p.y;
+                q.n_out = p.n_out; q.n_in = p.n_in; q.nc = nc;
+                q.row_bytes = p.row_bytes;
+                q.nblk = p.n_in / 256;
+                return launch_mvd(sd, q, stream);
             }
         }
     }

@@ -37,6 +37,10 @@ enum Tune : int {
     TUNE_MMH_G,       // fp16 matrix-core kernel: groups of 16 tokens per workgroup
     TUNE_MVK,         // 0 disables the K-split long-row kernel (one token, rows of 129..256 units)
     TUNE_MVK_WPC,     // K-split long-row kernel: resident waves per CU
+    TUNE_MVD,         // 0 disables the dense-read matrix-core kernel (Q4_K, 5..8 tokens)
+    TUNE_MVD_MIN,     // fewest tokens that it takes
+    TUNE_MVD_TPW,     // its row tiles per workgroup
+    TUNE_MVD_KS,      // its slices of the row
     TUNE_COUNT
 };
 
@@ -44,7 +48,8 @@ enum Tune : int {
 inline const char* const kTuneNames[TUNE_COUNT] = {
     "MV1",      "MV1_MAXNIT", "MV1_RW",  "MV1_NBUF", "MV1_WPC", "MV1_W",   "MV1_MODE", "MV1_HR",
     "MVL",      "MVL_WPC",    "MVL_W",   "MVC_WGPC", "MVC_RW",  "MVC_ROWS", "MVT_MAX", "MVT_WPC",
-    "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G",    "MVK",     "MVK_WPC"};
+    "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G",    "MVK",     "MVK_WPC",
+    "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS"};
 
 constexpr int TUNE_UNSET = INT_MIN;
 

@@ -190,6 +190,7 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, tune, fmt, split):
     from ggufengine_amd.gguf_types import TYPE_ID
     tune(MVM=2)   # the matrix-core path from 2 tokens on, whatever the format
     tune(MVT_MAX=1)   # (not the few-token Q4_K kernel)
+    tune(MVD=0)   # (nor the dense-read Q4_K kernel)
     tune(MVM_TPW=tpw)
     tune(MVM_KS=ks)
     for nc in (2, 7, 8, 12, 16):
@@ -204,6 +205,41 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, tune, fmt, split):
                                    nmq.stream_ptr()))
         torch.cuda.synchronize()
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+@pytest.mark.parametrize("shape", [(14336, 4096), (4096, 4096), (200, 4096), (1000, 2048), (333, 1024),
+                                   (130, 512)])
+@pytest.mark.parametrize("split", [None, (1, 4), (2, 8), (4, 2)])
+def test_mv_tokens_dense_mfma(nmq, oracle, tune, shape, split):
+    """Q4_K 2..8 tokens on the dense-read matrix-core kernel (weights and input moved into LDS by
+    global_load_lds; the default for 5..8 tokens): the planner's split and forced (tiles per workgroup,
+    K slices) splits, slices of 2 and 4 blocks, partial last tiles and tiles past the matrix."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out, n_in = shape
+    nblk = n_in // 256
+    if split is not None:
+        tpw, ks = split
+        if nblk % ks or (nblk // ks) not in (2, 4) or tpw * ks < 4:
+            pytest.skip("split outside the kernel's slices")
+        tune(MVD_TPW=tpw)
+        tune(MVD_KS=ks)
+    elif n_out < 16 * 4:
+        pytest.skip("planner keeps small matrices elsewhere")
+    tune(MVD_MIN=2)
+    tune(MVT_MAX=1)
+    raw = random_blocks("Q4_K", n_out * n_in // 256, seed=71 + n_out % 97)
+    raw_d = dev(raw)
+    for nc in (2, 5, 8) if n_out > 5000 else (2, 3, 4, 5, 6, 7, 8):
+        x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        x[:, 3] = -25.0
+        e = quant_dev(dev(x))
+        y = torch.full((nc, n_out), float("nan"), device="cuda")
+        say("mv tokens dense mfma", shape, split, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID["Q4_K"], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                   e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                   nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        _check_mv(oracle, "Q4_K", raw, n_out, n_in, x, y)
 
 
 @pytest.mark.parametrize("fmt", FMTS)

@@ -48,6 +48,9 @@ def hazards(asm: str, name: str):
     for hand, t in ins:
         op = t.split()[0]
         args = [a.strip() for a in t[len(op):].split(",")]
+        if hand and op.startswith("global_load_lds"):
+            pend.append((set(), t))   # counted by vmcnt, no register written
+            continue
         if hand and op.startswith("global_load"):
             pend.append((_vregs(args[0]), t))
             continue
@@ -119,3 +122,49 @@ def test_checker_finds_a_planted_read(asm):
     end = text.index(";;#ASMEND", m.end()) + len(";;#ASMEND")
     planted = text[:end] + f"\n\tv_mov_b32_e32 v250, v{m.group(1)}\n" + text[end:]
     assert hazards(planted, name)
+
+
+DMA_KERNEL = re.compile(r"^(_ZN3nmq10mvd_kernel\w*EEEvNS_9MvmParamsE):", re.M)
+
+
+def m0_outside_hand_code(asm: str, name: str):
+    """Instructions outside the inline-assembly blocks that name M0: the dense-read kernel sets M0 for
+    its hand-issued global_load_lds inside those blocks and relies on nothing else using it."""
+    body = asm[asm.index(name + ":"):]
+    body = body[:body.index("s_endpgm")]
+    bad, hand = [], False
+    for line in body.split("\n"):
+        t = line.split(";")[0].strip() if not line.strip().startswith(";;#ASM") else line.strip()
+        if t.startswith(";;#ASMSTART"):
+            hand = True
+        elif t.startswith(";;#ASMEND"):
+            hand = False
+        elif t and not hand and re.search(r"\bm0\b", t):
+            bad.append(t)
+    return bad
+
+
+def test_dense_read_kernels_touch_no_outstanding_register(asm):
+    """mvd_kernel reads (xd, xs) by hand (global_load_dwordx4) with its chunk reads (global_load_lds, no
+    destination register) in flight: no instruction may touch those registers before the wait."""
+    names = DMA_KERNEL.findall(asm["nmq_mv_q4_k.hip"])
+    assert names
+    bad = [h for n in names for h in hazards(asm["nmq_mv_q4_k.hip"], n)]
+    assert not bad, bad[:5]
+
+
+def test_dense_read_kernels_keep_m0_to_themselves(asm):
+    names = DMA_KERNEL.findall(asm["nmq_mv_q4_k.hip"])
+    assert len(names) == 2, names
+    bad = [(n, t) for n in names for t in m0_outside_hand_code(asm["nmq_mv_q4_k.hip"], n)]
+    assert not bad, bad[:5]
+    # and every hand block that writes M0 issues its LDS load right after
+    text = asm["nmq_mv_q4_k.hip"]
+    for n in names:
+        body = text[text.index(n + ":"):]
+        body = body[:body.index("s_endpgm")]
+        for blk in re.findall(r";;#ASMSTART(.*?);;#ASMEND", body, re.S):
+            ops = [l.strip() for l in blk.split("\n") if l.strip()]
+            if any("m0" in o for o in ops):
+                assert len(ops) == 2 and ops[0].startswith("s_mov_b32 m0") and \
+                    ops[1].startswith("global_load_lds_dwordx4"), ops

@@ -49,7 +49,7 @@ const char* nmq_strerror(int code);
  * take their launch shape from constants in mmvq.py:25-37 and cudakern.py:31-54).  name: a knob of
  * the launch planner without or with the "NMQ_" prefix (MV1, MV1_MODE, MV1_HR, MV1_WPC, MV1_W,
  * MV1_RW, MV1_NBUF, MV1_MAXNIT, MVL, MVL_WPC, MVL_W, MVC_WGPC, MVC_RW, MVC_ROWS, MVT_MAX, MVT_WPC,
- * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVD, MVD_MIN, MVD_TPW, MVD_KS); value
+ * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVD, MVD_MIN, MVD_TPW, MVD_KS, MV1_T); value
  * NMQ_TUNE_DEFAULT restores the measured default.
  * Process-wide, read by every later launch; the environment is never consulted.  NMQ_ERR_ARG for an
  * unknown name.  nmq_get_tuning writes the override or NMQ_TUNE_DEFAULT.

@@ -1530,6 +1530,8 @@ inline Mv1Shape plan_mv1(int n_out, int n_in, int n_mats, const DeviceInfo& di, 
     if (!tune(TUNE_MV1, 1)) return s;
     const int U = (n_in + 63) / 64;
     s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    const int tf = tune(TUNE_MV1_T, 0);
+    if (tf == 16 || tf == 32 || tf == 64) s.T = tf;
     const int nit = (U + s.T - 1) / s.T;
     if (nit > tune(TUNE_MV1_MAXNIT, 2)) return s;
     s.nitm = nit <= 1 ? 1 : (nit <= 2 ? 2 : 4);

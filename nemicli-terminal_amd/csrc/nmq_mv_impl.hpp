@@ -840,6 +840,54 @@ struct QdStepAsm {
     }
 };
 
+__device__ __forceinline__ u32x2 gload8s(const u8* base, u32 off) {
+    u32x2 v;
+    asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+    return v;
+}
+template <int OFF>
+__device__ __forceinline__ u32x4 gload16so(const u8* base, u32 off) {
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, %2 offset:%3" : "=v"(v) : "v"(off), "s"(base), "n"(OFF));
+    return v;
+}
+
+// Q6_K unit reads by hand for kernels with one row per wave (T = 64): five reads per unit from the row's
+// address in scalar registers and lane-constant offsets (Fmt<Q6_K>::load's layout: ql at 64h + 16j and
+// +32, qh at 128 + 32h + 16j, the scales at 192 + 8h, d at 208 of block u / 4).
+template <int NITM>
+struct Q6kStepAsm {
+    Fmt<NMQ_Q6_K>::Raw raw[NITM];
+    template <int T>
+    __device__ __forceinline__ void load(const RowMap& rm, int r, int lt, int U, int fb) {
+        static_assert(T == 64, "one row per wave");
+        const int rs = r < rm.n_out ? r : min(fb, rm.n_out - 1);
+        const u8* rp = (const u8*)uniform64((int64_t)rm.row(rs));
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            const int u = min(lt + it * T, U - 1), h = (u >> 1) & 1, j = u & 1;
+            const u32 ob = (u32)((u >> 2) * Fmt<NMQ_Q6_K>::BB), ol = ob + (u32)(64 * h + 16 * j);
+            raw[it].la = gload16s(rp, ol);
+            raw[it].lb = gload16so<32>(rp, ol);
+            raw[it].qh = gload16s(rp, ob + (u32)(128 + 32 * h + 16 * j));
+            raw[it].sc = gload8s(rp, ob + (u32)(192 + 8 * h));
+            raw[it].d = gload2us(rp, ob + 208u);
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+#pragma unroll
+        for (int it = 0; it < NITM; ++it) {
+            if (it == 0)
+                asm volatile("s_waitcnt vmcnt(%5)"
+                             : "+v"(raw[it].la), "+v"(raw[it].lb), "+v"(raw[it].qh), "+v"(raw[it].sc), "+v"(raw[it].d)
+                             : "n"(N));
+            else
+                asm volatile("" : "+v"(raw[it].la), "+v"(raw[it].lb), "+v"(raw[it].qh), "+v"(raw[it].sc), "+v"(raw[it].d));
+        }
+    }
+};
+
 // Hand-issued step buffers per format (HandStep<F, NITM>::NL reads per unit).
 template <int F, int NITM>
 struct HandStep : QdStepAsm<F, NITM> {
@@ -849,7 +897,13 @@ template <int NITM>
 struct HandStep<NMQ_Q4_K, NITM> : Q4kStepAsm<NITM> {
     static constexpr int NL = 3;
 };
+template <int NITM>
+struct HandStep<NMQ_Q6_K, NITM> : Q6kStepAsm<NITM> {  // one row per wave only (the K-split kernel)
+    static constexpr int NL = 5;
+};
 constexpr bool hand_format(int f) { return f == NMQ_Q4_K || f == NMQ_TQ2_0 || f == NMQ_IQ2_XXS; }
+// formats whose reads the K-split kernel issues by hand
+constexpr bool mvk_hand(int f) { return f == NMQ_Q4_K || f == NMQ_TQ2_0 || f == NMQ_Q6_K; }
 
 // Per-lane constants of the one-token path (units of a lane are fixed: u = lt + it*T).
 // TQ2_0 on the raw 2-bit codes c (value c - 1).  Run r of a unit (16 values, one xd) holds its codes at bit
@@ -1628,6 +1682,59 @@ __device__ __forceinline__ void load_slice(const int8_t* xq, const int8_t* xq2, 
     }
 }
 
+// load_slice with the reads issued by hand (gload16/gload8): wait<N>() waits for them with N later reads
+// out, then unpack() forms the slice.
+template <bool STRIDED>
+struct SliceAsm {
+    u32x4 a[4], c[4], dd;
+    u32x2 d2, s2;
+    __device__ __forceinline__ void load(const int8_t* xq, const int8_t* xq2, const float* xd, const float* xs, int u) {
+        if (!STRIDED) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[k] = gload16(xq + 64 * u + 16 * k);
+                c[k] = gload16(xq2 + 64 * u + 16 * k);
+            }
+            d2 = gload8(xd + 2 * u);
+            s2 = gload8(xs + 2 * u);
+        } else {
+            const int b = u >> 2, h = (u >> 1) & 1, j = u & 1;
+            const int v0 = 256 * b + 128 * h + 16 * j;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                a[k] = gload16(xq + v0 + 32 * k);
+                c[k] = gload16(xq2 + v0 + 32 * k);
+            }
+            dd = gload16(xd + 8 * b + 4 * h);
+        }
+    }
+    template <int N>
+    __device__ __forceinline__ void wait() {
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+        if (!STRIDED)
+            asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(c[0]), "+v"(c[1]), "+v"(c[2]),
+                         "+v"(c[3]), "+v"(d2), "+v"(s2));
+        else
+            asm volatile("" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(c[0]), "+v"(c[1]), "+v"(c[2]),
+                         "+v"(c[3]), "+v"(dd));
+    }
+    __device__ __forceinline__ void unpack(XSlice& x) const {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x.q[4 * k] = a[k].x; x.q[4 * k + 1] = a[k].y; x.q[4 * k + 2] = a[k].z; x.q[4 * k + 3] = a[k].w;
+            x.q2[4 * k] = c[k].x; x.q2[4 * k + 1] = c[k].y; x.q2[4 * k + 2] = c[k].z; x.q2[4 * k + 3] = c[k].w;
+        }
+        if (!STRIDED) {
+            x.d[0] = __uint_as_float(d2.x); x.d[1] = __uint_as_float(d2.y); x.d[2] = 0.f; x.d[3] = 0.f;
+            x.s[0] = __uint_as_float(s2.x); x.s[1] = __uint_as_float(s2.y);
+        } else {
+            x.d[0] = __uint_as_float(dd.x); x.d[1] = __uint_as_float(dd.y);
+            x.d[2] = __uint_as_float(dd.z); x.d[3] = __uint_as_float(dd.w);
+            x.s[0] = x.s[1] = 0.f;
+        }
+    }
+};
+
 // Rows of 65..256 units (one token, two-stage input): a workgroup of KS = ceil(U / 64) waves walks the rows
 // blockIdx.x, blockIdx.x + G, ... (G = gridDim.x); wave w takes units 64w .. 64w+63 of every row, one per lane,
 // with that unit's input slice read straight from global memory into registers once (no LDS staging) and the
@@ -1637,11 +1744,12 @@ __device__ __forceinline__ void load_slice(const int8_t* xq, const int8_t* xq2, 
 // few-token long-row kernel forms each token's sum.
 // EXT: rows of several matrices scheduled as one (segments, nmq_mv_multi), each output as a launch of its
 // matrix alone gives it.
-template <int F, int KS, int NBUF, bool EXT>
+template <int F, int KS, int NBUF, bool EXT, bool HR = false>
 __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
     args_early<EXT>(p);
     using FM = Fmt<F>;
     static_assert(F != NMQ_IQ2_XXS, "the grid table is staged by the LDS kernels only");
+    static_assert(!HR || (mvk_hand(F) && !EXT), "hand-issued reads: Q4_K, TQ2_0, Q6_K, without segments");
     __shared__ float part[KS][64];
     const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const RowMap rm = row_map<EXT>(p, p.w, p.y);
@@ -1649,15 +1757,72 @@ __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
     const int u = 64 * w + lane, uc = min(u, U - 1);
     const int G = gridDim.x;
     XSlice x[1];
-    load_slice<FM::STRIDED>(p.xq, p.xq2, p.xd, p.xs, uc, x[0]);
-    Mv1Step<F, 64, 1, 1> buf[NBUF];
+    if constexpr (!HR) load_slice<FM::STRIDED>(p.xq, p.xq2, p.xd, p.xs, uc, x[0]);
+    const u64* tab = nullptr;
+    float res = 0.f;
     int r = blockIdx.x;
+    int k = 0, first = r;
+    // the KS partial sums of the batch's k rows, added in slice order from zero (a macro rather than a
+    // lambda: a lambda capturing the row map by reference made the compiler keep the map in scratch)
+#define NMQ_MVK_FLUSH()                                                           \
+    do {                                                                          \
+        part[w][lane] = res;                                                      \
+        lds_barrier();                                                            \
+        if (threadIdx.x < (unsigned)k) {                                          \
+            float sum = 0.f;                                                      \
+            _Pragma("unroll") for (int q = 0; q < KS; ++q) sum += part[q][threadIdx.x]; \
+            *gpw<float>(rm.out(first + (int)threadIdx.x * G)) = sum;             \
+        }                                                                         \
+        lds_barrier();                                                            \
+        k = 0;                                                                    \
+        first = r;                                                                \
+    } while (0)
+    if constexpr (HR) {
+        // The reads of every step are issued by hand (with buffers rotating through the loop the compiler
+        // waits for all outstanding reads at its head) and each step waits for its own reads only.  The code
+        // from a read to its wait is straight-line: the loop leaves by a branch taken before any read of the
+        // step is issued, and every flush and the exit first wait for all outstanding reads.
+        // The input slice is read by hand too, ahead of the first weight steps, and waited for with them out.
+        using HS = HandStep<F, 1>;
+        constexpr int HW = HS::NL * (NBUF - 1);
+        HS hb[NBUF];
+        {
+            SliceAsm<FM::STRIDED> sl;
+            sl.load(p.xq, p.xq2, p.xd, p.xs, uc);
+#pragma unroll
+            for (int i = 0; i < NBUF - 1; ++i) hb[i].template load<64>(rm, r + i * G, u, U, r);
+            sl.template wait<HW>();
+            sl.unpack(x[0]);
+        }
+        const LaneConst lc = lane_const<F, 64, 1>(u, x);
+        bool more = true;
+        while (more) {
+#pragma unroll
+            for (int i = 0; i < NBUF; ++i) {
+                if (r >= p.n_out) {  // workgroup-uniform
+                    more = false;
+                    break;
+                }
+                hb[(i + NBUF - 1) % NBUF].template load<64>(rm, r + (NBUF - 1) * G, u, U, r);
+                hb[i].template wait<HW>();
+                const float v = unit_dot1<F, true>(hb[i].raw[0], uc, tab, x[0], lc, 0);
+                const float ws = team_sum<64>(u < U ? v : 0.f);
+                res = lane == k ? ws : res;
+                r += G;
+                if (++k == 64) {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    NMQ_MVK_FLUSH();
+                }
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the surplus reads of the last steps
+        if (k > 0) NMQ_MVK_FLUSH();
+        return;
+    }
+    Mv1Step<F, 64, 1, 1> buf[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i) buf[i].load(rm, r + i * G, u, U, r);
     const LaneConst lc = lane_const<F, 64, 1>(u, x);
-    const u64* tab = nullptr;
-    float res = 0.f;
-    int k = 0, first = r;
     for (;;) {
 #pragma unroll
         for (int i = 0; i < NBUF; ++i) {
@@ -1670,32 +1835,29 @@ __global__ __launch_bounds__(256) void mvk_kernel(MvParams p) {
                 ++k;
                 r += G;
             }
-            if (k == 64 || (!more && k > 0)) {  // flush a batch of rows
-                part[w][lane] = res;
-                lds_barrier();
-                if (threadIdx.x < (unsigned)k) {
-                    float sum = 0.f;
-#pragma unroll
-                    for (int q = 0; q < KS; ++q) sum += part[q][threadIdx.x];
-                    *gpw<float>(rm.out(first + (int)threadIdx.x * G)) = sum;
-                }
-                lds_barrier();
-                k = 0;
-                first = r;
-            }
+            if (k == 64 || (!more && k > 0)) NMQ_MVK_FLUSH();  // a batch of rows
             if (!more) return;
         }
     }
+#undef NMQ_MVK_FLUSH
 }
 
-template <int F, bool EXT>
+template <int F, bool EXT, bool HR, int NBUF = 3>
 inline MvKernel pick_mvk_e(int ks) {
-    return ks == 2 ? mvk_kernel<F, 2, 3, EXT> : (ks == 3 ? mvk_kernel<F, 3, 3, EXT> : mvk_kernel<F, 4, 3, EXT>);
+    return ks == 2 ? mvk_kernel<F, 2, NBUF, EXT, HR>
+                   : (ks == 3 ? mvk_kernel<F, 3, NBUF, EXT, HR> : mvk_kernel<F, 4, NBUF, EXT, HR>);
 }
+// Hand-issued reads only without segments: the first GPU run of the segment variant with them
+// (nmq_mv_multi over long Q6_K rows) faulted, and its cause is not known; the segment variant keeps the
+// compiler-scheduled reads.
 template <int F>
-inline MvKernel pick_mvk(int ks, bool ext) {
+inline MvKernel pick_mvk(int ks, bool ext, bool hr) {
     if constexpr (F == NMQ_IQ2_XXS) return nullptr;
-    else return ext ? pick_mvk_e<F, true>(ks) : pick_mvk_e<F, false>(ks);
+    else if constexpr (mvk_hand(F))
+        return ext ? pick_mvk_e<F, true, false>(ks)
+                   : (hr ? (tune(TUNE_MVK_NBUF, 3) == 4 ? pick_mvk_e<F, false, true, 4>(ks) : pick_mvk_e<F, false, true>(ks))
+                         : pick_mvk_e<F, false, false>(ks));
+    else return ext ? pick_mvk_e<F, true, false>(ks) : pick_mvk_e<F, false, false>(ks);
 }
 
 // ---- 2..4 tokens, long rows (Q6_K: the layer's down projection) ---------------------------------------
@@ -2015,11 +2177,18 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         const int U = (p.n_in + 63) / 64;
         if (nc == 1 && U > 128 && U <= 256 && p.ids == nullptr && p.xv == nullptr && tune(TUNE_MVK, 1) != 0) {
             const int ks = (U + 63) / 64;
-            int64_t g = (int64_t)tune(TUNE_MVK_WPC, 8) * di.cus / ks;
+            // Hand-issued reads (no segments, Q4_K / TQ2_0 / Q6_K): whole workgroups of about 4 waves per CU
+            // (Q6_K 4096x14336, KS = 4: one workgroup per CU 11.2 us, against 12.7 at 8 waves per CU, 13.4 at
+            // 3 and 16.0 at 5, where the workgroups do not divide evenly over the CUs, and 17.3 at 2); the
+            // compiler-scheduled reads: 8 waves per CU (12.9 us).
+            const bool hr = mvk_hand(F) && p.n_seg == 0 && tune(TUNE_MVK_HR, 1) != 0;
+            const int wpc = tune(TUNE_MVK_WPC, 0);
+            int64_t g = wpc > 0 ? (int64_t)wpc * di.cus / ks
+                                : (hr ? (int64_t)di.cus * (ks >= 4 ? 1 : 4 / ks) : (int64_t)8 * di.cus / ks);
             if (g < 1) g = 1;
             if (g > p.n_out) g = p.n_out;
             p.nt = 64 * ks;
-            hipLaunchKernelGGL(pick_mvk<F>(ks, p.n_seg > 0), dim3((unsigned)g), dim3(p.nt), 0, stream, p);
+            hipLaunchKernelGGL(pick_mvk<F>(ks, p.n_seg > 0, hr), dim3((unsigned)g), dim3(p.nt), 0, stream, p);
             return (int)hipGetLastError();
         }
     }

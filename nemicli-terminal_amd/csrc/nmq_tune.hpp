@@ -42,6 +42,8 @@ enum Tune : int {
     TUNE_MVD_TPW,     // its row tiles per workgroup
     TUNE_MVD_KS,      // its slices of the row
     TUNE_MV1_T,       // lanes per row of the persistent one-token kernel (16, 32, 64; 0: by row length)
+    TUNE_MVK_HR,      // 0: compiler-scheduled reads in the K-split long-row kernel
+    TUNE_MVK_NBUF,    // its row buffers with hand-issued reads (3, 4)
     TUNE_COUNT
 };
 
@@ -50,7 +52,7 @@ inline const char* const kTuneNames[TUNE_COUNT] = {
     "MV1",      "MV1_MAXNIT", "MV1_RW",  "MV1_NBUF", "MV1_WPC", "MV1_W",   "MV1_MODE", "MV1_HR",
     "MVL",      "MVL_WPC",    "MVL_W",   "MVC_WGPC", "MVC_RW",  "MVC_ROWS", "MVT_MAX", "MVT_WPC",
     "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G",    "MVK",     "MVK_WPC",
-    "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS",   "MV1_T"};
+    "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS",   "MV1_T",    "MVK_HR",   "MVK_NBUF"};
 
 constexpr int TUNE_UNSET = INT_MIN;
 

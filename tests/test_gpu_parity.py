@@ -131,14 +131,17 @@ def test_mv_one_token(nmq, oracle, fmt, shape):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("n_in", [8448, 10240, 14336, 16384])
-@pytest.mark.parametrize("kernel", ["ksplit", "longrow", "longrow_pipelined"])
+@pytest.mark.parametrize("kernel", ["ksplit", "ksplit_compiler_reads", "longrow", "longrow_pipelined"])
 def test_mv_one_token_long_rows(nmq, oracle, tune, fmt, n_in, kernel):
     """One token on rows of 132..256 units of 64 values (the Llama down projection has 224): the K-split
-    kernel (3 or 4 waves per row, input slices from global memory; IQ2_XXS always takes the long-row
-    kernel), and the long-row kernel with one row per wave and (with fewer resident waves than rows) the
-    variant that cycles two row buffers."""
+    kernel (3 or 4 waves per row, input slices from global memory; reads issued by hand for Q4_K, TQ2_0,
+    Q6_K, and the compiler-scheduled variant; IQ2_XXS always takes the long-row kernel), and the long-row
+    kernel with one row per wave and (with fewer resident waves than rows) the variant that cycles two row
+    buffers."""
     n_out = 300
-    if kernel != "ksplit":
+    if kernel == "ksplit_compiler_reads":
+        tune(MVK_HR=0)
+    if kernel.startswith("longrow"):
         tune(MVK=0)
     if kernel == "longrow_pipelined":
         tune(MVL_WPC=1)   # 1 wave per CU: fewer waves than rows
@@ -150,6 +153,30 @@ def test_mv_one_token_long_rows(nmq, oracle, tune, fmt, n_in, kernel):
     y = torch.full((1, n_out), float("nan"), device="cuda")
     from ggufengine_amd.gguf_types import TYPE_ID
     raw_d = dev(raw)  # kept alive until the launch has run
+    nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+                               e.xs.data_ptr(), y.data_ptr(), n_out, n_in, 1, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q6_K", "TQ2_0", "Q8_0"])
+@pytest.mark.parametrize("hr", [1, 0, 4])
+def test_mv_one_token_long_rows_batches(nmq, oracle, tune, fmt, hr):
+    """The K-split kernel with more than 64 rows per workgroup (1 resident wave per CU: 85 workgroups of 3
+    waves for 5600 rows of 8448 values, 65-66 rows each), so that its row batches are added and written in
+    the middle of the row loop as well as at the end, with hand-issued reads (hr = 1; Q8_0 has none) and
+    compiler-scheduled ones."""
+    n_out, n_in = 5600, 8448
+    tune(MVK_WPC=1)
+    tune(MVK_HR=1 if hr else 0)
+    tune(MVK_NBUF=4 if hr == 4 else 3)   # hr = 4: hand-issued reads with 4 row buffers
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=83)
+    x = np.random.default_rng(84).standard_normal((1, n_in)).astype(np.float32)
+    say("mv long rows batches", fmt, hr)
+    e = quant_dev(dev(x))
+    y = torch.full((1, n_out), float("nan"), device="cuda")
+    from ggufengine_amd.gguf_types import TYPE_ID
+    raw_d = dev(raw)
     nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
                                e.xs.data_ptr(), y.data_ptr(), n_out, n_in, 1, nmq.stream_ptr()))
     torch.cuda.synchronize()

@@ -77,7 +77,9 @@ def hazards(asm: str, name: str):
     return found
 
 
-SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip")
+SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip", "nmq_mv_q6_k.hip")
+# the K-split long-row kernel with hand-issued reads (mvk_kernel<..., HR = true>): Q4_K, TQ2_0, Q6_K
+KSPLIT_KERNEL = re.compile(r"^(_ZN3nmq10mvk_kernel\w*Lb1EEEvNS_8MvParamsE):", re.M)
 
 
 @pytest.fixture(scope="module")
@@ -96,7 +98,7 @@ def asm(tmp_path_factory):
     return {src: (out / (src + ".s")).read_text() for src in SOURCES}
 
 
-@pytest.mark.parametrize("src", SOURCES)
+@pytest.mark.parametrize("src", SOURCES[:3])
 def test_hand_read_kernels_exist(asm, src):
     names = HAND_KERNEL.findall(asm[src])
     one = [n for n in names if "mv1_kernel" in n]
@@ -109,8 +111,15 @@ def test_hand_read_kernels_exist(asm, src):
 
 @pytest.mark.parametrize("src", SOURCES)
 def test_no_access_to_registers_of_outstanding_reads(asm, src):
-    bad = [h for n in HAND_KERNEL.findall(asm[src]) for h in hazards(asm[src], n)]
+    bad = [h for n in HAND_KERNEL.findall(asm[src]) + KSPLIT_KERNEL.findall(asm[src]) for h in hazards(asm[src], n)]
     assert not bad, bad[:5]
+
+
+@pytest.mark.parametrize("src", ["nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_q6_k.hip"])
+def test_ksplit_hand_read_kernels_exist(asm, src):
+    # KS = 2, 3, 4 slices x 3 or 4 row buffers, without segments (the segment variant keeps
+    # compiler-scheduled reads)
+    assert len(KSPLIT_KERNEL.findall(asm[src])) == 6, KSPLIT_KERNEL.findall(asm[src])
 
 
 def test_checker_finds_a_planted_read(asm):
@@ -168,3 +177,18 @@ def test_dense_read_kernels_keep_m0_to_themselves(asm):
             if any("m0" in o for o in ops):
                 assert len(ops) == 2 and ops[0].startswith("s_mov_b32 m0") and \
                     ops[1].startswith("global_load_lds_dwordx4"), ops
+
+
+@pytest.mark.parametrize("src", SOURCES)
+def test_hand_read_kernels_use_no_scratch(asm, src):
+    """Kernels with hand-issued reads keep everything in registers: a value the compiler parks in scratch
+    memory comes back through reads and waits of its own among the hand-issued ones."""
+    text = asm[src]
+    names = HAND_KERNEL.findall(text) + KSPLIT_KERNEL.findall(text) + DMA_KERNEL.findall(text)
+    bad = []
+    for n in names:
+        body = text[text.index(n + ":"):]
+        body = body[:body.index("s_endpgm")]
+        if re.search(r"\bscratch_", body):
+            bad.append(n)
+    assert not bad, bad

@@ -264,6 +264,33 @@ int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64
                  int64_t work_bytes, void* stream);
 
 /*
+ * The gate and up projections of an expert layer with the gated activation in the same launch: for slot
+ * s = t*k + j (t < L) and row r < n_out,
+ *   g = W_gate_{ids[s]}[r,:] . x_t,   u = W_up_{ids[s]}[r,:] . x_t,   a[s][r] = bf16(silu(g) * u),
+ * g and u exactly as nmq_mv_experts_x forms them (x_group = k; x_mode NMQ_X_BF16, NMQ_X_F32 or
+ * NMQ_X_F32_BF16), silu(g) * u as nmq_silu_mul_quant forms it, and writes the two-stage input of a
+ * (L*k x n_out values, slot-major) to xq, xq2 (16-byte aligned), xd, xs -- bit for bit what
+ * nmq_mv_experts_x followed by nmq_silu_mul_quant writes.  Each workgroup computes 32 rows of both
+ * projections of one slot and quantises them as one group, so g and u are never written.  Requires
+ * n_out % 32 == 0 and rows of at most 4096 values (NMQ_ERR_SHAPE otherwise); L*k <= 32767.
+ * Replaces the gate and up calls of Experten.__call__ and the activation between them and the down call
+ * (models/moe.py:270-276 and 278-285: the gate and up matvecs, then Experten._gu, 252-255).
+ */
+int nmq_moe_gate_up(int fmt, const void* w_gate, const void* w_up, const int64_t* ids, int L, int k,
+                    int64_t per_expert, const void* x, int x_mode, int8_t* xq, int8_t* xq2, float* xd, float* xs,
+                    int n_out, int n_in, void* stream);
+
+/*
+ * nmq_moe_down on the two-stage input (slot s = t*k + j reads row s of xq, xq2, xd, xs: what
+ * nmq_moe_gate_up writes), each slot's product exactly as nmq_mv_experts forms it with x_group = 1;
+ * workspace, combine and errors as nmq_moe_down (nmq_moe_down_work_bytes sizes `work` for both).
+ * Replaces the down call of Experten.__call__ plus its weighted combine (models/moe.py:276-277, 284-285).
+ */
+int nmq_moe_down_q8(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const int8_t* xq,
+                    const int8_t* xq2, const float* xd, const float* xs, const float* wts, float* out, int n_out,
+                    int n_in, void* work, int64_t work_bytes, void* stream);
+
+/*
  * nmq_moe_down without a workspace argument, for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid allocation); no counterpart in the reference.
  * The two-launch form keeps its slot results in a device array inside the library, one per GPU, of

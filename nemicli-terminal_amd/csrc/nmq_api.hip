@@ -40,28 +40,6 @@ DeviceInfo device_info() {
 // Input modes: 0 bf16; 1 fp32; 2 fp32 rounded to bf16 first (what the reference's cudakern entry
 // points do to their input, cudakern.py:764); 3 silu(g) * u in fp32 (g = x, u second operand), then
 // rounded to bf16 (the gated activation of a MoE expert fed to the down projection as bf16).
-// Two-stage input of the value v held by this lane; value index i (i % 32 == lane % 32).  All 32
-// lanes of the lane's half-wave take part.
-__device__ __forceinline__ void quant32_store(float v, int64_t i, int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
-                                              float* __restrict__ xd, float* __restrict__ xs) {
-    const float a = half_max(fabsf(v));
-    const float d = a / 127.0f;
-    int q = 0, q2 = 0;
-    if (d > 0.0f) {
-        q = (int)rintf(v / d);
-        const float r = fmaf(-(float)q, d, v);
-        q2 = (int)rintf(r / (d * FEIN));
-        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
-    }
-    const float s = half_sum_xor(v);
-    xq[i] = (int8_t)q;
-    xq2[i] = (int8_t)q2;
-    if ((threadIdx.x & 31) == 0) {
-        xd[i >> 5] = d;
-        xs[i >> 5] = s;
-    }
-}
-
 template <int MODE>
 __global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ x, const float* __restrict__ u2,
                                                         int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
@@ -76,7 +54,7 @@ __global__ __launch_bounds__(256) void quant_q8_kernel(const void* __restrict__ 
         v = __uint_as_float((u32)((const u16*)x)[i] << 16);
     } else if constexpr (MODE == 3) {
         const float g = ((const float*)x)[i];
-        v = round_bf16(g / (1.0f + expf(-g)) * u2[i]);
+        v = silu_mul_bf16(g, u2[i]);
     } else {
         v = ((const float*)x)[i];
         if constexpr (MODE == 2) v = round_bf16(v);
@@ -468,6 +446,27 @@ static int launch_moe_down_any(int fmt, const MvParams& p, const Combine& c, int
         case NMQ_Q6_K: return launch_moe_down<NMQ_Q6_K>(p, c, L, s);
         case NMQ_IQ2_XXS: return launch_moe_down<NMQ_IQ2_XXS>(p, c, L, s);
         case NMQ_TQ2_0: return launch_moe_down<NMQ_TQ2_0>(p, c, L, s);
+        default: return NMQ_ERR_FORMAT;
+    }
+}
+
+template <int F>
+int launch_moe_gu(MvParams p, QuantOut o, hipStream_t stream);
+extern template int launch_moe_gu<NMQ_Q4_0>(MvParams, QuantOut, hipStream_t);
+extern template int launch_moe_gu<NMQ_Q8_0>(MvParams, QuantOut, hipStream_t);
+extern template int launch_moe_gu<NMQ_Q4_K>(MvParams, QuantOut, hipStream_t);
+extern template int launch_moe_gu<NMQ_Q6_K>(MvParams, QuantOut, hipStream_t);
+extern template int launch_moe_gu<NMQ_IQ2_XXS>(MvParams, QuantOut, hipStream_t);
+extern template int launch_moe_gu<NMQ_TQ2_0>(MvParams, QuantOut, hipStream_t);
+
+static int launch_moe_gu_any(int fmt, const MvParams& p, const QuantOut& o, hipStream_t s) {
+    switch (fmt) {
+        case NMQ_Q4_0: return launch_moe_gu<NMQ_Q4_0>(p, o, s);
+        case NMQ_Q8_0: return launch_moe_gu<NMQ_Q8_0>(p, o, s);
+        case NMQ_Q4_K: return launch_moe_gu<NMQ_Q4_K>(p, o, s);
+        case NMQ_Q6_K: return launch_moe_gu<NMQ_Q6_K>(p, o, s);
+        case NMQ_IQ2_XXS: return launch_moe_gu<NMQ_IQ2_XXS>(p, o, s);
+        case NMQ_TQ2_0: return launch_moe_gu<NMQ_TQ2_0>(p, o, s);
         default: return NMQ_ERR_FORMAT;
     }
 }
@@ -927,13 +926,18 @@ static int64_t moe_work_bytes(int L, int k, int n_out, int n_in) {
     return plan_moe_down(n_out, n_in, L, k, device_info()).ok ? 0 : (int64_t)L * k * n_out * 4;
 }
 
+static int moe_check_slots(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert,
+                           const float* wts, int n_out, int n_in) {
+    if (!ids || !wts || !aligned(wts, 4) || L < 1 || k < 1 || (int64_t)L * k > 65535) return NMQ_ERR_ARG;
+    return check_experts(fmt, w, L * k, per_expert, 1, n_out, n_in);
+}
+
 static int moe_check(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
                      int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in) {
     int e = check_w(fmt, w, out, n_out, n_in);
     if (e) return e;
     if ((e = check_values(x, x_mode, x2, n_in))) return e;
-    if (!ids || !wts || !aligned(wts, 4) || L < 1 || k < 1 || (int64_t)L * k > 65535) return NMQ_ERR_ARG;
-    return check_experts(fmt, w, L * k, per_expert, 1, n_out, n_in);
+    return moe_check_slots(fmt, w, ids, L, k, per_expert, wts, n_out, n_in);
 }
 
 // Device memory of nmq_moe_down_static: the slot results of the two-launch form (one copy per GPU the
@@ -960,10 +964,25 @@ static int scratch_address(void** at) {
     return NMQ_OK;
 }
 
-// The checked call on a workspace of at least moe_work_bytes(...) bytes at `work`.
-static int moe_launch(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
-                      int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, float* work,
-                      hipStream_t s) {
+// The checked call on a workspace of at least moe_work_bytes(...) bytes at `work`; p holds the weights, the
+// expert table and the input (values or the two-stage input), whose slot rows are consecutive (x_group 1).
+static int moe_launch(int fmt, MvParams p, int L, int k, const float* wts, float* out, float* work, hipStream_t s) {
+    p.x_group = 1;
+    p.n_ids = L * k;
+    const Combine c{wts, out, k, 0};
+    const int e = launch_moe_down_any(fmt, p, c, L, s);
+    if (e != NMQ_ERR_SHAPE) return e;
+    p.y = work;
+    const int e2 = launch_any(fmt, p, 1, L * k, s);
+    if (e2) return e2;
+    const int64_t blocks = ((int64_t)L * p.n_out + 255) / 256;
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, wts, L, k,
+                       p.n_out, out);
+    return (int)hipGetLastError();
+}
+
+static MvParams moe_values(const void* w, const int64_t* ids, int64_t per_expert, const void* x, int x_mode,
+                           const void* x2, int n_out, int n_in) {
     MvParams p{};
     p.w = (const u8*)w;
     p.ids = ids;
@@ -973,18 +992,7 @@ static int moe_launch(int fmt, const void* w, const int64_t* ids, int L, int k, 
     p.x_mode = x_mode;
     p.n_out = n_out;
     p.n_in = n_in;
-    p.x_group = 1;
-    p.n_ids = L * k;
-    const Combine c{wts, out, k, 0};
-    const int e = launch_moe_down_any(fmt, p, c, L, s);
-    if (e != NMQ_ERR_SHAPE) return e;
-    p.y = work;
-    const int e2 = launch_any(fmt, p, 1, L * k, s);
-    if (e2) return e2;
-    const int64_t blocks = ((int64_t)L * n_out + 255) / 256;
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)blocks), dim3(256), 0, s, (const float*)work, wts, L, k,
-                       n_out, out);
-    return (int)hipGetLastError();
+    return p;
 }
 
 extern "C" {
@@ -1005,8 +1013,56 @@ int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64
     const int64_t need = moe_work_bytes(L, k, n_out, n_in);
     if (need > 0 && (!work || !aligned(work, 256))) return NMQ_ERR_ARG;
     if (work_bytes < need) return NMQ_ERR_SHAPE;
-    return moe_launch(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in, (float*)work,
-                      (hipStream_t)stream);
+    return moe_launch(fmt, moe_values(w, ids, per_expert, x, x_mode, x2, n_out, n_in), L, k, wts, out,
+                      (float*)work, (hipStream_t)stream);
+}
+
+int nmq_moe_down_q8(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const int8_t* xq,
+                    const int8_t* xq2, const float* xd, const float* xs, const float* wts, float* out, int n_out,
+                    int n_in, void* work, int64_t work_bytes, void* stream) {
+    int e = check_mv(fmt, w, xq, xq2, xd, xs, out, n_out, n_in);
+    if (e) return e;
+    if ((e = moe_check_slots(fmt, w, ids, L, k, per_expert, wts, n_out, n_in))) return e;
+    const int64_t need = moe_work_bytes(L, k, n_out, n_in);
+    if (need > 0 && (!work || !aligned(work, 256))) return NMQ_ERR_ARG;
+    if (work_bytes < need) return NMQ_ERR_SHAPE;
+    MvParams p{};
+    p.w = (const u8*)w;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xq = xq;
+    p.xq2 = xq2;
+    p.xd = xd;
+    p.xs = xs;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    return moe_launch(fmt, p, L, k, wts, out, (float*)work, (hipStream_t)stream);
+}
+
+int nmq_moe_gate_up(int fmt, const void* w_gate, const void* w_up, const int64_t* ids, int L, int k,
+                    int64_t per_expert, const void* x, int x_mode, int8_t* xq, int8_t* xq2, float* xd, float* xs,
+                    int n_out, int n_in, void* stream) {
+    int e = check_mv(fmt, w_gate, xq, xq2, xd, xs, xd, n_out, n_in);
+    if (e) return e;
+    if ((e = check_w(fmt, w_up, xd, n_out, n_in))) return e;
+    if (x_mode == NMQ_X_SILU_MUL_BF16) return NMQ_ERR_ARG;
+    if ((e = check_values(x, x_mode, nullptr, n_in))) return e;
+    if (!ids || L < 1 || k < 1 || (int64_t)L * k > 32767) return NMQ_ERR_ARG;
+    if (n_out % 32) return NMQ_ERR_SHAPE;
+    if ((e = check_experts(fmt, w_gate, L * k, per_expert, k, n_out, n_in))) return e;
+    if ((e = check_experts(fmt, w_up, L * k, per_expert, k, n_out, n_in))) return e;
+    MvParams p{};
+    p.w = (const u8*)w_gate;
+    p.w2 = (const u8*)w_up;
+    p.ids = ids;
+    p.per_expert = per_expert;
+    p.xv = x;
+    p.x_mode = x_mode;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    p.x_group = k;
+    p.n_ids = L * k;
+    return launch_moe_gu_any(fmt, p, QuantOut{xq, xq2, xd, xs}, (hipStream_t)stream);
 }
 
 int nmq_moe_down_static(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
@@ -1017,8 +1073,8 @@ int nmq_moe_down_static(int fmt, const void* w, const int64_t* ids, int L, int k
     if (need > NMQ_MOE_SCRATCH_BYTES) return NMQ_ERR_SHAPE;
     void* work = nullptr;
     if ((e = scratch_address(&work))) return e;
-    return moe_launch(fmt, w, ids, L, k, per_expert, x, x_mode, x2, wts, out, n_out, n_in, (float*)work,
-                      (hipStream_t)stream);
+    return moe_launch(fmt, moe_values(w, ids, per_expert, x, x_mode, x2, n_out, n_in), L, k, wts, out,
+                      (float*)work, (hipStream_t)stream);
 }
 
 int nmq_block_sums(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, int32_t* s1, int32_t* s2, int n_out,

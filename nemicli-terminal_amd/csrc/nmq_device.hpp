@@ -83,6 +83,35 @@ __device__ __forceinline__ float round_bf16(float f) {
     return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
 }
 
+// The gated activation of an expert MLP as its down projection takes it: bf16(silu(g) * u), silu(g) =
+// g / (1 + exp(-g)) with an IEEE division.  Every kernel that forms it calls this one expression, so that
+// they agree bit for bit.
+__device__ __forceinline__ float silu_mul_bf16(float g, float u) { return round_bf16(g / (1.0f + expf(-g)) * u); }
+
+// Two-stage int8 input (reference mmvq.py:59-83) of the value v held by this lane, value index i
+// (i % 32 == lane % 32): d = max|v| / 127 over the lane's 32-lane half, q = rint(v / d), q2 = the
+// rounded residual in units of d / 254, and the group's sum (half_max / half_sum_xor).  All 32 lanes
+// of the half-wave take part.
+__device__ __forceinline__ void quant32_store(float v, int64_t i, int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
+                                              float* __restrict__ xd, float* __restrict__ xs) {
+    const float a = half_max(fabsf(v));
+    const float d = a / 127.0f;
+    int q = 0, q2 = 0;
+    if (d > 0.0f) {
+        q = (int)rintf(v / d);
+        const float r = fmaf(-(float)q, d, v);
+        q2 = (int)rintf(r / (d * FEIN));
+        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+    }
+    const float s = half_sum_xor(v);
+    xq[i] = (int8_t)q;
+    xq2[i] = (int8_t)q2;
+    if ((threadIdx.x & 31) == 0) {
+        xd[i >> 5] = d;
+        xs[i >> 5] = s;
+    }
+}
+
 __device__ __forceinline__ float h2f(u32 bits16) {
     return (float)__builtin_bit_cast(_Float16, (u16)(bits16 & 0xffffu));
 }

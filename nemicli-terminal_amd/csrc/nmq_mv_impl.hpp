@@ -354,7 +354,7 @@ __device__ __forceinline__ void stagev_store(const VRound& r, int rnd, u8* lds, 
     for (int e = 0; e < 4; ++e) {
         float t = r.v[e];
         if (mode == NMQ_X_F32_BF16) t = round_bf16(t);
-        else if (mode == NMQ_X_SILU_MUL_BF16) t = round_bf16(t / (1.0f + expf(-t)) * r.u[e]);
+        else if (mode == NMQ_X_SILU_MUL_BF16) t = silu_mul_bf16(t, r.u[e]);
         v[e] = in ? t : 0.f;
     }
     float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
@@ -1431,6 +1431,58 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
     }
 }
 
+// The gate and up projections of an expert layer with the gated activation in the same workgroup (MoE):
+// workgroup (x, s) computes rows [32x, 32x + 32) of slot s's gate projection (instance s: expert ids[s] of
+// tensor w) on waves 0 .. WH - 1 and of its up projection (instance n_ids + s, tensor w2) on waves
+// WH .. 2WH - 1, each wave P*RW rows with the chunk kernel's unit products and team sums (so every sum
+// equals that row of the gathered launch bit for bit), keeps the 64 sums in LDS, and then writes the
+// two-stage input of a[s][r] = silu_mul_bf16(g[r], u[r]) for its 32 rows -- one group of the down
+// projection's input.  The gate and up outputs never leave the workgroup and the activation needs no
+// launch of its own.  Slot s reads input row s / x_group (the token).
+struct QuantOut {
+    int8_t* xq;
+    int8_t* xq2;
+    float* xd;
+    float* xs;
+};
+
+template <int F, int T, int RW>
+__global__ __launch_bounds__(1024) void moe_gu_kernel(MvParams p, QuantOut o) {
+    args_early<true>(p);
+    using FM = Fmt<F>;
+    constexpr int P = 64 / T;
+    constexpr int WH = 32 / (P * RW);  // waves per projection
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    __shared__ float res[64];  // gate sums, then up sums
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int team = lane / T, lt = lane % T;
+    const int s = blockIdx.y;
+    const bool up = wave >= WH;
+    const int lr = ((up ? wave - WH : wave) * P + team) * RW;  // the team's first row in the group
+    const int r0 = blockIdx.x * 32 + lr;
+    int64_t xrow;
+    const u8* wbase = instance_weights(p, up ? p.n_ids + s : s, xrow);
+    const RowMap rm = row_map<false>(p, wbase, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    Mv1Step<F, T, RW, 1> a;
+    stage1_around<F, true, 1>(lds, tab, p, xrow, [&] { a.load(rm, r0, lt, U, r0); });
+    XSlice x[1];
+    read_slice<FM::STRIDED>(lds, p.ktp, min(lt, U - 1), x[0]);
+    const LaneConst lc = lane_const<F, T, 1>(lt, x);
+    float acc[RW];
+    mv1_dots<F, T, RW, 1>(a, x, lt, U, tab, lc, acc);
+    if (lt == 0) {
+#pragma unroll
+        for (int rr = 0; rr < RW; ++rr) res[(up ? 32 : 0) + lr + rr] = acc[rr];
+    }
+    lds_barrier();
+    if (wave == 0 && lane < 32) {
+        const float v = silu_mul_bf16(res[lane], res[32 + lane]);
+        quant32_store(v, (int64_t)s * p.n_out + blockIdx.x * 32 + lane, o.xq, o.xq2, o.xd, o.xs);
+    }
+}
+
 // ---- host side --------------------------------------------------------------------------------
 
 struct DeviceInfo {
@@ -2302,6 +2354,32 @@ int launch_moe_down(MvParams p, Combine c, int L, hipStream_t stream) {
     const MoeDownKernel kern = sh.T == 16 ? pick_moe_down_rw<F, 16>(sh.rw)
                              : sh.T == 32 ? pick_moe_down_rw<F, 32>(sh.rw) : pick_moe_down_rw<F, 64>(sh.rw);
     hipLaunchKernelGGL(kern, dim3((unsigned)sh.grid_x, (unsigned)L), dim3(p.nt), sh.lds, stream, p, c);
+    return (int)hipGetLastError();
+}
+
+
+// ---- gate and up projections with the gated activation (moe_gu_kernel) ----------------------------------
+typedef void (*MoeGuKernel)(MvParams, QuantOut);
+
+// One launch over the p.n_ids slots (value input).  T lanes per row with one unit each (rows of up to
+// 4096 values) and RW rows per team, so that 32 rows of a projection take 4 (T = 16) or 8 waves;
+// NMQ_ERR_SHAPE for longer rows or n_out not a multiple of 32 (a group of the output is one workgroup's).
+template <int F>
+int launch_moe_gu(MvParams p, QuantOut o, hipStream_t stream) {
+    using FM = Fmt<F>;
+    const DeviceInfo di = device_info();
+    const int U = (p.n_in + 63) / 64;
+    const int T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
+    if (U > T || p.n_out % 32 || p.n_ids < 1 || p.n_ids > 65535) return NMQ_ERR_SHAPE;
+    const int P = 64 / T, rw = T == 64 ? 4 : 2;
+    p.nblk = p.n_in / FM::BV;
+    p.row_bytes = (int64_t)p.nblk * FM::BB;
+    p.ktp = (p.n_in + 127) / 128 * 128;
+    p.nt = 64 * (2 * 32 / (P * rw));
+    const size_t lds = (size_t)p.ktp * 9 / 4;
+    if (lds > (size_t)di.lds_max || p.ktp / 4 > 2 * p.nt) return NMQ_ERR_SHAPE;
+    const MoeGuKernel k = T == 16 ? moe_gu_kernel<F, 16, 2> : (T == 32 ? moe_gu_kernel<F, 32, 2> : moe_gu_kernel<F, 64, 4>);
+    hipLaunchKernelGGL(k, dim3((unsigned)(p.n_out / 32), (unsigned)p.n_ids), dim3(p.nt), lds, stream, p, o);
     return (int)hipGetLastError();
 }
 

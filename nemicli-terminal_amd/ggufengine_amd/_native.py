@@ -67,6 +67,10 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_moe_down.restype = i
     L.nmq_moe_down_static.argtypes = [i, p, p, i, i, i64, p, i, p, p, p, i, i, p]
     L.nmq_moe_down_static.restype = i
+    L.nmq_moe_gate_up.argtypes = [i, p, p, p, i, i, i64, p, i, p, p, p, p, i, i, p]
+    L.nmq_moe_gate_up.restype = i
+    L.nmq_moe_down_q8.argtypes = [i, p, p, i, i, i64, p, p, p, p, p, p, i, i, p, i64, p]
+    L.nmq_moe_down_q8.restype = i
     L.nmq_stream_read.argtypes, L.nmq_stream_read.restype = [p, i64, p, i, i, i, p], i
     L.nmq_set_tuning.argtypes, L.nmq_set_tuning.restype = [ctypes.c_char_p, i], i
     L.nmq_get_tuning.argtypes, L.nmq_get_tuning.restype = [ctypes.c_char_p, p], i

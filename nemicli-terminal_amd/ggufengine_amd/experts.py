@@ -31,6 +31,9 @@ from . import _native, cudakern, hostmem
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
 from .mmvq import WERTE_BIS, Eingang, _starten, _werte, eingang_bf16
 
+# rows (values) up to which nmq_moe_gate_up takes the gate and up projections: one 64-value unit per lane
+GU_BIS = 4096
+
 
 class PackedExperts:
     """All experts of one tensor (n_exp, n_out, n_in) in their GGUF block bytes, multiplied on the device
@@ -283,11 +286,14 @@ class Experten:
         return (g.ggml_type == u.ggml_type and g.raw.shape == u.raw.shape and (g.adressen is None) == (u.adressen is None))
 
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights.
-        Two launches: gate and up together on every (token, slot), each token's input rounded to bf16
-        and quantised in the launch; down on every slot, its input bf16(silu(gate) * up) formed and
-        quantised in the launch, with the weighted combine in the same launch (nmq_moe_down).  (Rows longer than WERTE_BIS values, or a gate
-        and up of different layout: the input quantisations as launches of their own.)"""
+        """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights (reference
+        models/moe.py:264-285).  Two launches: gate and up of every (token, slot) with each token's input
+        rounded to bf16 and quantised in the launch, and the activation bf16(silu(gate) * up) formed and
+        quantised in the same workgroups (nmq_moe_gate_up: rows of up to GU_BIS values, FF a multiple of
+        32); then down on that two-stage input with the weighted combine in the same launch
+        (nmq_moe_down_q8).  Longer rows: gate and up into fp32 outputs, down forming the activation in its
+        staging (nmq_moe_down).  (Rows longer than WERTE_BIS values, or a gate and up of different layout:
+        the input quantisations as launches of their own.)"""
         L_, E = x.shape
         k = idx.shape[1]
         dev = x.device
@@ -299,14 +305,23 @@ class Experten:
         FF = self.gate.n_out
         xc = x.contiguous()
         flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
-        gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
         (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
-        _starten("mv_experts2", L.nmq_mv_experts_x, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
-                 flat.data_ptr(), n, per, xc.data_ptr(), _native.X_F32_BF16, None, k, gu.data_ptr(), FF, E, st)
         wd, perd = self.down._quelle(dev)
         out = torch.empty(L_, E, dtype=torch.float32, device=dev)
         wf = w.to(dev, torch.float32).contiguous()
         work = self._arbeitsplatz(L_, k, dev)
+        if E <= GU_BIS and FF % 32 == 0:
+            a = Eingang(n=n * FF, device=dev)
+            _starten("moe_gate_up", L.nmq_moe_gate_up, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
+                     flat.data_ptr(), L_, k, per, xc.data_ptr(), _native.X_F32_BF16, a.xq.data_ptr(),
+                     a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), FF, E, st)
+            _starten("moe_down", L.nmq_moe_down_q8, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), L_, k,
+                     perd, a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), wf.data_ptr(),
+                     out.data_ptr(), E, FF, work.data_ptr(), work.numel(), st)
+            return out
+        gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
+        _starten("mv_experts2", L.nmq_mv_experts_x, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
+                 flat.data_ptr(), n, per, xc.data_ptr(), _native.X_F32_BF16, None, k, gu.data_ptr(), FF, E, st)
         _starten("moe_down", L.nmq_moe_down, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), L_, k, perd,
                  gu.data_ptr(), _native.X_SILU_MUL_BF16, gu[n:].data_ptr(), wf.data_ptr(), out.data_ptr(), E, FF,
                  work.data_ptr(), work.numel(), st)

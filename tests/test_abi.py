@@ -202,3 +202,38 @@ def test_moe_down_checks_without_launching(L):
     assert call(work=a + 16, **long) == _native.NMQ_ERR_ARG       # not 256-byte aligned
     assert call(work_bytes=16, **long) == _native.NMQ_ERR_SHAPE   # too small
     assert call(n_in=700) == _native.NMQ_ERR_SHAPE                # not whole blocks
+
+
+def test_moe_gate_up_and_down_q8_check_without_launching(L):
+    """nmq_moe_gate_up and nmq_moe_down_q8 refuse bad arguments before anything is launched."""
+    from ggufengine_amd import _native
+    buf = ctypes.create_string_buffer(1 << 16)
+    a = (ctypes.addressof(buf) + 255) // 256 * 256
+    gu = dict(fmt=12, wg=a, wu=a, ids=a, L=1, k=8, per=768 * 8 * 144, x=a, mode=_native.X_F32_BF16, xq=a, xq2=a,
+              xd=a, xs=a, n_out=768, n_in=2048)
+
+    def gate_up(**kw):
+        v = {**gu, **kw}
+        return L.nmq_moe_gate_up(v["fmt"], v["wg"], v["wu"], v["ids"], v["L"], v["k"], v["per"], v["x"], v["mode"],
+                                 v["xq"], v["xq2"], v["xd"], v["xs"], v["n_out"], v["n_in"], None)
+    assert gate_up(ids=None) == _native.NMQ_ERR_ARG
+    assert gate_up(wu=None) == _native.NMQ_ERR_ARG
+    assert gate_up(xq=a + 1) == _native.NMQ_ERR_ARG                     # two-stage output: 16-byte aligned
+    assert gate_up(mode=_native.X_SILU_MUL_BF16) == _native.NMQ_ERR_ARG  # no second operand taken
+    assert gate_up(L=4096, k=16) == _native.NMQ_ERR_ARG                  # more than 32767 slots
+    assert gate_up(n_out=760, per=760 * 8 * 144) == _native.NMQ_ERR_SHAPE  # groups of 32 rows
+    assert gate_up(per=100) == _native.NMQ_ERR_SHAPE                     # experts overlap
+    assert gate_up(fmt=13) == _native.NMQ_ERR_FORMAT
+    dn = dict(fmt=14, w=a, ids=a, L=1, k=8, per=2048 * 20 * 210, xq=a, xq2=a, xd=a, xs=a, wts=a, out=a, n_out=2048,
+              n_in=5120, work=a, work_bytes=1 << 14)
+
+    def down(**kw):
+        v = {**dn, **kw}
+        return L.nmq_moe_down_q8(v["fmt"], v["w"], v["ids"], v["L"], v["k"], v["per"], v["xq"], v["xq2"], v["xd"],
+                                 v["xs"], v["wts"], v["out"], v["n_out"], v["n_in"], v["work"], v["work_bytes"], None)
+    assert down(ids=None) == _native.NMQ_ERR_ARG
+    assert down(xs=None) == _native.NMQ_ERR_ARG
+    assert down(wts=a + 2) == _native.NMQ_ERR_ARG
+    assert down(work=a + 16) == _native.NMQ_ERR_ARG      # rows too long for one launch: a workspace, 256-aligned
+    assert down(work_bytes=16) == _native.NMQ_ERR_SHAPE  # too small
+    assert down(n_in=5000) == _native.NMQ_ERR_SHAPE      # not whole blocks

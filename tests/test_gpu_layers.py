@@ -690,6 +690,163 @@ def test_band_refuses_a_pass_split_across_a_capture(nmq):
     torch.cuda.synchronize()
 
 
+
+# ---- gate and up with the activation in one launch (nmq_moe_gate_up), down on its two-stage input ----------
+
+def _gate_up_case(fmt, n_exp, FF, E, L, k, seed):
+    from ggufengine_amd.gguf_types import TYPE_ID
+    A = dev(random_blocks(fmt, n_exp * FF * E // BV[fmt], seed=seed))
+    B = dev(random_blocks(fmt, n_exp * FF * E // BV[fmt], seed=seed + 1))
+    rng = np.random.default_rng(seed + 2)
+    ids = torch.from_numpy(rng.integers(0, n_exp, L * k)).cuda()
+    x = dev(rng.standard_normal((L, E)).astype(np.float32))
+    return TYPE_ID[fmt], A, B, A.numel() // n_exp, ids, x, rng
+
+
+def _gate_up_two_launches(nmq, t, A, B, ids, per, x, mode, L, k, FF, E):
+    """nmq_mv_experts_x (gate and up of every slot) followed by nmq_silu_mul_quant."""
+    from ggufengine_amd import mmvq
+    n = L * k
+    gu = torch.full((2 * n, FF), float("nan"), device="cuda")
+    Lb = nmq.lib()
+    nmq.check(Lb.nmq_mv_experts_x(t, A.data_ptr(), B.data_ptr(), ids.data_ptr(), n, per, x.data_ptr(), mode, None, k,
+                                  gu.data_ptr(), FF, E, nmq.stream_ptr()))
+    a = mmvq.Eingang(n=n * FF, device=torch.device("cuda"))
+    nmq.check(Lb.nmq_silu_mul_quant(gu.data_ptr(), gu[n:].data_ptr(), a.xq.data_ptr(), a.xq2.data_ptr(),
+                                    a.xd.data_ptr(), a.xs.data_ptr(), n * FF, nmq.stream_ptr()))
+    return a, gu
+
+
+def _gate_up_fused(nmq, t, A, B, ids, per, x, mode, L, k, FF, E, a=None):
+    from ggufengine_amd import mmvq
+    n = L * k
+    if a is None:
+        a = mmvq.Eingang(n=n * FF, device=torch.device("cuda"))
+        for b in (a.xq, a.xq2):
+            b.fill_(77)
+        for b in (a.xd, a.xs):
+            b.fill_(float("nan"))
+    nmq.check(nmq.lib().nmq_moe_gate_up(t, A.data_ptr(), B.data_ptr(), ids.data_ptr(), L, k, per, x.data_ptr(), mode,
+                                        a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), FF, E,
+                                        nmq.stream_ptr()))
+    return a
+
+
+def _same_input(a, b):
+    return all(torch.equal(getattr(a, f), getattr(b, f)) for f in ("xq", "xq2", "xd", "xs"))
+
+
+# (format, FF rows, E values per row, tokens L, slots k): T = 16, 32 and 64 lanes per row, every format
+GATE_UP = [("Q4_K", 768, 2048, 1, 8), ("Q4_K", 768, 2048, 4, 8), ("Q4_K", 256, 1024, 3, 4), ("Q6_K", 512, 4096, 2, 2),
+           ("Q8_0", 320, 2080, 2, 3), ("TQ2_0", 256, 1536, 1, 8), ("IQ2_XXS", 256, 2048, 2, 4), ("Q4_0", 288, 864, 5, 2)]
+
+
+@pytest.mark.parametrize("fmt,FF,E,L,k", GATE_UP)
+def test_moe_gate_up_equals_gathered_launch_and_activation(nmq, fmt, FF, E, L, k):
+    """nmq_moe_gate_up (each workgroup: 32 rows of a slot's gate and up, then the activation and its
+    two-stage input) equals nmq_mv_experts_x followed by nmq_silu_mul_quant bit for bit (xq, xq2, xd, xs)."""
+    t, A, B, per, ids, x, rng = _gate_up_case(fmt, 12, FF, E, L, k, 261 + FF + L)
+    say("moe_gate_up", fmt, FF, E, L, k)
+    for mode in (nmq.X_F32_BF16, nmq.X_F32):
+        want, _ = _gate_up_two_launches(nmq, t, A, B, ids, per, x, mode, L, k, FF, E)
+        got = _gate_up_fused(nmq, t, A, B, ids, per, x, mode, L, k, FF, E)
+        torch.cuda.synchronize()
+        assert _same_input(got, want), (fmt, mode)
+    xb = x.to(torch.bfloat16).contiguous()
+    want, _ = _gate_up_two_launches(nmq, t, A, B, ids, per, xb, nmq.X_BF16, L, k, FF, E)
+    got = _gate_up_fused(nmq, t, A, B, ids, per, xb, nmq.X_BF16, L, k, FF, E)
+    torch.cuda.synchronize()
+    assert _same_input(got, want), (fmt, "bf16")
+
+
+def test_moe_gate_up_against_oracle(nmq, oracle):
+    """nmq_moe_gate_up against the oracle: g and u of every slot from the oracle's integer path on the
+    token's two-stage bf16 input, act = silu(g) * u in fp64; the launch's xd * (xq + xq2 / 254) is act
+    within the bf16 rounding of the activation (2^-8 relative) plus the second stage's step (xd / 254)."""
+    fmt, FF, E, L, k, n_exp = "Q4_K", 256, 2048, 2, 4, 6
+    t, A, B, per, ids, x, rng = _gate_up_case(fmt, n_exp, FF, E, L, k, 271)
+    say("moe_gate_up oracle")
+    a = _gate_up_fused(nmq, t, A, B, ids, per, x, nmq.X_F32_BF16, L, k, FF, E)
+    torch.cuda.synchronize()
+    Ac, Bc, idc = A.cpu().numpy(), B.cpu().numpy(), ids.cpu().numpy()
+    xd = a.xd.cpu().numpy().astype(np.float64)
+    got = (np.repeat(xd, 32) * (a.xq.cpu().numpy() + a.xq2.cpu().numpy() / 254.0)).reshape(L * k, FF)
+    step = np.repeat(xd, 32).reshape(L * k, FF) / 254.0
+    for s in range(L * k):
+        e = int(idc[s])
+        q = oracle.quant_q8(oracle.round_bf16(x[s // k].cpu().numpy()))
+        g = oracle.mv_int(fmt, _expert_rows(Ac, fmt, n_exp, FF, E, e), FF, E, *q)[0]
+        u = oracle.mv_int(fmt, _expert_rows(Bc, fmt, n_exp, FF, E, e), FF, E, *q)[0]
+        want = oracle.akt(g, u)
+        tol = 2.0 ** -8 * np.abs(want) + step[s] + 1e-5 * np.abs(want).max()
+        assert np.all(np.abs(got[s] - want) <= tol), s
+
+
+def test_moe_down_q8_equals_value_input(nmq):
+    """nmq_moe_down_q8 on the two-stage input of bf16(silu(g) * u) equals nmq_moe_down on g and u (the
+    activation formed in its staging) bit for bit: one launch (rows of 768 values) and the workspace form
+    (5120)."""
+    from ggufengine_amd import mmvq
+    for fmt, L, k, E, FF in [("Q6_K", 1, 8, 2048, 768), ("Q6_K", 4, 8, 2048, 768), ("Q4_K", 2, 8, 256, 5120)]:
+        t, w, per, gu, rng = _moe_down_case(nmq, fmt, L, k, E, FF, 16, 281 + L)
+        n = L * k
+        work = _moe_down_work(nmq, t, L, k, E, FF)
+        ids = torch.from_numpy(rng.integers(0, 16, n)).cuda()
+        wts = dev(rng.random((L, k)).astype(np.float32))
+        say("moe_down_q8", fmt, L, k, E, FF)
+        want = _moe_down_fused(nmq, t, w, per, ids, gu, wts, L, k, E, FF, work)
+        a = mmvq.Eingang(n=n * FF, device=torch.device("cuda"))
+        Lb = nmq.lib()
+        nmq.check(Lb.nmq_silu_mul_quant(gu.data_ptr(), gu[n:].data_ptr(), a.xq.data_ptr(), a.xq2.data_ptr(),
+                                        a.xd.data_ptr(), a.xs.data_ptr(), n * FF, nmq.stream_ptr()))
+        got = torch.full((L, E), float("nan"), device="cuda")
+        nmq.check(Lb.nmq_moe_down_q8(t, w.data_ptr(), ids.data_ptr(), L, k, per, a.xq.data_ptr(), a.xq2.data_ptr(),
+                                     a.xd.data_ptr(), a.xs.data_ptr(), wts.data_ptr(), got.data_ptr(), E, FF,
+                                     work.data_ptr(), work.numel(), nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (fmt, L, k, FF)
+
+
+def test_moe_gate_up_graph_replays(nmq):
+    """nmq_moe_gate_up + nmq_moe_down_q8 captured in one HIP graph, replayed with new ids and weights written
+    between replays (eager work in between): every replay equals the eager calls."""
+    from ggufengine_amd import mmvq
+    fmt, FF, E, L, k = "Q4_K", 768, 2048, 1, 8
+    t, A, B, per, ids, x, rng = _gate_up_case(fmt, 16, FF, E, L, k, 291)
+    D = dev(random_blocks("Q6_K", 16 * E * FF // 256, seed=292))
+    perd = D.numel() // 16
+    wts = dev(rng.random((L, k)).astype(np.float32))
+    a = mmvq.Eingang(n=L * k * FF, device=torch.device("cuda"))
+    out = torch.empty(L, E, device="cuda")
+    Lb = nmq.lib()
+
+    def layer(a, out):
+        _gate_up_fused(nmq, t, A, B, ids, per, x, nmq.X_F32_BF16, L, k, FF, E, a)
+        nmq.check(Lb.nmq_moe_down_q8(14, D.data_ptr(), ids.data_ptr(), L, k, perd, a.xq.data_ptr(), a.xq2.data_ptr(),
+                                     a.xd.data_ptr(), a.xs.data_ptr(), wts.data_ptr(), out.data_ptr(), E, FF, None, 0,
+                                     nmq.stream_ptr()))
+        return out
+    say("moe_gate_up graph")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        layer(a, out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer(a, out)
+    for rep in range(4):
+        ids.copy_(torch.from_numpy(rng.integers(0, 16, L * k)))
+        wts.copy_(torch.from_numpy(rng.random((L, k)).astype(np.float32)))
+        x.copy_(torch.from_numpy(rng.standard_normal((L, E)).astype(np.float32)))
+        g.replay()
+        torch.cuda.synchronize()
+        a2 = mmvq.Eingang(n=L * k * FF, device=torch.device("cuda"))
+        want = layer(a2, torch.empty(L, E, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+
+
 # ---- down projection fused with the weighted combine (nmq_moe_down) ----------------------------------------
 
 def _moe_down_case(nmq, fmt, L, k, E, FF, n_exp, seed):

@@ -49,7 +49,8 @@ const char* nmq_strerror(int code);
  * take their launch shape from constants in mmvq.py:25-37 and cudakern.py:31-54).  name: a knob of
  * the launch planner without or with the "NMQ_" prefix (MV1, MV1_MODE, MV1_HR, MV1_WPC, MV1_W,
  * MV1_RW, MV1_NBUF, MV1_MAXNIT, MVL, MVL_WPC, MVL_W, MVC_WGPC, MVC_RW, MVC_ROWS, MVT_MAX, MVT_WPC,
- * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVD, MVD_MIN, MVD_TPW, MVD_KS, MV1_T); value
+ * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVK_HR, MVK_NBUF, MVD, MVD_MIN, MVD_TPW,
+ * MVD_KS, MV1_T, MOE_GU_RW, MOE_GU_WGS); value
  * NMQ_TUNE_DEFAULT restores the measured default.
  * Process-wide, read by every later launch; the environment is never consulted.  NMQ_ERR_ARG for an
  * unknown name.  nmq_get_tuning writes the override or NMQ_TUNE_DEFAULT.
@@ -289,6 +290,25 @@ int nmq_moe_gate_up(int fmt, const void* w_gate, const void* w_up, const int64_t
 int nmq_moe_down_q8(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const int8_t* xq,
                     const int8_t* xq2, const float* xd, const float* xs, const float* wts, float* out, int n_out,
                     int n_in, void* work, int64_t work_bytes, void* stream);
+
+/*
+ * The whole expert layer of an MoE block: for token t < L with slots s = t*k + j (expert ids[s], weight
+ * wts[s]),
+ *   a_s = bf16(silu(W_gate_{ids[s]} . x_t) * (W_up_{ids[s]} . x_t)),   out[t] = sum_j wts[s] * (W_down_{ids[s]} . a_s),
+ * bit for bit nmq_moe_gate_up followed by nmq_moe_down_q8 (and so nmq_mv_experts_x, nmq_silu_mul_quant,
+ * nmq_mv_experts and nmq_moe_combine).  Gate and up: fmt_gu, FF x E, experts per_gu bytes apart (or address
+ * tables, per_gu < 0); down: fmt_down, E x FF, per_down; x: L x E values (NMQ_X_BF16, NMQ_X_F32 or
+ * NMQ_X_F32_BF16); out: fp32 L x E; FF % 32 == 0; L*k <= 32767.
+ * work: nmq_moe_layer_work_bytes(L, k, E, FF) bytes, 256-byte aligned (no clearing needed); calls that
+ * overlap in time must not share it.  Two launches: nmq_moe_gate_up + nmq_moe_down_q8 while the gate|up
+ * workgroups ((FF / 32) * L * k) fit one per CU and the rows fit that kernel (E <= 4096), else the gathered
+ * gate|up launch into fp32 (in `work`) followed by nmq_moe_down forming the activation in its staging.
+ * Replaces Experten.__call__ (models/moe.py:264-277).
+ */
+int nmq_moe_layer_work_bytes(int L, int k, int E, int FF, int64_t* bytes);
+int nmq_moe_layer(int fmt_gu, const void* w_gate, const void* w_up, int64_t per_gu, int fmt_down, const void* w_down,
+                  int64_t per_down, const int64_t* ids, const float* wts, int L, int k, const void* x, int x_mode,
+                  float* out, int E, int FF, void* work, int64_t work_bytes, void* stream);
 
 /*
  * nmq_moe_down without a workspace argument, for callers that cannot allocate device memory (code under

@@ -1446,21 +1446,19 @@ struct QuantOut {
     float* xs;
 };
 
+// Workgroup (group g, slot s) of the gate|up kernel; the rows of a projection on WH = 32 / (P*RW) waves (the
+// workgroup has 2*WH).  res: 64 floats of LDS.  Wave 0 writes the group's two-stage input.
 template <int F, int T, int RW>
-__global__ __launch_bounds__(1024) void moe_gu_kernel(MvParams p, QuantOut o) {
-    args_early<true>(p);
+__device__ __forceinline__ void moe_gu_body(const MvParams& p, const QuantOut& o, int g, int s, u8* lds, u64* tab,
+                                            float* res) {
     using FM = Fmt<F>;
     constexpr int P = 64 / T;
     constexpr int WH = 32 / (P * RW);  // waves per projection
-    extern __shared__ __attribute__((aligned(16))) u8 lds[];
-    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
-    __shared__ float res[64];  // gate sums, then up sums
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int team = lane / T, lt = lane % T;
-    const int s = blockIdx.y;
     const bool up = wave >= WH;
     const int lr = ((up ? wave - WH : wave) * P + team) * RW;  // the team's first row in the group
-    const int r0 = blockIdx.x * 32 + lr;
+    const int r0 = g * 32 + lr;
     int64_t xrow;
     const u8* wbase = instance_weights(p, up ? p.n_ids + s : s, xrow);
     const RowMap rm = row_map<false>(p, wbase, p.y);
@@ -1479,8 +1477,17 @@ __global__ __launch_bounds__(1024) void moe_gu_kernel(MvParams p, QuantOut o) {
     lds_barrier();
     if (wave == 0 && lane < 32) {
         const float v = silu_mul_bf16(res[lane], res[32 + lane]);
-        quant32_store(v, (int64_t)s * p.n_out + blockIdx.x * 32 + lane, o.xq, o.xq2, o.xd, o.xs);
+        quant32_store(v, (int64_t)s * p.n_out + g * 32 + lane, o.xq, o.xq2, o.xd, o.xs);
     }
+}
+
+template <int F, int T, int RW>
+__global__ __launch_bounds__(1024) void moe_gu_kernel(MvParams p, QuantOut o) {
+    args_early<true>(p);
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    __shared__ float res[64];  // gate sums, then up sums
+    moe_gu_body<F, T, RW>(p, o, blockIdx.x, blockIdx.y, lds, tab, res);
 }
 
 // ---- host side --------------------------------------------------------------------------------
@@ -2362,7 +2369,9 @@ int launch_moe_down(MvParams p, Combine c, int L, hipStream_t stream) {
 typedef void (*MoeGuKernel)(MvParams, QuantOut);
 
 // One launch over the p.n_ids slots (value input).  T lanes per row with one unit each (rows of up to
-// 4096 values) and RW rows per team, so that 32 rows of a projection take 4 (T = 16) or 8 waves;
+// 4096 values) and RW rows per team: 32 rows of a projection take 32 / (P*RW) waves, so a workgroup has
+// 2 to 16.  While the workgroups fit one per CU, the smaller RW (more waves per workgroup); with more, the
+// larger (more workgroups resident per CU, one's weight reads overlapping another's compute).
 // NMQ_ERR_SHAPE for longer rows or n_out not a multiple of 32 (a group of the output is one workgroup's).
 template <int F>
 int launch_moe_gu(MvParams p, QuantOut o, hipStream_t stream) {
@@ -2371,14 +2380,21 @@ int launch_moe_gu(MvParams p, QuantOut o, hipStream_t stream) {
     const int U = (p.n_in + 63) / 64;
     const int T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     if (U > T || p.n_out % 32 || p.n_ids < 1 || p.n_ids > 65535) return NMQ_ERR_SHAPE;
-    const int P = 64 / T, rw = T == 64 ? 4 : 2;
+    const int P = 64 / T;
+    const int64_t wgs = (int64_t)(p.n_out / 32) * p.n_ids;
+    const int lo = T == 64 ? 4 : 2;
+    int rw = tune(TUNE_MOE_GU_RW, wgs <= di.cus ? lo : 2 * lo);
+    rw = rw <= lo ? lo : 2 * lo;
     p.nblk = p.n_in / FM::BV;
     p.row_bytes = (int64_t)p.nblk * FM::BB;
     p.ktp = (p.n_in + 127) / 128 * 128;
     p.nt = 64 * (2 * 32 / (P * rw));
     const size_t lds = (size_t)p.ktp * 9 / 4;
     if (lds > (size_t)di.lds_max || p.ktp / 4 > 2 * p.nt) return NMQ_ERR_SHAPE;
-    const MoeGuKernel k = T == 16 ? moe_gu_kernel<F, 16, 2> : (T == 32 ? moe_gu_kernel<F, 32, 2> : moe_gu_kernel<F, 64, 4>);
+    const bool big = rw > lo;
+    const MoeGuKernel k = T == 16 ? (big ? moe_gu_kernel<F, 16, 4> : moe_gu_kernel<F, 16, 2>)
+                        : T == 32 ? (big ? moe_gu_kernel<F, 32, 4> : moe_gu_kernel<F, 32, 2>)
+                                  : (big ? moe_gu_kernel<F, 64, 8> : moe_gu_kernel<F, 64, 4>);
     hipLaunchKernelGGL(k, dim3((unsigned)(p.n_out / 32), (unsigned)p.n_ids), dim3(p.nt), lds, stream, p, o);
     return (int)hipGetLastError();
 }

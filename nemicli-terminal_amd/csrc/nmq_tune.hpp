@@ -44,6 +44,8 @@ enum Tune : int {
     TUNE_MV1_T,       // lanes per row of the persistent one-token kernel (16, 32, 64; 0: by row length)
     TUNE_MVK_HR,      // 0: compiler-scheduled reads in the K-split long-row kernel
     TUNE_MVK_NBUF,    // its row buffers with hand-issued reads (3, 4)
+    TUNE_MOE_GU_RW,   // rows per team of the MoE gate|up kernel (2, 4; 4, 8 for rows of 2049..4096 values)
+    TUNE_MOE_GU_WGS,  // most workgroups of the gate|up kernel in the layer (default one per CU)
     TUNE_COUNT
 };
 
@@ -52,7 +54,8 @@ inline const char* const kTuneNames[TUNE_COUNT] = {
     "MV1",      "MV1_MAXNIT", "MV1_RW",  "MV1_NBUF", "MV1_WPC", "MV1_W",   "MV1_MODE", "MV1_HR",
     "MVL",      "MVL_WPC",    "MVL_W",   "MVC_WGPC", "MVC_RW",  "MVC_ROWS", "MVT_MAX", "MVT_WPC",
     "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G",    "MVK",     "MVK_WPC",
-    "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS",   "MV1_T",    "MVK_HR",   "MVK_NBUF"};
+    "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS",   "MV1_T",    "MVK_HR",   "MVK_NBUF",
+    "MOE_GU_RW", "MOE_GU_WGS"};
 
 constexpr int TUNE_UNSET = INT_MIN;
 

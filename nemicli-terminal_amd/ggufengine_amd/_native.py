@@ -71,6 +71,9 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_moe_gate_up.restype = i
     L.nmq_moe_down_q8.argtypes = [i, p, p, i, i, i64, p, p, p, p, p, p, i, i, p, i64, p]
     L.nmq_moe_down_q8.restype = i
+    L.nmq_moe_layer_work_bytes.argtypes, L.nmq_moe_layer_work_bytes.restype = [i, i, i, i, p], i
+    L.nmq_moe_layer.argtypes = [i, p, p, i64, i, p, i64, p, p, i, i, p, i, p, i, i, p, i64, p]
+    L.nmq_moe_layer.restype = i
     L.nmq_stream_read.argtypes, L.nmq_stream_read.restype = [p, i64, p, i, i, i, p], i
     L.nmq_set_tuning.argtypes, L.nmq_set_tuning.restype = [ctypes.c_char_p, i], i
     L.nmq_get_tuning.argtypes, L.nmq_get_tuning.restype = [ctypes.c_char_p, p], i

@@ -31,9 +31,6 @@ from . import _native, cudakern, hostmem
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
 from .mmvq import WERTE_BIS, Eingang, _starten, _werte, eingang_bf16
 
-# rows (values) up to which nmq_moe_gate_up takes the gate and up projections: one 64-value unit per lane
-GU_BIS = 4096
-
 
 class PackedExperts:
     """All experts of one tensor (n_exp, n_out, n_in) in their GGUF block bytes, multiplied on the device
@@ -287,52 +284,34 @@ class Experten:
 
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights (reference
-        models/moe.py:264-285).  Two launches: gate and up of every (token, slot) with each token's input
-        rounded to bf16 and quantised in the launch, and the activation bf16(silu(gate) * up) formed and
-        quantised in the same workgroups (nmq_moe_gate_up: rows of up to GU_BIS values, FF a multiple of
-        32); then down on that two-stage input with the weighted combine in the same launch
-        (nmq_moe_down_q8).  Longer rows: gate and up into fp32 outputs, down forming the activation in its
-        staging (nmq_moe_down).  (Rows longer than WERTE_BIS values, or a gate and up of different layout:
-        the input quantisations as launches of their own.)"""
+        models/moe.py:264-277).  One call of nmq_moe_layer, two launches: gate|up with the activation
+        quantised in the same workgroups, then the down launch with the weighted combine on that input; for
+        more tokens the gathered gate|up launch into fp32, then the down launch forming the activation in its
+        staging.  (Rows longer than WERTE_BIS values, or a gate and up
+        of different layout: the input quantisations as launches of their own.)"""
         L_, E = x.shape
         k = idx.shape[1]
         dev = x.device
-        if not self._fused() or max(E, self.gate.n_out) > WERTE_BIS or x.dtype != torch.float32:
+        if (not self._fused() or max(E, self.gate.n_out) > WERTE_BIS or x.dtype != torch.float32
+                or self.gate.n_out % 32):
             return self._aufgeteilt(x, idx, w)
-        L = _native.lib()
-        st = _native.stream_ptr(dev)
-        n = L_ * k
         FF = self.gate.n_out
-        xc = x.contiguous()
         flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
         (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
         wd, perd = self.down._quelle(dev)
         out = torch.empty(L_, E, dtype=torch.float32, device=dev)
         wf = w.to(dev, torch.float32).contiguous()
-        work = self._arbeitsplatz(L_, k, dev)
-        if E <= GU_BIS and FF % 32 == 0:
-            a = Eingang(n=n * FF, device=dev)
-            _starten("moe_gate_up", L.nmq_moe_gate_up, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
-                     flat.data_ptr(), L_, k, per, xc.data_ptr(), _native.X_F32_BF16, a.xq.data_ptr(),
-                     a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), FF, E, st)
-            _starten("moe_down", L.nmq_moe_down_q8, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), L_, k,
-                     perd, a.xq.data_ptr(), a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), wf.data_ptr(),
-                     out.data_ptr(), E, FF, work.data_ptr(), work.numel(), st)
-            return out
-        gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
-        _starten("mv_experts2", L.nmq_mv_experts_x, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
-                 flat.data_ptr(), n, per, xc.data_ptr(), _native.X_F32_BF16, None, k, gu.data_ptr(), FF, E, st)
-        _starten("moe_down", L.nmq_moe_down, TYPE_ID[self.down.name], wd.data_ptr(), flat.data_ptr(), L_, k, perd,
-                 gu.data_ptr(), _native.X_SILU_MUL_BF16, gu[n:].data_ptr(), wf.data_ptr(), out.data_ptr(), E, FF,
-                 work.data_ptr(), work.numel(), st)
+        work = self._arbeitsplatz(L_, k, E, FF, dev)
+        _starten("moe_layer", _native.lib().nmq_moe_layer, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(), per,
+                 TYPE_ID[self.down.name], wd.data_ptr(), perd, flat.data_ptr(), wf.data_ptr(), L_, k,
+                 x.contiguous().data_ptr(), _native.X_F32_BF16, out.data_ptr(), E, FF, work.data_ptr(), work.numel(),
+                 _native.stream_ptr(dev))
         return out
 
-    def _arbeitsplatz(self, L_: int, k: int, dev) -> torch.Tensor:
-        """The fused down launch's workspace for L_ tokens of k slots: kept per layer and device, grown
-        when needed, zeroed once when made (the launch leaves its counters zero)."""
+    def _arbeitsplatz(self, L_: int, k: int, E: int, FF: int, dev) -> torch.Tensor:
+        """nmq_moe_layer's workspace for L_ tokens of k slots: kept per layer and device, grown when needed."""
         need = ctypes.c_int64(0)
-        _native.check(_native.lib().nmq_moe_down_work_bytes(TYPE_ID[self.down.name], L_, k, self.down.n_out,
-                                                            self.down.n_in, ctypes.byref(need)))
+        _native.check(_native.lib().nmq_moe_layer_work_bytes(L_, k, E, FF, ctypes.byref(need)))
         have = self._work.get(dev)
         if have is None or have.numel() < need.value:
             have = torch.zeros(max(need.value, 256), dtype=torch.uint8, device=dev)

@@ -237,3 +237,32 @@ def test_moe_gate_up_and_down_q8_check_without_launching(L):
     assert down(work=a + 16) == _native.NMQ_ERR_ARG      # rows too long for one launch: a workspace, 256-aligned
     assert down(work_bytes=16) == _native.NMQ_ERR_SHAPE  # too small
     assert down(n_in=5000) == _native.NMQ_ERR_SHAPE      # not whole blocks
+
+
+def test_moe_layer_checks_without_launching(L):
+    """nmq_moe_layer sizes its workspace and refuses bad arguments before anything is launched."""
+    from ggufengine_amd import _native
+    need = ctypes.c_int64(0)
+    assert L.nmq_moe_layer_work_bytes(1, 8, 2048, 768, ctypes.byref(need)) == 0
+    n = 8 * 768
+    assert need.value >= 2 * n + 2 * (n // 32 * 4) + 2 * n * 4            # activation, fp32 gate|up
+    assert L.nmq_moe_layer_work_bytes(0, 8, 2048, 768, ctypes.byref(need)) == _native.NMQ_ERR_ARG
+    buf = ctypes.create_string_buffer(1 << 16)
+    a = (ctypes.addressof(buf) + 255) // 256 * 256
+    args = dict(fg=12, wg=a, wu=a, per=768 * 8 * 144, fd=14, wd=a, perd=2048 * 3 * 210, ids=a, wts=a, L=1, k=8, x=a,
+                mode=_native.X_F32_BF16, out=a, E=2048, FF=768, work=a, work_bytes=1 << 30)
+
+    def call(**kw):
+        v = {**args, **kw}
+        return L.nmq_moe_layer(v["fg"], v["wg"], v["wu"], v["per"], v["fd"], v["wd"], v["perd"], v["ids"], v["wts"],
+                               v["L"], v["k"], v["x"], v["mode"], v["out"], v["E"], v["FF"], v["work"],
+                               v["work_bytes"], None)
+    assert call(ids=None) == _native.NMQ_ERR_ARG
+    assert call(wd=None) == _native.NMQ_ERR_ARG
+    assert call(mode=_native.X_SILU_MUL_BF16) == _native.NMQ_ERR_ARG
+    assert call(work=None) == _native.NMQ_ERR_ARG
+    assert call(work=a + 64) == _native.NMQ_ERR_ARG                 # 256-byte aligned
+    assert call(work_bytes=1024) == _native.NMQ_ERR_SHAPE           # too small
+    assert call(FF=760, per=760 * 8 * 144) == _native.NMQ_ERR_SHAPE  # groups of 32 rows
+    assert call(perd=100) == _native.NMQ_ERR_SHAPE                   # down experts overlap
+    assert call(fd=13) == _native.NMQ_ERR_FORMAT

@@ -741,12 +741,16 @@ GATE_UP = [("Q4_K", 768, 2048, 1, 8), ("Q4_K", 768, 2048, 4, 8), ("Q4_K", 256, 1
            ("Q8_0", 320, 2080, 2, 3), ("TQ2_0", 256, 1536, 1, 8), ("IQ2_XXS", 256, 2048, 2, 4), ("Q4_0", 288, 864, 5, 2)]
 
 
+@pytest.mark.parametrize("rows", ["default", "fewer", "more"])
 @pytest.mark.parametrize("fmt,FF,E,L,k", GATE_UP)
-def test_moe_gate_up_equals_gathered_launch_and_activation(nmq, fmt, FF, E, L, k):
+def test_moe_gate_up_equals_gathered_launch_and_activation(nmq, tune, fmt, FF, E, L, k, rows):
     """nmq_moe_gate_up (each workgroup: 32 rows of a slot's gate and up, then the activation and its
-    two-stage input) equals nmq_mv_experts_x followed by nmq_silu_mul_quant bit for bit (xq, xq2, xd, xs)."""
+    two-stage input) equals nmq_mv_experts_x followed by nmq_silu_mul_quant bit for bit (xq, xq2, xd, xs),
+    with either number of rows per team (the planner's choice, 2 or 4 -- 4 or 8 for rows over 2048 values)."""
+    if rows != "default":
+        tune(MOE_GU_RW=(2 if rows == "fewer" else 4) * (2 if E > 2048 else 1))
     t, A, B, per, ids, x, rng = _gate_up_case(fmt, 12, FF, E, L, k, 261 + FF + L)
-    say("moe_gate_up", fmt, FF, E, L, k)
+    say("moe_gate_up", fmt, FF, E, L, k, rows)
     for mode in (nmq.X_F32_BF16, nmq.X_F32):
         want, _ = _gate_up_two_launches(nmq, t, A, B, ids, per, x, mode, L, k, FF, E)
         got = _gate_up_fused(nmq, t, A, B, ids, per, x, mode, L, k, FF, E)
@@ -843,6 +847,108 @@ def test_moe_gate_up_graph_replays(nmq):
         torch.cuda.synchronize()
         a2 = mmvq.Eingang(n=L * k * FF, device=torch.device("cuda"))
         want = layer(a2, torch.empty(L, E, device="cuda"))
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), rep
+
+
+
+# ---- the whole expert layer (nmq_moe_layer) ------------------------------------------------------------------
+
+def _layer_case(fg, fd, n_exp, E, FF, seed):
+    from ggufengine_amd.gguf_types import TYPE_ID
+    A = dev(random_blocks(fg, n_exp * FF * E // BV[fg], seed=seed))
+    B = dev(random_blocks(fg, n_exp * FF * E // BV[fg], seed=seed + 1))
+    D = dev(random_blocks(fd, n_exp * E * FF // BV[fd], seed=seed + 2))
+    return TYPE_ID[fg], TYPE_ID[fd], A, B, D, A.numel() // n_exp, D.numel() // n_exp
+
+
+def _layer_launch_by_launch(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF):
+    """nmq_mv_experts_x (gate and up) -> nmq_silu_mul_quant -> nmq_mv_experts (down) -> nmq_moe_combine."""
+    n = L * k
+    a, _ = _gate_up_two_launches(nmq, tg, A, B, ids, per, x, nmq.X_F32_BF16, L, k, FF, E)
+    y = torch.empty(n, E, device="cuda")
+    out = torch.empty(L, E, device="cuda")
+    Lb = nmq.lib()
+    nmq.check(Lb.nmq_mv_experts(td, D.data_ptr(), ids.data_ptr(), n, perd, a.xq.data_ptr(), a.xq2.data_ptr(),
+                                a.xd.data_ptr(), a.xs.data_ptr(), 1, y.data_ptr(), E, FF, nmq.stream_ptr()))
+    nmq.check(Lb.nmq_moe_combine(y.data_ptr(), wts.data_ptr(), L, k, E, out.data_ptr(), nmq.stream_ptr()))
+    return out
+
+
+def _layer_work(nmq, L, k, E, FF):
+    import ctypes
+    need = ctypes.c_int64(0)
+    nmq.check(nmq.lib().nmq_moe_layer_work_bytes(L, k, E, FF, ctypes.byref(need)))
+    return torch.zeros(need.value, dtype=torch.uint8, device="cuda")
+
+
+def _layer_call(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF, work, out=None):
+    out = torch.full((L, E), float("nan"), device="cuda") if out is None else out
+    nmq.check(nmq.lib().nmq_moe_layer(tg, A.data_ptr(), B.data_ptr(), per, td, D.data_ptr(), perd, ids.data_ptr(),
+                                      wts.data_ptr(), L, k, x.data_ptr(), nmq.X_F32_BF16, out.data_ptr(), E, FF,
+                                      work.data_ptr(), work.numel(), nmq.stream_ptr()))
+    return out
+
+
+# (gate|up format, down format, E, FF, tokens L, slots k, path): "gu" = gate|up kernel + down launch on its
+# two-stage input (the default for these shapes), "gathered" = the gathered gate|up launch + down forming the
+# activation (the default for many tokens)
+LAYER = [("Q4_K", "Q6_K", 2048, 768, 1, 8, "gu"), ("Q4_K", "Q4_K", 4096, 1024, 1, 4, "gu"),
+         ("Q4_K", "Q6_K", 2048, 1536, 1, 4, "gu"), ("Q4_K", "Q6_K", 2048, 768, 1, 3, "gu"),
+         ("Q4_K", "Q6_K", 2048, 768, 4, 8, "gathered"), ("Q8_0", "Q8_0", 1024, 512, 1, 8, "gu"),
+         ("Q6_K", "Q4_K", 2048, 768, 2, 4, "gathered"), ("Q4_K", "Q6_K", 2048, 768, 1, 8, "gathered"),
+         ("Q4_K", "Q6_K", 256, 5120, 2, 8, "gu")]
+
+
+@pytest.mark.parametrize("fg,fd,E,FF,L,k,path", LAYER)
+def test_moe_layer_equals_launch_by_launch(nmq, tune, fg, fd, E, FF, L, k, path):
+    """nmq_moe_layer equals the gathered gate|up launch, the activation's quantisation, the gathered down
+    launch and the combine, bit for bit, over three calls in a row on one workspace with new routings,
+    weights and inputs (FF 5120: the down launch through its workspace)."""
+    if path == "gathered":
+        tune(MOE_GU_WGS=0)
+    n_exp = 12
+    tg, td, A, B, D, per, perd = _layer_case(fg, fd, n_exp, E, FF, 301 + E + FF + L * k)
+    work = _layer_work(nmq, L, k, E, FF)
+    rng = np.random.default_rng(311 + L * k)
+    say("moe_layer", fg, fd, E, FF, L, k, path)
+    for call in range(3):
+        ids = torch.from_numpy(rng.integers(0, n_exp, L * k)).cuda()
+        wts = dev(rng.random((L, k)).astype(np.float32))
+        x = dev(rng.standard_normal((L, E)).astype(np.float32))
+        want = _layer_launch_by_launch(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF)
+        got = _layer_call(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF, work)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (call, path)
+
+
+def test_moe_layer_graph_replays(nmq):
+    """One nmq_moe_layer call captured in a HIP graph and replayed with new ids, weights and inputs written
+    between replays (eager work in between): every replay equals the launch-by-launch layer."""
+    E, FF, L, k, n_exp = 2048, 768, 1, 8, 16
+    tg, td, A, B, D, per, perd = _layer_case("Q4_K", "Q6_K", n_exp, E, FF, 321)
+    work = _layer_work(nmq, L, k, E, FF)
+    rng = np.random.default_rng(322)
+    ids = torch.from_numpy(rng.integers(0, n_exp, L * k)).cuda()
+    wts = dev(rng.random((L, k)).astype(np.float32))
+    x = dev(rng.standard_normal((L, E)).astype(np.float32))
+    out = torch.empty(L, E, device="cuda")
+    say("moe_layer graph")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        _layer_call(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF, work, out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        _layer_call(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF, work, out)
+    for rep in range(4):
+        ids.copy_(torch.from_numpy(rng.integers(0, n_exp, L * k)))
+        wts.copy_(torch.from_numpy(rng.random((L, k)).astype(np.float32)))
+        x.copy_(torch.from_numpy(rng.standard_normal((L, E)).astype(np.float32)))
+        g.replay()
+        torch.cuda.synchronize()
+        want = _layer_launch_by_launch(nmq, tg, td, A, B, D, per, perd, ids, wts, x, L, k, E, FF)
         torch.cuda.synchronize()
         assert torch.equal(out, want), rep
 

@@ -3,12 +3,13 @@
 
 Headline (one JSON line on stdout): Q4_K 14336x4096 mat-vec at batch 1 (the gate/up projection of a
 Llama-3-8B decoder layer) -- GB/s of algorithmic bytes, % of the 8 TB/s HBM peak, us per mat-vec --
-plus us per Llama-3-8B layer: the 7 mat-vecs on their 4 fp32 inputs in 5 launches (q, k, v in one
-nmq_mv_x launch, gate and up in another, o, each quantising its 4096-value input itself; the down
-input quantised by its own launch), checked against the oracle.  Beside it: the same layer with 4 quantisation launches and nmq_mv_multi
-(us_per_layer_multi), and with one launch per matrix (us_per_layer_separate); the layer and the layer
-with its inputs formed (us_per_layer_fused_inputs) also as HIP graphs of 1 and 32 layers, replayed
-(us_per_layer_graph*).
+plus us per Llama-3-8B layer: the 7 mat-vecs in 4 launches (q, k, v in one nmq_mv_x launch and o in
+another, each quantising its fp32 4096-value input itself; gate and up in one nmq_mv_gate_up_act launch
+that also forms the activation silu(gate) * up and quantises it as the down input; down), checked
+against the oracle.  Beside it: the layer with the down input given and quantised by its own launch
+(us_per_layer_values, 5 launches), with 4 quantisation launches and nmq_mv_multi (us_per_layer_multi),
+and with one launch per matrix (us_per_layer_separate); the layer and the layer with its inputs formed
+(us_per_layer_fused_inputs) also as HIP graphs of 1 and 32 layers, replayed (us_per_layer_graph*).
 
 A "step" is one launch of the mat-vec kernel over one token whose two-stage int8 input (Eingang) is
 already resident in HBM.  The weight matrix of each step is one of several identical copies whose
@@ -725,12 +726,25 @@ def main():
             one nmq_mv launch per matrix; "multi": the matrices of one input (q, k, v and gate, up) in
             one nmq_mv_multi launch; "values": the launches on 4096-value inputs take the fp32 input
             directly (nmq_mv_x: each launch quantises it itself), the down projection (14336 values,
-            where staging fp32 values costs more than a quantisation launch) as in "multi"."""
+            where staging fp32 values costs more than a quantisation launch) as in "multi"; "act": as
+            "values", but the down input is the layer's own activation silu(gate) * up, formed and
+            quantised by the gate|up launch (nmq_mv_gate_up_act) -- 4 launches."""
             lw = layers[li % nl]
             for inp, names in order:
                 f, k, wp, rows_, yp = mats_of(lw, names)
                 m = len(names)
-                if how == "values" and k <= VALUES_MAX_N_IN:
+                if how == "act" and inp == "x_ffn":
+                    ea = eg["act"]
+                    _native.check(L.nmq_mv_gate_up_act(TYPE[f], wp[0], wp[1], xin[inp].data_ptr(), _native.X_F32,
+                                                       _native.ACT_SILU, ea.xq.data_ptr(), ea.xq2.data_ptr(),
+                                                       ea.xd.data_ptr(), ea.xs.data_ptr(), rows_[0], k, st))
+                    continue
+                if how == "act" and inp == "act":
+                    ea = eg["act"]
+                    _native.check(L.nmq_mv(TYPE[f], wp[0], ea.xq.data_ptr(), ea.xq2.data_ptr(), ea.xd.data_ptr(),
+                                           ea.xs.data_ptr(), yp[0], rows_[0], k, 1, st))
+                    continue
+                if how in ("values", "act") and k <= VALUES_MAX_N_IN:
                     _native.check(L.nmq_mv_x(TYPE[f], m, (ctypes.c_void_p * m)(*wp), (ctypes.c_int * m)(*rows_),
                                              (ctypes.c_void_p * m)(*yp), xin[inp].data_ptr(), _native.X_F32, None,
                                              k, st))
@@ -746,9 +760,9 @@ def main():
                         _native.check(L.nmq_mv(TYPE[f], w_, *ep, y_, r_, k, 1, st))
 
         reps = max(20, args.steps // 10)
-        for how in ("separate", "multi", "values"):
+        for how in ("separate", "multi", "values", "act"):
             us_layer = _events_us(lambda i: one_layer(i, how), reps, max(5, args.warmup // 10))
-            if how != "values":
+            if how != "act":
                 cfg[f"us_per_layer_{how}"] = round(us_layer, 3)
         cfg["us_per_layer"] = round(us_layer, 3)
 
@@ -773,25 +787,34 @@ def main():
             us = _events_us(lambda i: graphs[i % nl].replay(), n_rep, max(5, args.warmup // 10))
             return round(us / per, 3)
 
-        cfg["us_per_layer_graph"] = graph_us(lambda j, st: one_layer(j, "values", st))
-        cfg["us_per_layer_graph_32_layers"] = graph_us(lambda j, st: one_layer(j, "values", st), 32)
+        cfg["us_per_layer_graph"] = graph_us(lambda j, st: one_layer(j, "act", st))
+        cfg["us_per_layer_graph_32_layers"] = graph_us(lambda j, st: one_layer(j, "act", st), 32)
         cfg["layer_weight_bytes"] = layer_bytes
         cfg["layer_pct_hbm_peak"] = round(100 * layer_bytes / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 2)
-        # the layer's outputs (last step, value input; the weight copies are identical) against
-        # the oracle: every matrix of the layer, max relative error per output row-vector
-        errs = []
+        # the layer's outputs against the oracle (the weight copies are identical), max relative error per
+        # output row-vector: every matrix of the "values" form on its given input, then the down
+        # projection of the "act" form on the oracle's silu(gate) * up
+        one_layer(0, "values")
+        torch.cuda.synchronize()
+        errs, ref = [], {}
         for inp, names in order:
             xv = xin[inp].cpu().numpy()[None]
             for n in names:
                 f, r, k = spec[n][1], spec[n][2], spec[n][3]
-                errs.append(float(oracle.rel_err_rows(ys[n].cpu().numpy()[None],
-                                                      oracle.mv_deq(f, raws_np[n], r, k, xv)).max()))
+                ref[n] = oracle.mv_deq(f, raws_np[n], r, k, xv)
+                errs.append(float(oracle.rel_err_rows(ys[n].cpu().numpy()[None], ref[n]).max()))
+        one_layer(0, "act")
+        torch.cuda.synchronize()
+        act_o = oracle.akt(ref["gate"][0], ref["up"][0]).astype(np.float32)[None]
+        f, r, k = spec["down"][1], spec["down"][2], spec["down"][3]
+        errs.append(float(oracle.rel_err_rows(ys["down"].cpu().numpy()[None],
+                                              oracle.mv_deq(f, raws_np["down"], r, k, act_o)).max()))
         cfg["layer_max_rel_err_vs_oracle"] = max(errs)
 
         # The same layer with its inputs formed as the reference's one-token step forms them
         # (models/baukasten.py:217-241 without rope and attention): RMS norm fused with the q/k/v input,
-        # the attention output quantised, residual add + RMS norm fused with the gate/up input,
-        # silu(gate) * up fused with the down input.  Same launches, more work in the input producers.
+        # the attention output quantised, residual add + RMS norm fused with the gate/up input, the gate|up
+        # launch forming silu(gate) * up and the down input (nmq_mv_gate_up_act, akt_q8's arithmetic).
         E, FF = 4096, 14336
         rng_s = np.random.Generator(np.random.PCG64(34))
         h_s = torch.from_numpy(rng_s.standard_normal(E, dtype=np.float32)).to(dev)
@@ -822,9 +845,9 @@ def main():
             mv_named(lw, "o", eg["attn_out"], st)
             _native.check(L.nmq_norm_q8(h_s.data_ptr(), ys["o"].data_ptr(), 1.0, hn_s.data_ptr(), nw_s.data_ptr(),
                                         1e-5, xn_s.data_ptr(), *ptrs(eg["x_ffn"]), E, st))
-            mv_shared(lw, ("gate", "up"), eg["x_ffn"], st)
-            _native.check(L.nmq_akt_q8(ys["gate"].data_ptr(), ys["up"].data_ptr(), 0, a_s.data_ptr(),
-                                       *ptrs(eg["act"]), FF, st))
+            _native.check(L.nmq_mv_gate_up_act(TYPE["Q4_K"], lw["gate"].data_ptr(), lw["up"].data_ptr(),
+                                               xn_s.data_ptr(), _native.X_F32, _native.ACT_SILU,
+                                               *ptrs(eg["act"]), FF, E, st))
             mv_named(lw, "down", eg["act"], st)
 
         cfg["us_per_layer_fused_inputs"] = round(_events_us(step_layer, reps, max(5, args.warmup // 10)), 3)

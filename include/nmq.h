@@ -50,7 +50,7 @@ const char* nmq_strerror(int code);
  * the launch planner without or with the "NMQ_" prefix (MV1, MV1_MODE, MV1_HR, MV1_WPC, MV1_W,
  * MV1_RW, MV1_NBUF, MV1_MAXNIT, MVL, MVL_WPC, MVL_W, MVC_WGPC, MVC_RW, MVC_ROWS, MVT_MAX, MVT_WPC,
  * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVK_HR, MVK_NBUF, MVD, MVD_MIN, MVD_TPW,
- * MVD_KS, MV1_T, MOE_GU_RW, MOE_GU_WGS); value
+ * MVD_KS, MV1_T, MOE_GU_RW, MOE_GU_WGS, MVP_RPW, MVP_WGS); value
  * NMQ_TUNE_DEFAULT restores the measured default.
  * Process-wide, read by every later launch; the environment is never consulted.  NMQ_ERR_ARG for an
  * unknown name.  nmq_get_tuning writes the override or NMQ_TUNE_DEFAULT.
@@ -263,6 +263,24 @@ int nmq_moe_down_work_bytes(int fmt, int L, int k, int n_out, int n_in, int64_t*
 int nmq_moe_down(int fmt, const void* w, const int64_t* ids, int L, int k, int64_t per_expert, const void* x,
                  int x_mode, const void* x2, const float* wts, float* out, int n_out, int n_in, void* work,
                  int64_t work_bytes, void* stream);
+
+/*
+ * The gate and up projections of a dense FFN with the activation, one token:
+ *   a[r] = act(W_gate[r,:] . x) * (W_up[r,:] . x),   r < n_out,
+ * act: NMQ_ACT_SILU or NMQ_ACT_GELU as nmq_akt_q8 forms them, | NMQ_ACT_BF16 to round a to bf16 (as
+ * nmq_silu_mul_quant does for silu); each product exactly as nmq_mv_x forms it from the same x and x_mode
+ * (NMQ_X_F32 or NMQ_X_F32_BF16).  Writes the two-stage input of a (n_out values) to xq, xq2 (16-byte
+ * aligned), xd, xs: bit for bit nmq_mv_x on both matrices followed by nmq_akt_q8 (or nmq_silu_mul_quant),
+ * in one launch and without the fp32 outputs.  Q4_K, TQ2_0 and IQ2_XXS, rows of at most 4096 values,
+ * n_out % 32 == 0; NMQ_ERR_SHAPE otherwise (the caller then takes the two launches).
+ * Replaces the gate and up calls of the FFN and the activation between them and the down call (the
+ * reference's one-token step: mmvq mv on gate and up, then akt_q8, mmvq.py:122-133, 964-971).
+ */
+#define NMQ_ACT_SILU 0
+#define NMQ_ACT_GELU 1
+#define NMQ_ACT_BF16 2
+int nmq_mv_gate_up_act(int fmt, const void* w_gate, const void* w_up, const void* x, int x_mode, int act,
+                       int8_t* xq, int8_t* xq2, float* xd, float* xs, int n_out, int n_in, void* stream);
 
 /*
  * The gate and up projections of an expert layer with the gated activation in the same launch: for slot

@@ -151,10 +151,7 @@ __global__ __launch_bounds__(256) void akt_q8_kernel(const float* __restrict__ g
     asm volatile("" ::"s"(g), "s"(u), "s"(a), "s"(xq), "s"(xq2), "s"(xd), "s"(xs), "s"(n));
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // launched with 256 threads
     if ((i & ~(int64_t)31) >= n) return;
-    const float x = g[i];
-    float v;
-    if constexpr (GELU) v = 0.5f * x * (1.0f + tanhf(0.7978845608f * (x + 0.044715f * x * x * x)));
-    else v = x / (1.0f + expf(-x));
+    float v = act_value(g[i], GELU != 0);
     if (u) v *= u[i];
     a[i] = v;
     quant32_store(v, i, xq, xq2, xd, xs);
@@ -467,6 +464,27 @@ static int launch_moe_gu_any(int fmt, const MvParams& p, const QuantOut& o, hipS
         case NMQ_Q6_K: return launch_moe_gu<NMQ_Q6_K>(p, o, s);
         case NMQ_IQ2_XXS: return launch_moe_gu<NMQ_IQ2_XXS>(p, o, s);
         case NMQ_TQ2_0: return launch_moe_gu<NMQ_TQ2_0>(p, o, s);
+        default: return NMQ_ERR_FORMAT;
+    }
+}
+
+template <int F>
+int launch_mvp(MvParams p, QuantOut o, hipStream_t stream);
+extern template int launch_mvp<NMQ_Q4_0>(MvParams, QuantOut, hipStream_t);
+extern template int launch_mvp<NMQ_Q8_0>(MvParams, QuantOut, hipStream_t);
+extern template int launch_mvp<NMQ_Q4_K>(MvParams, QuantOut, hipStream_t);
+extern template int launch_mvp<NMQ_Q6_K>(MvParams, QuantOut, hipStream_t);
+extern template int launch_mvp<NMQ_IQ2_XXS>(MvParams, QuantOut, hipStream_t);
+extern template int launch_mvp<NMQ_TQ2_0>(MvParams, QuantOut, hipStream_t);
+
+static int launch_mvp_any(int fmt, const MvParams& p, const QuantOut& o, hipStream_t s) {
+    switch (fmt) {
+        case NMQ_Q4_0: return launch_mvp<NMQ_Q4_0>(p, o, s);
+        case NMQ_Q8_0: return launch_mvp<NMQ_Q8_0>(p, o, s);
+        case NMQ_Q4_K: return launch_mvp<NMQ_Q4_K>(p, o, s);
+        case NMQ_Q6_K: return launch_mvp<NMQ_Q6_K>(p, o, s);
+        case NMQ_IQ2_XXS: return launch_mvp<NMQ_IQ2_XXS>(p, o, s);
+        case NMQ_TQ2_0: return launch_mvp<NMQ_TQ2_0>(p, o, s);
         default: return NMQ_ERR_FORMAT;
     }
 }
@@ -915,6 +933,28 @@ int nmq_mv_experts_x(int fmt, const void* w_a, const void* w_b, const int64_t* i
     p.x_group = x_group;
     p.n_ids = n_ids;
     return launch_any(fmt, p, 1, w_b ? 2 * n_ids : n_ids, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int nmq_mv_gate_up_act(int fmt, const void* w_gate, const void* w_up, const void* x, int x_mode, int act,
+                       int8_t* xq, int8_t* xq2, float* xd, float* xs, int n_out, int n_in, void* stream) {
+    int e = check_mv(fmt, w_gate, xq, xq2, xd, xs, xd, n_out, n_in);
+    if (e) return e;
+    if ((e = check_w(fmt, w_up, xd, n_out, n_in))) return e;
+    if (x_mode == NMQ_X_SILU_MUL_BF16) return NMQ_ERR_ARG;
+    if ((e = check_values(x, x_mode, nullptr, n_in))) return e;
+    if (act & ~(NMQ_ACT_GELU | NMQ_ACT_BF16)) return NMQ_ERR_ARG;
+    MvParams p{};
+    p.w = (const u8*)w_gate;
+    p.w2 = (const u8*)w_up;
+    p.xv = x;
+    p.x_mode = x_mode;
+    p.n_out = n_out;
+    p.n_in = n_in;
+    return launch_mvp_any(fmt, p, QuantOut{xq, xq2, xd, xs, act}, (hipStream_t)stream);
 }
 
 }  // extern "C"

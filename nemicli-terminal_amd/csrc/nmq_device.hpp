@@ -83,32 +83,49 @@ __device__ __forceinline__ float round_bf16(float f) {
     return __uint_as_float((u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
 }
 
-// The gated activation of an expert MLP as its down projection takes it: bf16(silu(g) * u), silu(g) =
-// g / (1 + exp(-g)) with an IEEE division.  Every kernel that forms it calls this one expression, so that
-// they agree bit for bit.
-__device__ __forceinline__ float silu_mul_bf16(float g, float u) { return round_bf16(g / (1.0f + expf(-g)) * u); }
+// The activation of an FFN's gate value g (reference mmvq.py:122-133): silu(g) = g / (1 + exp(-g)) with an
+// IEEE division, or the tanh form of gelu.  Every kernel that forms an activation calls these expressions,
+// so that they agree bit for bit.
+__device__ __forceinline__ float act_value(float g, bool gelu) {
+    return gelu ? 0.5f * g * (1.0f + tanhf(0.7978845608f * (g + 0.044715f * g * g * g))) : g / (1.0f + expf(-g));
+}
 
-// Two-stage int8 input (reference mmvq.py:59-83) of the value v held by this lane, value index i
-// (i % 32 == lane % 32): d = max|v| / 127 over the lane's 32-lane half, q = rint(v / d), q2 = the
-// rounded residual in units of d / 254, and the group's sum (half_max / half_sum_xor).  All 32 lanes
-// of the half-wave take part.
+// The gated activation of an expert MLP as its down projection takes it: bf16(silu(g) * u).
+__device__ __forceinline__ float silu_mul_bf16(float g, float u) { return round_bf16(act_value(g, false) * u); }
+
+// Two-stage int8 input (reference mmvq.py:59-83) of the value v held by this lane (group = the lane's
+// 32-lane half): d = max|v| / 127 over the group, q = rint(v / d), q2 = the rounded residual in units of
+// d / 254, and the group's sum (half_max / half_sum_xor).  All 32 lanes of the half-wave take part.
+struct Quant32 {
+    int q, q2;
+    float d, s;
+};
+
+__device__ __forceinline__ Quant32 quant32(float v) {
+    Quant32 r;
+    const float a = half_max(fabsf(v));
+    r.d = a / 127.0f;
+    r.q = 0;
+    r.q2 = 0;
+    if (r.d > 0.0f) {
+        r.q = (int)rintf(v / r.d);
+        const float e = fmaf(-(float)r.q, r.d, v);
+        const int q2 = (int)rintf(e / (r.d * FEIN));
+        r.q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
+    }
+    r.s = half_sum_xor(v);
+    return r;
+}
+
+// quant32 of v stored as value index i (i % 32 == lane % 32).
 __device__ __forceinline__ void quant32_store(float v, int64_t i, int8_t* __restrict__ xq, int8_t* __restrict__ xq2,
                                               float* __restrict__ xd, float* __restrict__ xs) {
-    const float a = half_max(fabsf(v));
-    const float d = a / 127.0f;
-    int q = 0, q2 = 0;
-    if (d > 0.0f) {
-        q = (int)rintf(v / d);
-        const float r = fmaf(-(float)q, d, v);
-        q2 = (int)rintf(r / (d * FEIN));
-        q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
-    }
-    const float s = half_sum_xor(v);
-    xq[i] = (int8_t)q;
-    xq2[i] = (int8_t)q2;
+    const Quant32 r = quant32(v);
+    xq[i] = (int8_t)r.q;
+    xq2[i] = (int8_t)r.q2;
     if ((threadIdx.x & 31) == 0) {
-        xd[i >> 5] = d;
-        xs[i >> 5] = s;
+        xd[i >> 5] = r.d;
+        xs[i >> 5] = r.s;
     }
 }
 

@@ -1138,6 +1138,90 @@ __global__ __launch_bounds__(512) void mv1_kernel(MvParams p) {
     }
 }
 
+// Where a launch writes a two-stage input (xq, xq2: one byte per value; xd, xs: one float per 32 values),
+// and of which activation (NMQ_ACT_*: silu or gelu, rounded to bf16 or not; the MoE kernel: silu, bf16).
+struct QuantOut {
+    int8_t* xq;
+    int8_t* xq2;
+    float* xd;
+    float* xs;
+    int act;
+};
+
+// ---- gate and up of a dense FFN with the activation, one token (mvp_kernel) -----------------------------
+// Rows of the gate (tensor w) and up (tensor w2) projections in groups of 32: workgroup b takes groups b,
+// b + gridDim.x, ...  Waves 0..W/2-1 compute the groups' gate rows, W/2..W-1 their up rows, RPW rows per
+// group each, one row per step with the one-token kernel's hand-issued reads (64 lanes, one unit per lane:
+// rows of up to 4096 values) and NBUF - 1 steps in flight, across groups too.  A row's sum is the
+// persistent kernel's (acc = 0 + the unit's product, team_sum<64>), so every sum equals that row of the
+// gathered launch bit for bit.  The sums go to LDS as each group ends; no wave waits for another until
+// the last step.  Then (every read complete, one barrier) wave w takes groups w, w + W, ...: lanes 0..31
+// form a = act(g) * u (o.act: silu or gelu, rounded to bf16 or not; the expressions of the activation
+// launches) and write its two-stage input (quant32).  The group loop body is
+// straight-line code of RPW steps, RPW a multiple of NBUF, so the step buffers sit in the same registers
+// at every iteration.
+constexpr int MVP_MAXG = 16;  // groups per workgroup
+
+template <int F, int HR, int RPW>
+__global__ __launch_bounds__(4096 / RPW) void mvp_kernel(MvParams p, QuantOut o) {
+    static_assert(hand_format(F) && (HR == 1 || HR == 2), "hand-read formats; two-stage (1) or fp32 (2) input");
+    args_early<true>(p);
+    using FM = Fmt<F>;
+    using HS = HandStep<F, 1>;
+    constexpr int T = 64, NBUF = 4, W = 64 / RPW;  // W waves: 32 rows of each projection per group
+    static_assert(RPW % NBUF == 0, "the step buffers rotate through whole groups");
+    constexpr int HW = HS::NL * (NBUF - 1);
+    extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
+    __shared__ float res[MVP_MAXG][64];  // per group: the gate sums, then the up sums
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool up = wave >= W / 2;
+    const int wj = up ? wave - W / 2 : wave;
+    const RowMap rm = row_map<false>(p, up ? p.w2 : p.w, p.y);
+    const int U = (p.n_in + 63) >> 6;
+    const int nb = gridDim.x, G = p.n_out >> 5;
+    const int ng = (G - (int)blockIdx.x + nb - 1) / nb;  // this workgroup's groups (the launcher: 1..MVP_MAXG)
+    const int fb = (int)blockIdx.x * 32;                // a row of this workgroup (surplus reads go there)
+    // step q: row 32 (b + (q / RPW) nb) + RPW wj + q % RPW; past the last group the row is >= n_out and
+    // the read goes to row fb instead
+    auto row_of = [&](int q) { return ((int)blockIdx.x + (q / RPW) * nb) * 32 + wj * RPW + q % RPW; };
+    HS hb[NBUF];
+    auto issue = [&] {
+#pragma unroll
+        for (int i = 0; i < NBUF - 1; ++i) hb[i].template load<T>(rm, row_of(i), lane, U, fb);
+    };
+    if constexpr (HR == 1) stage1_hand<F, HW>(lds, tab, p, 0, issue);
+    else stagev_hand<F, HW>(lds, tab, p, 0, issue);
+    XSlice x[1];
+    read_slice<FM::STRIDED>(lds, p.ktp, min(lane, U - 1), x[0]);
+    const LaneConst lc = lane_const<F, T, 1>(lane, x);
+    float mine = 0.f;  // lane k: the k-th row of the wave's current group
+    for (int gi = 0; gi < ng; ++gi) {
+#pragma unroll
+        for (int k = 0; k < RPW; ++k) {
+            const int i = k % NBUF;
+            hb[(i + NBUF - 1) % NBUF].template load<T>(rm, row_of(gi * RPW + k + NBUF - 1), lane, U, fb);
+            hb[i].template wait<HW>();  // this step's reads; the later steps stay out
+            float acc = 0.f;
+            const float v = unit_dot1<F, true>(hb[i].raw[0], min(lane, U - 1), tab, x[0], lc, 0);
+            acc += lane < U ? v : 0.f;
+            acc = team_sum<T>(acc);
+            mine = lane == k ? acc : mine;
+        }
+        if (lane < RPW) res[gi][(up ? 32 : 0) + wj * RPW + lane] = mine;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the surplus reads of the last steps
+    lds_barrier();
+    for (int gi = wave; gi < ng; gi += W) {
+        if (lane < 32) {
+            const int64_t at = ((int64_t)blockIdx.x + (int64_t)gi * nb) * 32 + lane;
+            float v = act_value(res[gi][lane], (o.act & NMQ_ACT_GELU) != 0) * res[gi][32 + lane];
+            if (o.act & NMQ_ACT_BF16) v = round_bf16(v);
+            quant32_store(v, at, o.xq, o.xq2, o.xd, o.xs);
+        }
+    }
+}
+
 // ---- 2..4 tokens (speculative verification), Q4_K ----------------------------------------------------
 // The one-token kernel with hand-issued reads for NC tokens: all inputs staged in LDS (one round each,
 // read by hand ahead of the first weight steps), all slices held in registers, every weight unit
@@ -1439,13 +1523,6 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
 // two-stage input of a[s][r] = silu_mul_bf16(g[r], u[r]) for its 32 rows -- one group of the down
 // projection's input.  The gate and up outputs never leave the workgroup and the activation needs no
 // launch of its own.  Slot s reads input row s / x_group (the token).
-struct QuantOut {
-    int8_t* xq;
-    int8_t* xq2;
-    float* xd;
-    float* xs;
-};
-
 // Workgroup (group g, slot s) of the gate|up kernel; the rows of a projection on WH = 32 / (P*RW) waves (the
 // workgroup has 2*WH).  res: 64 floats of LDS.  Wave 0 writes the group's two-stage input.
 template <int F, int T, int RW>
@@ -2397,6 +2474,46 @@ int launch_moe_gu(MvParams p, QuantOut o, hipStream_t stream) {
                                   : (big ? moe_gu_kernel<F, 64, 8> : moe_gu_kernel<F, 64, 4>);
     hipLaunchKernelGGL(k, dim3((unsigned)(p.n_out / 32), (unsigned)p.n_ids), dim3(p.nt), lds, stream, p, o);
     return (int)hipGetLastError();
+}
+
+
+// ---- gate|up with the activation of a dense FFN (mvp_kernel) --------------------------------------------
+typedef void (*MvpKernel)(MvParams, QuantOut);
+
+// One launch: p.w gate, p.w2 up (n_out x n_in each), fp32 input values (NMQ_X_F32 / NMQ_X_F32_BF16; the
+// kernel also takes the two-stage input, HR = 1, which no entry point passes yet).  NMQ_ERR_SHAPE where
+// the kernel does not apply: other formats or input modes, rows of more than 4096 values, n_out not a
+// multiple of 32.  16 waves of 4 rows per group (NMQ_MVP_RPW = 4) or 8 of 8; workgroups: the fewest groups
+// per workgroup that the CUs allow, spread evenly (NMQ_MVP_WGS overrides).  Measured on MI355X, Llama-3-8B
+// gate|up 14336x4096 Q4_K: 14.3 us at 16 waves and 2 groups per workgroup (224 workgroups), 14.7 at 256
+// workgroups (1 or 2 groups), 18.4 at 448 (one each), 15.3 with 8 waves; the gathered launch alone takes
+// 14.4-14.5 us and with the activation launch after it 16.8-17.3.
+template <int F>
+int launch_mvp(MvParams p, QuantOut o, hipStream_t stream) {
+    if constexpr (!hand_format(F)) {
+        return NMQ_ERR_SHAPE;
+    } else {
+        using FM = Fmt<F>;
+        const DeviceInfo di = device_info();
+        const int U = (p.n_in + 63) / 64;
+        if (U > 64 || p.n_out % 32 || p.n_out < 32) return NMQ_ERR_SHAPE;
+        if (!p.xv || (p.x_mode != NMQ_X_F32 && p.x_mode != NMQ_X_F32_BF16)) return NMQ_ERR_SHAPE;
+        const int rpw = tune(TUNE_MVP_RPW, 4) == 8 ? 8 : 4;
+        p.nt = 64 * (64 / rpw);
+        p.nblk = p.n_in / FM::BV;
+        p.row_bytes = (int64_t)p.nblk * FM::BB;
+        p.ktp = (p.n_in + 127) / 128 * 128;
+        const size_t lds = (size_t)p.ktp * 9 / 4;
+        if (lds > (size_t)di.lds_max || p.ktp / 4 > 2 * p.nt) return NMQ_ERR_SHAPE;
+        const int G = p.n_out / 32;
+        const int per = (G + di.cus - 1) / di.cus;  // groups per workgroup
+        int nb = tune(TUNE_MVP_WGS, (G + per - 1) / per);
+        nb = nb < 1 ? 1 : (nb > G ? G : nb);
+        if ((G + nb - 1) / nb > MVP_MAXG) nb = (G + MVP_MAXG - 1) / MVP_MAXG;
+        const MvpKernel k = rpw == 8 ? mvp_kernel<F, 2, 8> : mvp_kernel<F, 2, 4>;
+        hipLaunchKernelGGL(k, dim3((unsigned)nb), dim3(p.nt), lds, stream, p, o);
+        return (int)hipGetLastError();
+    }
 }
 
 }  // namespace nmq

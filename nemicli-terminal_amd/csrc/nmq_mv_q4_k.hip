@@ -6,5 +6,6 @@ namespace nmq {
 template int launch_mv<NMQ_Q4_K>(MvParams, int, int, hipStream_t);
 template int launch_moe_down<NMQ_Q4_K>(MvParams, Combine, int, hipStream_t);
 template int launch_moe_gu<NMQ_Q4_K>(MvParams, QuantOut, hipStream_t);
+template int launch_mvp<NMQ_Q4_K>(MvParams, QuantOut, hipStream_t);
 template int launch_mmh<NMQ_Q4_K>(MmhParams, hipStream_t);
 }  // namespace nmq

@@ -5,4 +5,5 @@ namespace nmq {
 template int launch_mv<NMQ_Q8_0>(MvParams, int, int, hipStream_t);
 template int launch_moe_down<NMQ_Q8_0>(MvParams, Combine, int, hipStream_t);
 template int launch_moe_gu<NMQ_Q8_0>(MvParams, QuantOut, hipStream_t);
+template int launch_mvp<NMQ_Q8_0>(MvParams, QuantOut, hipStream_t);
 }  // namespace nmq

@@ -20,6 +20,7 @@ LIB_PATH = os.path.abspath(os.path.join(HERE, "..", "libnmq.so"))
 
 NMQ_OK, NMQ_ERR_FORMAT, NMQ_ERR_SHAPE, NMQ_ERR_ARG, NMQ_ERR_DEVICE = 0, -1, -2, -3, -4
 X_BF16, X_F32, X_F32_BF16, X_SILU_MUL_BF16 = 0, 1, 2, 3   # include/nmq.h NMQ_X_*
+ACT_SILU, ACT_GELU, ACT_BF16 = 0, 1, 2                    # include/nmq.h NMQ_ACT_*
 X_MAX_N_IN = 16384
 ABI_VERSION = 2
 MAX_COLS = 8
@@ -74,6 +75,8 @@ def _bind(L: ctypes.CDLL) -> ctypes.CDLL:
     L.nmq_moe_layer_work_bytes.argtypes, L.nmq_moe_layer_work_bytes.restype = [i, i, i, i, p], i
     L.nmq_moe_layer.argtypes = [i, p, p, i64, i, p, i64, p, p, i, i, p, i, p, i, i, p, i64, p]
     L.nmq_moe_layer.restype = i
+    L.nmq_mv_gate_up_act.argtypes = [i, p, p, p, i, i, p, p, p, p, i, i, p]
+    L.nmq_mv_gate_up_act.restype = i
     L.nmq_stream_read.argtypes, L.nmq_stream_read.restype = [p, i64, p, i, i, i, p], i
     L.nmq_set_tuning.argtypes, L.nmq_set_tuning.restype = [ctypes.c_char_p, i], i
     L.nmq_get_tuning.argtypes, L.nmq_get_tuning.restype = [ctypes.c_char_p, p], i

@@ -133,7 +133,7 @@ def test_moe_layer_stages(nmq, oracle, L):
                                   oracle.round_bf16(act_o[i:i + 1].astype(np.float32)))[0]
                     for i, (_, _, e) in enumerate(pairs)])
     full = (y_o.reshape(L, k, E) * wts[:, :, None]).sum(1)
-    assert oracle.rel_err_rows(out, full).max() <= 1e-2
+    assert oracle.rel_err_rows(out, full).max() <= 2e-3
 
 
 # ---- fused entry points of the expert layer --------------------------------------------------------------
@@ -184,9 +184,19 @@ def test_silu_mul_quant(nmq, oracle):
     rec = xq * d + xq2 * d / 254.0
     step = np.abs(act.astype(np.float64)) * 2.0 ** -8
     assert np.all(np.abs(rec - act) <= d / 508.0 + step + 1e-30)
-    # and in nearly every group bit for bit
+    # and bit for bit in every group whose bf16 activations the device's expf cannot move: the fp32 value
+    # silu(g) * u here and on the device differ by a few ulp at most (expf against numpy's exp, then the
+    # correctly rounded division and product), so a group whose values all round to the same bf16 value
+    # anywhere within 4 ulp of numpy's must match exactly
+    pre = (g / (np.float32(1) + np.exp(-g, dtype=np.float32)) * u).astype(np.float32)
+    lo, hi = pre.copy(), pre.copy()
+    for _ in range(4):
+        lo = np.nextafter(lo, np.float32(-np.inf))
+        hi = np.nextafter(hi, np.float32(np.inf))
+    fixed = ~(oracle.round_bf16(lo) != oracle.round_bf16(hi)).reshape(-1, 32).any(1)
     same = (np.all((xq == rxq).reshape(-1, 32), 1) & np.all((xq2 == rxq2).reshape(-1, 32), 1) & (xd == rxd) & (xs == rxs))
-    assert same.mean() >= 0.99, same.mean()
+    assert fixed.mean() >= 0.99, fixed.mean()
+    assert np.all(same[fixed]), np.flatnonzero(fixed & ~same)
     assert np.all(xq[:32] == 0) and xd[0] == 0.0
 
 

@@ -754,3 +754,83 @@ def test_few_tokens_long_rows_equal_one_by_one(nmq, oracle, shape, nc):
     for t in range(nc):
         assert torch.equal(yn[t], ys[t]), (shape, nc, t)
     _check_mv(oracle, "Q6_K", raw, n_out, n_in, x, yn)
+
+
+# ---- dense gate|up with the activation (nmq_mv_gate_up_act) ----------------------------------------------------
+
+# (format, n_out, n_in, knobs): the Llama-3-8B shape, 8 and 4 rows per wave, several groups per workgroup
+GATE_UP_ACT = [("Q4_K", 14336, 4096, {}), ("Q4_K", 14336, 4096, {"MVP_RPW": 4}),
+               ("Q4_K", 14336, 4096, {"MVP_WGS": 7}), ("Q4_K", 1024, 2048, {}), ("Q4_K", 320, 1024, {"MVP_WGS": 3}),
+               ("TQ2_0", 4096, 4096, {}), ("TQ2_0", 2048, 1536, {"MVP_RPW": 4, "MVP_WGS": 9}),
+               ("IQ2_XXS", 4096, 4096, {}), ("IQ2_XXS", 1536, 2048, {"MVP_WGS": 11})]
+
+
+@pytest.mark.parametrize("fmt,n_out,n_in,knobs", GATE_UP_ACT)
+def test_gate_up_act_equals_two_launches(nmq, oracle, tune, fmt, n_out, n_in, knobs):
+    """nmq_mv_gate_up_act (gate and up rows of 32-row groups in one workgroup, the activation and its
+    two-stage input in the same launch) equals nmq_mv_x on both matrices followed by nmq_akt_q8 (silu, gelu)
+    or nmq_silu_mul_quant (silu rounded to bf16), bit for bit, for fp32 input with and without the bf16
+    rounding; and the activation against the oracle."""
+    from ggufengine_amd import mmvq
+    from ggufengine_amd.gguf_types import TYPE_ID
+    tune(**knobs)
+    Lb = nmq.lib()
+    rawg = random_blocks(fmt, n_out * n_in // BV[fmt], seed=401 + n_out)
+    rawu = random_blocks(fmt, n_out * n_in // BV[fmt], seed=402 + n_out)
+    A, B = dev(rawg), dev(rawu)
+    rng = np.random.default_rng(403 + n_in)
+    x = dev(rng.standard_normal(n_in).astype(np.float32))
+    t = TYPE_ID[fmt]
+    a = torch.empty(n_out, device="cuda")
+    say("gate_up_act", fmt, n_out, n_in, knobs)
+    for mode, act in ((nmq.X_F32, nmq.ACT_SILU), (nmq.X_F32_BF16, nmq.ACT_SILU), (nmq.X_F32, nmq.ACT_GELU),
+                      (nmq.X_F32_BF16, nmq.ACT_SILU | nmq.ACT_BF16)):
+        y = torch.full((2, n_out), float("nan"), device="cuda")
+        nmq.check(Lb.nmq_mv_x(t, 2, (ctypes.c_void_p * 2)(A.data_ptr(), B.data_ptr()), (ctypes.c_int * 2)(n_out, n_out),
+                              (ctypes.c_void_p * 2)(y[0].data_ptr(), y[1].data_ptr()), x.data_ptr(), mode, None, n_in,
+                              nmq.stream_ptr()))
+        want = mmvq.Eingang(n=n_out, device=torch.device("cuda"))
+        wp = (want.xq.data_ptr(), want.xq2.data_ptr(), want.xd.data_ptr(), want.xs.data_ptr())
+        if act & nmq.ACT_BF16:
+            nmq.check(Lb.nmq_silu_mul_quant(y[0].data_ptr(), y[1].data_ptr(), *wp, n_out, nmq.stream_ptr()))
+        else:
+            nmq.check(Lb.nmq_akt_q8(y[0].data_ptr(), y[1].data_ptr(), act & nmq.ACT_GELU, a.data_ptr(), *wp, n_out,
+                                    nmq.stream_ptr()))
+        got = mmvq.Eingang(n=n_out, device=torch.device("cuda"))
+        for b in (got.xq, got.xq2):
+            b.fill_(77)
+        for b in (got.xd, got.xs):
+            b.fill_(float("nan"))
+        nmq.check(Lb.nmq_mv_gate_up_act(t, A.data_ptr(), B.data_ptr(), x.data_ptr(), mode, act, got.xq.data_ptr(),
+                                        got.xq2.data_ptr(), got.xd.data_ptr(), got.xs.data_ptr(), n_out, n_in,
+                                        nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        for f in ("xq", "xq2", "xd", "xs"):
+            assert torch.equal(getattr(got, f), getattr(want, f)), (f, mode, act)
+        if mode == nmq.X_F32 and act == nmq.ACT_SILU:
+            # the activation against the oracle's products
+            g = oracle.mv_deq(fmt, rawg, n_out, n_in, x.cpu().numpy()[None])[0]
+            u = oracle.mv_deq(fmt, rawu, n_out, n_in, x.cpu().numpy()[None])[0]
+            ref = oracle.akt(g, u)
+            xd = np.repeat(got.xd.cpu().numpy().astype(np.float64), 32)
+            rec = xd * (got.xq.cpu().numpy() + got.xq2.cpu().numpy() / 254.0)
+            assert np.max(np.abs(rec - ref)) <= 2e-3 * np.abs(ref).max()
+
+
+def test_gate_up_act_refuses_what_it_does_not_take(nmq):
+    from ggufengine_amd.gguf_types import TYPE_ID
+    Lb = nmq.lib()
+    a = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(4096, device="cuda")
+    q = torch.zeros(4096, dtype=torch.int8, device="cuda")
+    f = torch.zeros(128, device="cuda")
+
+    def call(fmt, n_out, n_in, mode, act=0):
+        return Lb.nmq_mv_gate_up_act(fmt, a.data_ptr(), a.data_ptr(), x.data_ptr(), mode, act, q.data_ptr(),
+                                     q.data_ptr(), f.data_ptr(), f.data_ptr(), n_out, n_in, nmq.stream_ptr())
+    assert call(TYPE_ID["Q6_K"], 64, 1024, nmq.X_F32) == nmq.NMQ_ERR_SHAPE   # not a hand-read format
+    assert call(TYPE_ID["Q4_K"], 48, 1024, nmq.X_F32) == nmq.NMQ_ERR_SHAPE   # groups of 32 rows
+    assert call(TYPE_ID["Q4_K"], 64, 8192, nmq.X_F32) == nmq.NMQ_ERR_SHAPE   # rows over 4096 values
+    assert call(TYPE_ID["Q4_K"], 64, 1024, nmq.X_BF16) == nmq.NMQ_ERR_SHAPE  # fp32 input only
+    assert call(TYPE_ID["Q4_K"], 64, 1024, nmq.X_F32, 4) == nmq.NMQ_ERR_ARG  # unknown activation
+    torch.cuda.synchronize()

@@ -1,4 +1,5 @@
-"""The one-token kernels with hand-issued reads (mv1_kernel<..., HR = 1 or 2>: Q4_K, TQ2_0, IQ2_XXS) rely on the
+"""The one-token kernels with hand-issued reads (mv1_kernel<..., HR = 1 or 2>, mvt_kernel, mvp_kernel: Q4_K, TQ2_0,
+IQ2_XXS; mvk_kernel, mvd_kernel) rely on the
 compiler never touching a register whose read is still outstanding: the compiler does not see those
 reads, so a copy of such a register (which it could place at a branch join or to split a live range)
 would silently take a stale value.  This test compiles the sources to gfx950 assembly and checks,
@@ -16,6 +17,8 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(REPO, "nemicli-terminal_amd", "csrc")
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 HAND_KERNEL = re.compile(r"^(_ZN3nmq10mv1_kernel\w*Li[12]EEEvNS_8MvParamsE|_ZN3nmq10mvt_kernel\w*EEEvNS_8MvParamsE):", re.M)
+# the dense gate|up kernel with the activation (fp32 input, 8 or 4 rows per wave and group)
+PAIR_KERNEL = re.compile(r"^(_ZN3nmq10mvp_kernel\w*EEEvNS_8MvParamsENS_8QuantOutE):", re.M)
 
 
 def _vregs(op):
@@ -111,8 +114,14 @@ def test_hand_read_kernels_exist(asm, src):
 
 @pytest.mark.parametrize("src", SOURCES)
 def test_no_access_to_registers_of_outstanding_reads(asm, src):
-    bad = [h for n in HAND_KERNEL.findall(asm[src]) + KSPLIT_KERNEL.findall(asm[src]) for h in hazards(asm[src], n)]
+    names = HAND_KERNEL.findall(asm[src]) + KSPLIT_KERNEL.findall(asm[src]) + PAIR_KERNEL.findall(asm[src])
+    bad = [h for n in names for h in hazards(asm[src], n)]
     assert not bad, bad[:5]
+
+
+@pytest.mark.parametrize("src", SOURCES[:3])
+def test_pair_kernels_exist(asm, src):
+    assert len(PAIR_KERNEL.findall(asm[src])) == 2, PAIR_KERNEL.findall(asm[src])
 
 
 @pytest.mark.parametrize("src", ["nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_q6_k.hip"])
@@ -184,7 +193,7 @@ def test_hand_read_kernels_use_no_scratch(asm, src):
     """Kernels with hand-issued reads keep everything in registers: a value the compiler parks in scratch
     memory comes back through reads and waits of its own among the hand-issued ones."""
     text = asm[src]
-    names = HAND_KERNEL.findall(text) + KSPLIT_KERNEL.findall(text) + DMA_KERNEL.findall(text)
+    names = HAND_KERNEL.findall(text) + KSPLIT_KERNEL.findall(text) + DMA_KERNEL.findall(text) + PAIR_KERNEL.findall(text)
     bad = []
     for n in names:
         body = text[text.index(n + ":"):]

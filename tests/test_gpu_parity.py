@@ -70,6 +70,43 @@ def test_quant_q8_bitexact(nmq, oracle, dtype):
         assert np.array_equal(host(g).view(np.uint8), np.ascontiguousarray(r).view(np.uint8)), name
 
 
+def test_quant_q8_ties_and_tiny_scales(nmq, oracle):
+    """Groups whose quotients v / d fall exactly on half-integers (d = 2^k: max = 127 * 2^k), within an ulp
+    of them, and groups with a scale below 2^-100 (the reciprocal-product shortcut does not apply there):
+    the two-stage input equals the oracle's (IEEE division, round half to even) bit for bit, from
+    nmq_quant_q8 and from the value staging of a mat-vec (nmq_mv_x against nmq_mv on that input)."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    rng = np.random.default_rng(17)
+    groups = []
+    for k in range(-6, 7):
+        d = np.float32(2.0 ** k)
+        half = (rng.integers(-126, 126, 31) + 0.5).astype(np.float32) * d
+        g = np.concatenate([[np.float32(127) * d], half]).astype(np.float32)
+        groups += [g, np.nextafter(g, np.float32(np.inf)), np.nextafter(g, np.float32(-np.inf))]
+    for sc in (1e-38, 1e-33, 2.0 ** -110):
+        groups.append((rng.standard_normal(32) * sc).astype(np.float32))
+    x = np.concatenate(groups).astype(np.float32)
+    n = (x.size + 255) // 256 * 256
+    x = np.concatenate([x, (rng.standard_normal(n - x.size) * 3).astype(np.float32)])
+    say("quant_q8 ties", n)
+    e = quant_dev(torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    for name, g, r in zip(("xq", "xq2", "xd", "xs"), (e.xq, e.xq2, e.xd, e.xs), oracle.quant_q8(x)):
+        assert np.array_equal(host(g).view(np.uint8), np.ascontiguousarray(r).view(np.uint8)), name
+    raw = random_blocks("Q4_K", 64 * n // 256, seed=18)
+    w = dev(raw)
+    y1 = torch.full((64,), float("nan"), device="cuda")
+    y2 = torch.full((64,), float("nan"), device="cuda")
+    L = nmq.lib()
+    xd_ = dev(x)
+    nmq.check(L.nmq_mv_x(TYPE_ID["Q4_K"], 1, (ctypes.c_void_p * 1)(w.data_ptr()), (ctypes.c_int * 1)(64),
+                         (ctypes.c_void_p * 1)(y1.data_ptr()), xd_.data_ptr(), nmq.X_F32, None, n, nmq.stream_ptr()))
+    nmq.check(L.nmq_mv(TYPE_ID["Q4_K"], w.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(),
+                       e.xs.data_ptr(), y2.data_ptr(), 64, n, 1, nmq.stream_ptr()))
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
 # ---- integer sums --------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("fmt", FMTS)

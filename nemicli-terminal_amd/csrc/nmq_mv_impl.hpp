@@ -343,6 +343,48 @@ __device__ __forceinline__ void stagev_load(VRound& r, int rnd, const void* x, c
     }
 }
 
+// The two stages of a lane's four values v in a group of scale d (0: an all-zero group):
+// q = rint(v / d), q2 = rint((v - q d) / (d FEIN)) clamped to +-127, every quotient the IEEE one.  For
+// d >= 2^-100 the product t = v * rcp(d) (v_rcp_f32: 1 ulp) lies within 128 * 1.5 * 2^-23 of the exact
+// quotient and the IEEE quotient within 128 * 2^-24, so where t is more than 2^-14 from the half-integer
+// between its neighbours both round to the same integer (the test below may see the unrounded product;
+// the difference, half an ulp of t, is inside the slack).  Only a wave with a lane next to such a
+// half-integer, or with a scale below 2^-100, divides (one scalar branch per stage).
+__device__ __forceinline__ void quant4(const float (&v)[4], float d, int (&q)[4], int (&q2)[4]) {
+    const bool small = d > 0.0f && !(d >= 0x1p-100f);
+    const float rd = __builtin_amdgcn_rcpf(d);
+    float t[4];
+    bool near = small;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        t[e] = v[e] * rd;
+        near |= fabsf(t[e] - floorf(t[e]) - 0.5f) <= 0x1p-14f;
+    }
+    if (__builtin_amdgcn_ballot_w64(near) != 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t[e] = v[e] / d;
+    }
+    const float b = d * FEIN, rb = __builtin_amdgcn_rcpf(b);
+    float r[4], t2[4];
+    bool near2 = small;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        q[e] = d > 0.0f ? (int)rintf(t[e]) : 0;
+        r[e] = fmaf(-(float)q[e], d, v[e]);
+        t2[e] = r[e] * rb;
+        near2 |= fabsf(t2[e] - floorf(t2[e]) - 0.5f) <= 0x1p-14f;
+    }
+    if (__builtin_amdgcn_ballot_w64(near2) != 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) t2[e] = r[e] / b;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int k = (int)rintf(t2[e]);
+        q2[e] = d > 0.0f ? (k < -127 ? -127 : (k > 127 ? 127 : k)) : 0;
+    }
+}
+
 template <bool STRIDED>
 __device__ __forceinline__ void stagev_store(const VRound& r, int rnd, u8* lds, int mode, int n_in, int ktp, int nt) {
     const int j = rnd * nt + (int)threadIdx.x;
@@ -362,18 +404,13 @@ __device__ __forceinline__ void stagev_store(const VRound& r, int rnd, u8* lds, 
     m = fmaxf(m, dpp_f<0x4E>(m));  // quad_perm 2,3,0,1: lane ^ 2
     m = fmaxf(m, dpp_f<0xB1>(m));  // quad_perm 1,0,3,2: lane ^ 1
     const float d = m / 127.0f;
+    int q[4], q2[4];
+    quant4(v, d, q, q2);
     u32 pq = 0u, pq2 = 0u;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        int q = 0, q2 = 0;
-        if (d > 0.0f) {
-            q = (int)rintf(v[e] / d);
-            const float rr = fmaf(-(float)q, d, v[e]);
-            q2 = (int)rintf(rr / (d * FEIN));
-            q2 = q2 < -127 ? -127 : (q2 > 127 ? 127 : q2);
-        }
-        pq |= ((u32)q & 0xffu) << (8 * e);
-        pq2 |= ((u32)q2 & 0xffu) << (8 * e);
+        pq |= ((u32)q[e] & 0xffu) << (8 * e);
+        pq2 |= ((u32)q2[e] & 0xffu) << (8 * e);
     }
     float a[4];
 #pragma unroll

@@ -1527,6 +1527,9 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
     const int U = (p.n_in + 63) >> 6;
     const int lr = (wj * P + team) * RW;  // the team's first row in the block
     const int r0 = blockIdx.x * R + lr;
+    // the token's slot weights, read now so that the combine at the end does not wait for memory
+    __shared__ float wt[16];
+    const float wv = (int)threadIdx.x < c.k ? gp<float>(c.w)[(int64_t)t * c.k + threadIdx.x] : 0.f;
     Mv1Step<F, T, RW, 1> a;
     MvParams q = p;  // the token's k input rows as one row of k*n_in values
     q.n_in = p.n_in * c.k;
@@ -1541,8 +1544,8 @@ __global__ __launch_bounds__(1024) void moe_down_kernel(MvParams p, Combine c) {
 #pragma unroll
         for (int rr = 0; rr < RW; ++rr) res[j * R + lr + rr] = acc[rr];
     }
+    if ((int)threadIdx.x < c.k) wt[threadIdx.x] = wv;
     lds_barrier();
-    const float* wt = c.w + (int64_t)t * c.k;
     for (int r = (int)threadIdx.x; r < R; r += p.nt) {
         const int row = blockIdx.x * R + r;
         if (row >= p.n_out) break;

@@ -329,6 +329,28 @@ def akt_q8(g: torch.Tensor, u: Optional[torch.Tensor], gelu: bool):
     return a, e
 
 
+def gate_up_akt(fmt: str, raw_gate: torch.Tensor, raw_up: torch.Tensor, x: torch.Tensor, n_out: int, n_in: int,
+                gelu: bool = False) -> Eingang:
+    """The FFN's gate and up mat-vecs on one token and act(gate) * up as the down projection's Eingang
+    (reference models/baukasten.py:217-241: mv on gate and up, then akt_q8): one launch where the library
+    takes the shape (nmq_mv_gate_up_act: Q4_K, TQ2_0, IQ2_XXS, rows of at most 4096 values, n_out % 32 == 0,
+    an fp32 input), bit for bit mv_mehrere + akt_q8; otherwise those two calls."""
+    dev = raw_gate.device
+    xf = _f32(x)
+    if xf.numel() != n_in:
+        raise ValueError(f"gate_up_akt: one token of {n_in} values expected, the input holds {xf.numel()}")
+    e = Eingang(n=n_out, device=dev)
+    rc = _native.lib().nmq_mv_gate_up_act(TYPE_ID[fmt], raw_gate.data_ptr(), raw_up.data_ptr(), xf.data_ptr(),
+                                          _native.X_F32, _native.ACT_GELU if gelu else _native.ACT_SILU,
+                                          e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(),
+                                          n_out, n_in, _native.stream_ptr(dev))
+    if rc != _native.NMQ_ERR_SHAPE:
+        _native.check(rc)
+        return e
+    g, u = mv_mehrere(fmt, [raw_gate, raw_up], xf, [n_out, n_out], n_in)
+    return akt_q8(g, u, gelu)[1]
+
+
 def schritt_moeglich(device, H: int, Hkv: int, D: int) -> bool:
     """The whole fused one-token step also needs rope_kv and attention1, which are not part of this
     library: always False, so callers run their general layer path (reference mmvq.py:1009-1014,

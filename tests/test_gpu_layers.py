@@ -862,6 +862,24 @@ def test_moe_gate_up_graph_replays(nmq):
 
 
 
+
+@pytest.mark.parametrize("fmt,n_out,n_in,gelu", [("Q4_K", 14336, 4096, False), ("Q4_K", 1024, 2048, True),
+                                                 ("Q6_K", 1024, 2048, False)])
+def test_gate_up_akt_equals_mv_and_akt(nmq, fmt, n_out, n_in, gelu):
+    """mmvq.gate_up_akt (one launch for Q4_K; Q6_K through mv_mehrere + akt_q8) gives the Eingang of
+    mv_mehrere on gate and up followed by akt_q8, bit for bit."""
+    from ggufengine_amd import mmvq
+    A = dev(random_blocks(fmt, n_out * n_in // 256, seed=501 + n_in))
+    B = dev(random_blocks(fmt, n_out * n_in // 256, seed=502 + n_in))
+    x = dev(np.random.default_rng(503).standard_normal(n_in).astype(np.float32))
+    say("gate_up_akt", fmt, n_out, n_in, gelu)
+    got = mmvq.gate_up_akt(fmt, A, B, x, n_out, n_in, gelu)
+    g, u = mmvq.mv_mehrere(fmt, [A, B], x, [n_out, n_out], n_in)
+    want = mmvq.akt_q8(g, u, gelu)[1]
+    torch.cuda.synchronize()
+    for f in ("xq", "xq2", "xd", "xs"):
+        assert torch.equal(getattr(got, f), getattr(want, f)), f
+
 # ---- the whole expert layer (nmq_moe_layer) ------------------------------------------------------------------
 
 def _layer_case(fg, fd, n_exp, E, FF, seed):

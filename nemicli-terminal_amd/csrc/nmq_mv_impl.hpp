@@ -2200,13 +2200,18 @@ inline MvKernel pick_mvc(int T, int rw, bool ext) {
 // values: the launch forms the input from values in its staging (more rounds the fewer threads a
 // workgroup has), else it reads the two-stage input.
 inline Mv1Shape plan_mvc(int n_out, int n_in, int n_mats, const DeviceInfo& di, bool values = true,
-                          bool four_rows = false) {
+                          bool four_rows = false, bool wide_tab = false) {
     Mv1Shape s{};
     const int U = (n_in + 63) / 64;
     s.T = U <= 16 ? 16 : (U <= 32 ? 32 : 64);
     if (U > s.T) return s;  // one unit per lane only
     const int P = 64 / s.T;
-    const int wg_per_cu = tune(TUNE_MVC_WGPC, 1);
+    // two-stage input, formats without the four-row teams (Q8_0, Q4_0, Q6_K), at least 16 rows per CU: 4
+    // workgroups per CU (measured on MI355X, one token: 4096x4096 Q8_0 6.15 -> 5.66 us, Q4_0 5.16 -> 4.54,
+    // Q6_K 5.90 -> 5.14; 6144x4096 Q8_0 8.24 -> 7.30; but 1024x4096 Q8_0 2.92 -> 3.86, so not below 16 rows
+    // per CU; IQ2_XXS 4096x4096 4.22 against 4.40)
+    const bool quad = !values && !four_rows && !wide_tab && (int64_t)n_out * n_mats >= (int64_t)16 * di.cus;
+    const int wg_per_cu = tune(TUNE_MVC_WGPC, quad ? 4 : 1);
     int64_t wgs = (int64_t)di.cus * wg_per_cu / n_mats;
     if (wgs < 1) wgs = 1;
     const int64_t R = ((int64_t)n_out + wgs - 1) / wgs;  // rows per workgroup
@@ -2338,7 +2343,8 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     const int mvc_max = tune(TUNE_MVC_ROWS, n_mats > 1 ? 64 : 24);
     const int mode = tune(TUNE_MV1_MODE, rows_per_cu > mvc_max ? 2 : 1);
     if (nc == 1 && mode == 1) {
-        const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di, p.xv != nullptr, F == NMQ_Q4_K || F == NMQ_TQ2_0);
+        const Mv1Shape sc = plan_mvc(p.n_out, p.n_in, n_mats, di, p.xv != nullptr, F == NMQ_Q4_K || F == NMQ_TQ2_0,
+                                     F == NMQ_IQ2_XXS);
         if (sc.ok) {
             p.ktp = sc.ktp;
             MvKernel k = pick_mvc<F>(sc.T, sc.rw, ext);

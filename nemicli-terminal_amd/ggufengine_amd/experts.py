@@ -251,12 +251,32 @@ class ExpertenLager:
         return int(coming.numel())
 
 
-def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float = 1.0
-            ) -> Tuple[torch.Tensor, torch.Tensor]:
-    """Softmax router (reference baukasten.py:171-190, softmax gating, no groups):
-    logits (L, n_exp) -> (ids (L, k) int64, weights (L, k) float32)."""
-    p = torch.softmax(logits.float(), dim=-1)
-    idx = p.topk(k, dim=-1)[1]
+def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float = 1.0, sigmoid: bool = False,
+            wahl_bias: Optional[torch.Tensor] = None, n_group: int = 1, group_used: int = 1,
+            nach_auswahl: bool = False) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Router of a MoE layer (reference baukasten.py:156-190): logits (L, n_exp) -> (ids (L, k) int64,
+    weights (L, k) float32).
+    - nach_auswahl: the k largest logits, their softmax as the weights (softmax after the selection).
+    - otherwise p = softmax(logits) (or sigmoid(logits) with `sigmoid`); the choice is made on
+      p + wahl_bias (a per-expert selection correction that the weights do not see); with n_group > 1 the
+      experts form n_group equal groups, and only the group_used groups with the best score (the group's
+      largest choice value; with sigmoid the sum of its two largest) stay eligible.  The weights are p at
+      the chosen experts, divided by their sum when `normieren`, then times `scale`."""
+    x = logits.float()
+    if nach_auswahl:
+        top, idx = x.topk(k, dim=-1)
+        return idx, torch.softmax(top, dim=-1)
+    p = torch.sigmoid(x) if sigmoid else torch.softmax(x, dim=-1)
+    wahl = p if wahl_bias is None else p + wahl_bias.to(p.device, torch.float32)
+    if n_group > 1:
+        L_, n = wahl.shape
+        je = n // n_group
+        gruppen = wahl.view(L_, n_group, je)
+        wert = gruppen.topk(min(2, je), dim=-1)[0].sum(-1) if sigmoid else gruppen.amax(-1)
+        offen = torch.zeros(L_, n_group, dtype=torch.bool, device=wahl.device)
+        offen.scatter_(1, wert.topk(group_used, dim=-1)[1], True)
+        wahl = wahl.masked_fill(~offen.repeat_interleave(je, dim=1), float("-inf"))
+    idx = wahl.topk(k, dim=-1)[1]
     w = p.gather(-1, idx)
     if normieren:
         w = w / (w.sum(-1, keepdim=True) + 1e-20)
@@ -264,15 +284,58 @@ def auswahl(logits: torch.Tensor, k: int, normieren: bool = True, scale: float =
 
 
 class Experten:
-    """Expert MLP of a MoE layer, gate/up/down in block format (reference moe.py:252-321, silu gate)."""
+    """Expert MLP of a MoE layer in block format (reference moe.py:205-321): gate and up as two tensors or
+    fused as one [gate | up] tensor of 2*FF rows per expert, or up alone (act(up), no gate); down; an
+    optional bias per expert for each part ({"gate", "up", "gate_up", "down"}: (n_exp, width) fp32); the
+    activation `akt` ("silu", "gelu" for the tanh form, or a callable on fp32 tensors) or `glu(gate, up)`
+    combining both projections.  The silu-gated form without biases runs as nmq_moe_layer (two launches);
+    every other form through the gathered launches with the bias, activation and combine in torch."""
 
-    def __init__(self, gate: PackedExperts, up: PackedExperts, down: PackedExperts):
-        if not (gate.n_exp == up.n_exp == down.n_exp and gate.n_out == up.n_out == down.n_in
-                and gate.n_in == up.n_in == down.n_out):
+    def __init__(self, gate: Optional[PackedExperts], up: Optional[PackedExperts], down: PackedExperts,
+                 gate_up: Optional[PackedExperts] = None, bias: Optional[dict] = None, akt="silu", glu=None):
+        if gate_up is not None:
+            if gate is not None or up is not None:
+                raise GGUFError("Experten: either gate_up or gate/up")
+            ff = gate_up.n_out // 2
+            teile, n_in = [gate_up], gate_up.n_in
+            if gate_up.n_out != 2 * ff or ff != down.n_in:
+                raise GGUFError("Experten: the fused [gate | up] tensor needs 2 x the down projection's inputs")
+        else:
+            if up is None:
+                raise GGUFError("Experten: up (or gate_up) is required")
+            teile = [t for t in (gate, up) if t is not None]
+            ff, n_in = up.n_out, up.n_in
+            if any(t.n_out != ff or t.n_in != n_in for t in teile) or ff != down.n_in:
+                raise GGUFError("Experten: gate/up/down shapes do not fit together")
+        if down.n_out != n_in or any(t.n_exp != down.n_exp for t in teile):
             raise GGUFError("Experten: gate/up/down shapes do not fit together")
-        self.gate, self.up, self.down = gate, up, down
-        self.n_exp = gate.n_exp
+        self.gate, self.up, self.down, self.gate_up = gate, up, down, gate_up
+        self.n_exp, self.ff = down.n_exp, ff
+        breite = {"gate": ff, "up": ff, "gate_up": 2 * ff, "down": down.n_out}
+        self.bias = {}
+        for name, b in (bias or {}).items():
+            if name not in breite or tuple(b.shape) != (self.n_exp, breite[name]):
+                raise GGUFError(f"Experten: bias {name!r} of shape {tuple(b.shape)}")
+            self.bias[name] = b.float()
+        if isinstance(akt, str) and akt not in ("silu", "gelu"):
+            raise ValueError(f"Experten: activation {akt!r} (silu, gelu or a callable)")
+        self.akt, self.glu = akt, glu
         self._work: dict = {}
+
+    def _gate_up_quellen(self, dev):
+        """(format, gate pointer, up pointer, per_expert) for the fused launches, or None where they do not
+        apply (no gate, or a fused [gate | up] tensor read through an address table)."""
+        if self.gate_up is not None:
+            if self.gate_up.adressen is not None:
+                return None
+            gu = self.gate_up
+            raw, per = gu._quelle(dev)
+            _, bs, ts = GGML_TYPES[gu.ggml_type]
+            return gu.name, raw.data_ptr(), raw.data_ptr() + self.ff * (gu.n_in // bs) * ts, per
+        if self.gate is None or not self._fused():
+            return None
+        (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
+        return self.gate.name, wa.data_ptr(), wb.data_ptr(), per
 
     @staticmethod
     def _gu(h_gate: torch.Tensor, h_up: torch.Tensor) -> torch.Tensor:
@@ -284,29 +347,59 @@ class Experten:
 
     def __call__(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """x (L, E) -> (L, E) float32; idx (L, k) expert ids, w (L, k) their weights (reference
-        models/moe.py:264-277).  One call of nmq_moe_layer, two launches: gate|up with the activation
-        quantised in the same workgroups, then the down launch with the weighted combine on that input; for
-        more tokens the gathered gate|up launch into fp32, then the down launch forming the activation in its
-        staging.  (Rows longer than WERTE_BIS values, or a gate and up
-        of different layout: the input quantisations as launches of their own.)"""
+        models/moe.py:264-277).  The silu-gated form without biases is one call of nmq_moe_layer, two
+        launches: gate|up with the activation quantised in the same workgroups, then the down launch with the
+        weighted combine on that input; for more tokens the gathered gate|up launch into fp32, then the down
+        launch forming the activation in its staging.  (Rows longer than WERTE_BIS values, or a gate and up
+        of different layout: the input quantisations as launches of their own.)  Other forms: _allgemein."""
+        if self.bias or self.glu is not None or self.akt != "silu" or (self.gate is None and self.gate_up is None):
+            return self._allgemein(x, idx, w)
         L_, E = x.shape
         k = idx.shape[1]
         dev = x.device
-        if (not self._fused() or max(E, self.gate.n_out) > WERTE_BIS or x.dtype != torch.float32
-                or self.gate.n_out % 32):
+        q = self._gate_up_quellen(dev)
+        FF = self.ff
+        if q is None or max(E, FF) > WERTE_BIS or x.dtype != torch.float32 or FF % 32:
             return self._aufgeteilt(x, idx, w)
-        FF = self.gate.n_out
+        name, wa, wb, per = q
         flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
-        (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
         wd, perd = self.down._quelle(dev)
         out = torch.empty(L_, E, dtype=torch.float32, device=dev)
         wf = w.to(dev, torch.float32).contiguous()
         work = self._arbeitsplatz(L_, k, E, FF, dev)
-        _starten("moe_layer", _native.lib().nmq_moe_layer, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(), per,
-                 TYPE_ID[self.down.name], wd.data_ptr(), perd, flat.data_ptr(), wf.data_ptr(), L_, k,
-                 x.contiguous().data_ptr(), _native.X_F32_BF16, out.data_ptr(), E, FF, work.data_ptr(), work.numel(),
-                 _native.stream_ptr(dev))
+        _starten("moe_layer", _native.lib().nmq_moe_layer, TYPE_ID[name], wa, wb, per, TYPE_ID[self.down.name],
+                 wd.data_ptr(), perd, flat.data_ptr(), wf.data_ptr(), L_, k, x.contiguous().data_ptr(),
+                 _native.X_F32_BF16, out.data_ptr(), E, FF, work.data_ptr(), work.numel(), _native.stream_ptr(dev))
         return out
+
+    def _aktiviert(self, g: Optional[torch.Tensor], u: torch.Tensor) -> torch.Tensor:
+        """glu(gate, up), act(gate) * up, or act(up) without a gate (reference moe.py:252-255)."""
+        if self.glu is not None:
+            return self.glu(g, u)
+        akt = self.akt
+        f = F.silu if akt == "silu" else ((lambda t: F.gelu(t, approximate="tanh")) if akt == "gelu" else akt)
+        return f(u) if g is None else f(g) * u
+
+    def _allgemein(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """Every form of the layer: the gathered launches on each token's bf16 input (gate and up, or the
+        fused [gate | up] tensor, or up alone), each part's bias per expert added, the activation in torch,
+        the gathered down launch on each slot's activation (rounded to bf16 in the launch) plus its bias, and
+        the weighted sum over the slots (reference moe.py:264-277)."""
+        L_, E = x.shape
+        e = eingang_bf16(x)
+        flat = idx.reshape(-1).to(x.device, torch.int64).contiguous()
+
+        def mit_bias(name, y):
+            b = self.bias.get(name)
+            return y if b is None else y + b.to(y.device).index_select(0, flat)
+        if self.gate_up is not None:
+            gu = mit_bias("gate_up", self.gate_up.matvec_tokens(idx, e))
+            g, u = gu[:, :self.ff], gu[:, self.ff:]
+        else:
+            g = mit_bias("gate", self.gate.matvec_tokens(idx, e)) if self.gate is not None else None
+            u = mit_bias("up", self.up.matvec_tokens(idx, e))
+        y = mit_bias("down", self.down.matvec_je(flat, self._aktiviert(g, u).contiguous()))
+        return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)
 
     def _arbeitsplatz(self, L_: int, k: int, E: int, FF: int, dev) -> torch.Tensor:
         """nmq_moe_layer's workspace for L_ tokens of k slots: kept per layer and device, grown when needed."""
@@ -319,28 +412,24 @@ class Experten:
         return have
 
     def _aufgeteilt(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-        """The same layer with the inputs quantised by launches of their own (five launches when gate
-        and up share a layout, else the per-tensor path)."""
+        """The silu-gated layer with the inputs quantised by launches of their own (five launches when gate
+        and up share a layout or come fused, else _allgemein)."""
         L_, E = x.shape
         k = idx.shape[1]
-        if not self._fused():
-            e = eingang_bf16(x)
-            g = self.gate.matvec_tokens(idx, e)
-            u = self.up.matvec_tokens(idx, e)
-            y = self.down.matvec_je(idx.reshape(-1), self._gu(g, u))
-            return (y.view(L_, -1, E) * w.float().unsqueeze(-1)).sum(1)
-        L = _native.lib()
         dev = x.device
+        q = self._gate_up_quellen(dev)
+        if q is None:
+            return self._allgemein(x, idx, w)
+        name, wa, wb, per = q
+        L = _native.lib()
         st = _native.stream_ptr(dev)
         n = L_ * k
-        FF = self.gate.n_out
+        FF = self.ff
         e = eingang_bf16(x)
         flat = idx.reshape(-1).to(dev, torch.int64).contiguous()
         gu = torch.empty(2 * n, FF, dtype=torch.float32, device=dev)
-        (wa, per), (wb, _) = self.gate._quelle(dev), self.up._quelle(dev)
-        _starten("mv_experts2", L.nmq_mv_experts2, TYPE_ID[self.gate.name], wa.data_ptr(), wb.data_ptr(),
-                 flat.data_ptr(), n, per, e.xq.data_ptr(), e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k,
-                 gu.data_ptr(), FF, E, st)
+        _starten("mv_experts2", L.nmq_mv_experts2, TYPE_ID[name], wa, wb, flat.data_ptr(), n, per, e.xq.data_ptr(),
+                 e.xq2.data_ptr(), e.xd.data_ptr(), e.xs.data_ptr(), k, gu.data_ptr(), FF, E, st)
         a = Eingang(n=n * FF, device=dev)
         _starten("silu_mul_quant", L.nmq_silu_mul_quant, gu.data_ptr(), gu[n:].data_ptr(), a.xq.data_ptr(),
                  a.xq2.data_ptr(), a.xd.data_ptr(), a.xs.data_ptr(), n * FF, st)

@@ -341,6 +341,83 @@ def test_expert_layer_three_launches_equal_five(nmq, L):
     assert torch.equal(a, b)
 
 
+def _expert_parts(n_exp, E, FF, seed):
+    from ggufengine_amd import experts
+    g_raw = random_blocks("Q4_K", n_exp * FF * E // 256, seed=seed)
+    u_raw = random_blocks("Q4_K", n_exp * FF * E // 256, seed=seed + 1)
+    d_raw = random_blocks("Q6_K", n_exp * E * FF // 256, seed=seed + 2)
+    gu_raw = np.concatenate([g_raw.reshape(n_exp, -1), u_raw.reshape(n_exp, -1)], axis=1).reshape(-1)
+    P = experts.PackedExperts
+    return (g_raw, u_raw, d_raw, P(dev(g_raw), 12, n_exp, FF, E), P(dev(u_raw), 12, n_exp, FF, E),
+            P(dev(d_raw), 14, n_exp, E, FF), P(dev(gu_raw), 12, n_exp, 2 * FF, E))
+
+
+@pytest.mark.parametrize("L", [1, 4])
+def test_expert_layer_fused_gate_up_tensor(nmq, L):
+    """Experten on one [gate | up] tensor (2*FF rows per expert, as GGUF's ffn_gate_up_exps) equals the layer
+    on separate gate and up tensors bit for bit, in the two-launch and the five-launch forms."""
+    from ggufengine_amd import experts
+    n_exp, k, E, FF = 12, 8, 2048, 768
+    _, _, _, G, U, D, GU = _expert_parts(n_exp, E, FF, 601)
+    sep = experts.Experten(G, U, D)
+    fus = experts.Experten(None, None, D, gate_up=GU)
+    rng = np.random.default_rng(602 + L)
+    x = dev(rng.standard_normal((L, E)).astype(np.float32))
+    idx, w = experts.auswahl(dev(rng.standard_normal((L, n_exp)).astype(np.float32)), k)
+    say("expert layer fused gate_up", L)
+    a, b = sep(x, idx, w), fus(x, idx, w)
+    c, d = sep._aufgeteilt(x, idx, w), fus._aufgeteilt(x, idx, w)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
+
+
+@pytest.mark.parametrize("form", ["bias_gelu", "no_gate", "fused_bias_glu"])
+def test_expert_layer_general_forms(nmq, oracle, form):
+    """The layer's other forms (reference moe.py:205-277): per-expert biases with the tanh-gelu activation;
+    up alone (act(up)); the fused [gate | up] tensor with its bias and a custom glu.  Against the oracle:
+    gate/up products on the tokens' bf16 inputs, biases, the activation in fp64 rounded to bf16 (the down
+    launch's input), down products plus bias, the weighted sum; max relative error per row <= 2e-3."""
+    from ggufengine_amd import experts
+    n_exp, k, E, FF, L = 10, 4, 1024, 512, 3
+    g_raw, u_raw, d_raw, G, U, D, GU = _expert_parts(n_exp, E, FF, 611)
+    rng = np.random.default_rng(612)
+    bias = {n: (rng.standard_normal((n_exp, wd)) * 0.05).astype(np.float32)
+            for n, wd in (("gate", FF), ("up", FF), ("gate_up", 2 * FF), ("down", E))}
+    glu_t = lambda g, u: g * torch.sigmoid(1.702 * g) * (u + 1.0)
+    glu_n = lambda g, u: g / (1.0 + np.exp(-1.702 * g)) * (u + 1.0)
+    if form == "bias_gelu":
+        layer = experts.Experten(G, U, D, bias={n: dev(bias[n]) for n in ("gate", "up", "down")}, akt="gelu")
+    elif form == "no_gate":
+        layer = experts.Experten(None, U, D)
+    else:
+        layer = experts.Experten(None, None, D, gate_up=GU, bias={n: dev(bias[n]) for n in ("gate_up", "down")},
+                                 glu=glu_t)
+    x = rng.standard_normal((L, E)).astype(np.float32)
+    idx, w = experts.auswahl(dev(rng.standard_normal((L, n_exp)).astype(np.float32)), k)
+    say("expert layer form", form)
+    out = layer(dev(x), idx, w).cpu().numpy()
+    ids, wts = idx.cpu().numpy(), w.cpu().numpy().astype(np.float64)
+    xb = oracle.round_bf16(x)
+    ref = np.zeros((L, E))
+    for t in range(L):
+        for j in range(k):
+            e = int(ids[t, j])
+            g = oracle.mv_deq("Q4_K", _expert_rows(g_raw, "Q4_K", n_exp, FF, E, e), FF, E, xb[t:t + 1])[0]
+            u = oracle.mv_deq("Q4_K", _expert_rows(u_raw, "Q4_K", n_exp, FF, E, e), FF, E, xb[t:t + 1])[0]
+            if form == "bias_gelu":
+                a = oracle.akt(g + bias["gate"][e], u + bias["up"][e], gelu=True)
+            elif form == "no_gate":
+                a = oracle.akt(u)
+            else:
+                a = glu_n(g + bias["gate_up"][e, :FF], u + bias["gate_up"][e, FF:])
+            ab = oracle.round_bf16(a.astype(np.float32))
+            y = oracle.mv_deq("Q6_K", _expert_rows(d_raw, "Q6_K", n_exp, E, FF, e), E, FF, ab[None])[0]
+            if form != "no_gate":
+                y = y + bias["down"][e]
+            ref[t] += wts[t, j] * y
+    assert oracle.rel_err_rows(out, ref).max() <= 2e-3
+
+
 def test_llama3_8b_layer_full_size(nmq, oracle):
     """The mat-vecs of a full Llama-3-8B decoder layer at batch 1 (q, k, v, o, gate, up Q4_K; down Q6_K
     4096x14336), weights ~N(0, 0.02) quantised by the library's encoders, run as the layer runs them

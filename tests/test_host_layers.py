@@ -41,6 +41,64 @@ def test_router_scale_and_no_renormalisation():
     assert torch.allclose(w, 2.5 * p[:, [0, 2]])
 
 
+def _router_variant_restated(logits: np.ndarray, k: int, sigmoid: bool, bias, n_group: int, group_used: int):
+    """The router's variants written out per token with numpy: p = sigmoid or softmax; the choice on p + bias;
+    groups scored by their largest choice value (sigmoid: the sum of the two largest), the group_used best
+    kept; the k largest kept choices; weights p there, renormalised."""
+    z = logits.astype(np.float64)
+    if sigmoid:
+        p = 1.0 / (1.0 + np.exp(-z))
+    else:
+        p = np.exp(z - z.max(-1, keepdims=True))
+        p /= p.sum(-1, keepdims=True)
+    choice = p + (0.0 if bias is None else bias.astype(np.float64))
+    ids, ws = [], []
+    for t in range(z.shape[0]):
+        c = choice[t].copy()
+        if n_group > 1:
+            je = c.size // n_group
+            score = [np.sort(c[g * je:(g + 1) * je])[::-1][:min(2, je)].sum() if sigmoid else c[g * je:(g + 1) * je].max()
+                     for g in range(n_group)]
+            keep = set(np.argsort(-np.array(score), kind="stable")[:group_used].tolist())
+            for g in range(n_group):
+                if g not in keep:
+                    c[g * je:(g + 1) * je] = -np.inf
+        sel = np.argsort(-c, kind="stable")[:k]
+        wt = p[t, sel]
+        ids.append(sel)
+        ws.append(wt / (wt.sum() + 1e-20))
+    return np.array(ids), np.array(ws)
+
+
+@pytest.mark.parametrize("sigmoid,use_bias,n_group,group_used", [(True, True, 8, 4), (False, False, 4, 2),
+                                                                   (True, False, 1, 1), (False, True, 1, 1)])
+def test_router_variants(sigmoid, use_bias, n_group, group_used):
+    """Sigmoid gating, a selection bias the weights do not see, grouped selection (reference
+    baukasten.py:171-190) against the per-token restatement: the same experts, weights within 1e-6."""
+    rng = np.random.default_rng(7 + n_group)
+    logits = rng.standard_normal((5, 64)).astype(np.float32)
+    bias = (rng.standard_normal(64) * 0.3).astype(np.float32) if use_bias else None
+    idx, w = experts.auswahl(torch.from_numpy(logits), 6, sigmoid=sigmoid,
+                             wahl_bias=None if bias is None else torch.from_numpy(bias), n_group=n_group,
+                             group_used=group_used)
+    ridx, rw = _router_variant_restated(logits, 6, sigmoid, bias, n_group, group_used)
+    for t in range(5):
+        a = dict(zip(idx[t].tolist(), w[t].tolist()))
+        b = dict(zip(ridx[t].tolist(), rw[t].tolist()))
+        assert set(a) == set(b), t
+        assert all(abs(a[e] - b[e]) <= 1e-6 for e in a)
+    if n_group > 1:  # every chosen expert lies in one of group_used groups
+        je = 64 // n_group
+        assert all(len({e // je for e in row}) <= group_used for row in idx.tolist())
+
+
+def test_router_softmax_after_selection():
+    logits = torch.tensor([[0.5, 3.0, -1.0, 2.0, 1.0]])
+    idx, w = experts.auswahl(logits, 3, nach_auswahl=True)
+    assert idx.tolist() == [[1, 3, 4]]
+    assert torch.allclose(w, torch.softmax(torch.tensor([[3.0, 2.0, 1.0]]), -1))
+
+
 def test_block_layers_refuse_cpu_tensors():
     raw = torch.zeros(4 * 16 * 144, dtype=torch.uint8)
     with pytest.raises(RuntimeError):

@@ -27,9 +27,13 @@ from typing import Optional, Tuple
 import torch
 import torch.nn.functional as F
 
-from . import _native, cudakern, hostmem
+from . import _native, cudakern, hostmem, packed
 from .gguf_types import GGML_TYPES, GGUFError, TYPE_ID
 from .mmvq import WERTE_BIS, Eingang, _starten, _werte, eingang_bf16
+
+# (token, slot) pairs per expert (on average) from which Experten sorts them by expert and multiplies every
+# used expert's rows at once (one host read per layer, so not inside a graph capture)
+SORTIERT_AB = 4
 
 
 class PackedExperts:
@@ -321,6 +325,7 @@ class Experten:
             raise ValueError(f"Experten: activation {akt!r} (silu, gelu or a callable)")
         self.akt, self.glu = akt, glu
         self._work: dict = {}
+        self._matrizen: dict = {}
 
     def _gate_up_quellen(self, dev):
         """(format, gate pointer, up pointer, per_expert) for the fused launches, or None where they do not
@@ -352,6 +357,8 @@ class Experten:
         weighted combine on that input; for more tokens the gathered gate|up launch into fp32, then the down
         launch forming the activation in its staging.  (Rows longer than WERTE_BIS values, or a gate and up
         of different layout: the input quantisations as launches of their own.)  Other forms: _allgemein."""
+        if idx.numel() >= SORTIERT_AB * self.n_exp:
+            return self._sortiert(x, idx, w)
         if self.bias or self.glu is not None or self.akt != "silu" or (self.gate is None and self.gate_up is None):
             return self._allgemein(x, idx, w)
         L_, E = x.shape
@@ -379,6 +386,51 @@ class Experten:
         akt = self.akt
         f = F.silu if akt == "silu" else ((lambda t: F.gelu(t, approximate="tanh")) if akt == "gelu" else akt)
         return f(u) if g is None else f(g) * u
+
+    def _matrix(self, teil: str, e: int) -> packed.PackedLinear:
+        """Expert e of part `teil` as a matrix (its block bytes in place), kept for later calls."""
+        key = (teil, e)
+        m = self._matrizen.get(key)
+        if m is None:
+            t = getattr(self, teil)
+            m = packed.PackedLinear(t.raw[e], t.ggml_type, t.n_out, t.n_in, dtype=torch.float32)
+            self._matrizen[key] = m
+        return m
+
+    def _sortiert(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+        """Many tokens (reference moe.py:290-321): the (token, slot) pairs sorted by expert, every used expert's
+        rows multiplied at once as a matrix (PackedLinear's dispatch by row count: the int8 mat-vec kernels,
+        the matrix cores, or unpacked weights), one host read of the per-expert counts, the results put back
+        in (token, slot) order and summed there in a fixed order."""
+        L_, E = x.shape
+        k = idx.shape[1]
+        flat = idx.reshape(-1).to(x.device, torch.int64)
+        folge = flat.sort(stable=True)[1]
+        xs = x.to(torch.bfloat16).float()[folge // k]   # the gathered launches' bf16 input
+        anzahl = torch.bincount(flat, minlength=self.n_exp).tolist()
+        ys = torch.empty(L_ * k, E, dtype=torch.float32, device=x.device)
+        a = 0
+        for e, c in enumerate(anzahl):
+            if not c:
+                continue
+            sl = slice(a, a + c)
+            a += c
+            xe = xs[sl]
+
+            def mit_bias(name, y):
+                b = self.bias.get(name)
+                return y if b is None else y + b[e].to(y.device)
+            if self.gate_up is not None:
+                gu = mit_bias("gate_up", self._matrix("gate_up", e)(xe))
+                g, u = gu[:, :self.ff], gu[:, self.ff:]
+            else:
+                g = mit_bias("gate", self._matrix("gate", e)(xe)) if self.gate is not None else None
+                u = mit_bias("up", self._matrix("up", e)(xe))
+            act = self._aktiviert(g, u).to(torch.bfloat16).float()
+            ys[sl] = mit_bias("down", self._matrix("down", e)(act))
+        back = torch.empty_like(ys)
+        back[folge] = ys
+        return (back.view(L_, k, E) * w.float().to(x.device).unsqueeze(-1)).sum(1)
 
     def _allgemein(self, x: torch.Tensor, idx: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
         """Every form of the layer: the gathered launches on each token's bf16 input (gate and up, or the

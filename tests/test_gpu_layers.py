@@ -418,6 +418,47 @@ def test_expert_layer_general_forms(nmq, oracle, form):
     assert oracle.rel_err_rows(out, ref).max() <= 2e-3
 
 
+@pytest.mark.parametrize("form", ["silu", "fused_bias_gelu"])
+def test_expert_layer_many_tokens_sorted(nmq, oracle, form):
+    """Many tokens (at least SORTIERT_AB pairs per expert): the (token, slot) pairs sorted by expert, each
+    used expert's rows as one matrix call (1 to 20 rows here: mat-vec, matrix-core and unpack routes), put
+    back and summed in (token, slot) order; against the oracle chain, max relative error per row <= 2e-3."""
+    from ggufengine_amd import experts
+    n_exp, k, E, FF, L = 6, 2, 1024, 512, 40
+    g_raw, u_raw, d_raw, G, U, D, GU = _expert_parts(n_exp, E, FF, 621)
+    rng = np.random.default_rng(622)
+    bias = {n: (rng.standard_normal((n_exp, wd)) * 0.05).astype(np.float32) for n, wd in (("gate_up", 2 * FF), ("down", E))}
+    if form == "silu":
+        layer = experts.Experten(G, U, D)
+    else:
+        layer = experts.Experten(None, None, D, gate_up=GU, bias={n: dev(b) for n, b in bias.items()}, akt="gelu")
+    x = rng.standard_normal((L, E)).astype(np.float32)
+    logits = rng.standard_normal((L, n_exp)).astype(np.float32)
+    logits[:, 0] += 3.0                       # expert 0 takes most tokens, others few
+    idx, w = experts.auswahl(dev(logits), k)
+    assert idx.numel() >= experts.SORTIERT_AB * n_exp
+    say("expert layer sorted", form)
+    out = layer(dev(x), idx, w).cpu().numpy()
+    ids, wts = idx.cpu().numpy(), w.cpu().numpy().astype(np.float64)
+    xb = oracle.round_bf16(x)
+    ref = np.zeros((L, E))
+    for t in range(L):
+        for j in range(k):
+            e = int(ids[t, j])
+            g = oracle.mv_deq("Q4_K", _expert_rows(g_raw, "Q4_K", n_exp, FF, E, e), FF, E, xb[t:t + 1])[0]
+            u = oracle.mv_deq("Q4_K", _expert_rows(u_raw, "Q4_K", n_exp, FF, E, e), FF, E, xb[t:t + 1])[0]
+            if form == "silu":
+                a = oracle.akt(g, u)
+            else:
+                a = oracle.akt(g + bias["gate_up"][e, :FF], u + bias["gate_up"][e, FF:], gelu=True)
+            ab = oracle.round_bf16(a.astype(np.float32))
+            y = oracle.mv_deq("Q6_K", _expert_rows(d_raw, "Q6_K", n_exp, E, FF, e), E, FF, ab[None])[0]
+            if form != "silu":
+                y = y + bias["down"][e]
+            ref[t] += wts[t, j] * y
+    assert oracle.rel_err_rows(out, ref).max() <= 2e-3
+
+
 def test_llama3_8b_layer_full_size(nmq, oracle):
     """The mat-vecs of a full Llama-3-8B decoder layer at batch 1 (q, k, v, o, gate, up Q4_K; down Q6_K
     4096x14336), weights ~N(0, 0.02) quantised by the library's encoders, run as the layer runs them

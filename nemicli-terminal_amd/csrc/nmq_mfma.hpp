@@ -419,7 +419,7 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     }
 }
 
-// ---- Q4_K, 5..8 tokens: dense reads straight into LDS ----------------------------------------------
+// ---- Q4_K (5..8 tokens), Q4_0 and Q8_0 (2..8 tokens): dense reads straight into LDS ---------------
 // mvm_kernel reads, per instruction, 8 bytes of each of 16 rows per lane group: 16 short pieces per read.
 // A CU issuing those for 16 waves stalls for longer than HBM takes to deliver the bytes (per-wave time
 // stamps: 10 us until the last wave has issued its reads, against 6 us with dense reads of the same
@@ -428,9 +428,11 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
 // (lane l's 16 bytes land at the LDS address of the instruction + 16 l, no registers in between):
 //   - the input rows (xq, xq2 of each token) row-major, 16 + n_in bytes apart, so that the 16 rows' A
 //     operands of a step (8 bytes at row n, 32 step + 8 k-block) fall on distinct banks;
-//   - the weights, per wave in chunks of 2 blocks x 16 rows: slot u = 64 j + lane of instruction j holds
-//     piece u % 19 of row u / 19 (18 pieces of 16 bytes per row, slot 18 a padding copy of piece 17, so
-//     rows are 304 bytes apart and the 16 rows' operands fall on distinct banks).
+//   - the weights, per wave in chunks of CHB 256-value blocks x 16 rows (Q4_K, Q4_0: 2 blocks of 144
+//     bytes; Q8_0: 1 block of 272 bytes, 8 GGUF blocks of 34): slot u = 64 j + lane of instruction j
+//     holds piece min(u % 19, PR - 1) of row u / 19 (PR = 18 or 17 pieces of 16 bytes per row, the
+//     slots past them padding copies of the last piece, so rows are 304 bytes apart and the 16 rows'
+//     operands fall on distinct banks).
 // (xd / 254, xs) per step and token are read densely into registers and stored as mvm_kernel stores them.
 // A wave holds one chunk buffer: chunk c + 1 is requested as soon as chunk c's operands are in registers,
 // and streams in while chunk c is computed.
@@ -457,94 +459,178 @@ __device__ __forceinline__ void vm_wait() {
 }
 
 // Per-lane offsets of the chunk reads (the same for every chunk), from the chunk's first byte in row
-// rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % 19, 17) of row
+// rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % 19, PR - 1) of row
 // min(row0 + u / 19, n_out - 1) >= rb0, so every offset is non-negative, also for tiles past the matrix.
 struct ChunkOffsets {
     u32 o[5];
 };
+template <int PR>
 __device__ __forceinline__ ChunkOffsets mvd_offsets(const MvmParams& p, int row0, int lane) {
     ChunkOffsets c;
     const int rb0 = min(row0, p.n_out - 1);
 #pragma unroll
     for (int j = 0; j < 5; ++j) {
         const int u = 64 * j + lane;
-        const int r = min(row0 + u / 19, p.n_out - 1) - rb0, k = min(u % 19, 17);
+        const int r = min(row0 + u / 19, p.n_out - 1) - rb0, k = min(u % 19, PR - 1);
         c.o[j] = (u32)(r * (int)p.row_bytes + 16 * k);
     }
     return c;
 }
 
-// chunk of blocks blk, blk + 1 of rows row0 .. row0 + 15 into buf (5 instructions; the last one with 48 lanes)
+// chunk of CHB blocks from blk on, rows row0 .. row0 + 15, into buf (5 instructions; the last one with 48
+// lanes)
+template <int F>
 __device__ __forceinline__ void mvd_chunk(u8* buf, const MvmParams& p, const ChunkOffsets& co, int row0, int blk,
                                           int lane) {
-    const u8* base = p.w + (int64_t)min(row0, p.n_out - 1) * p.row_bytes + (int64_t)blk * Mfma<NMQ_Q4_K>::BB;
+    const u8* base = p.w + (int64_t)min(row0, p.n_out - 1) * p.row_bytes + (int64_t)blk * Mfma<F>::BB;
 #pragma unroll
     for (int j = 0; j < 5; ++j)
         if (j < 4 || lane < 48) dma16s(base, co.o[j], buf + 1024 * j);
 }
 
-// Mfma<Q4_K>::load from the chunk buffer: block bb (0, 1) of the chunk, the lane's row n and k-block kb.
-__device__ __forceinline__ void mvd_frag(Mfma<NMQ_Q4_K>::Raw& r, const u8* buf, int bb, int n, int kb) {
-    const u8* b = buf + n * MVD_ROW + Mfma<NMQ_Q4_K>::BB * bb;
-    r.h = *(const u32x4*)b;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.q[i] = *(const u32x2*)(b + 16 + 32 * i + 8 * kb);
-}
+// Per-format pieces of the dense-read kernel.  CHB: 256-value blocks per chunk, PR: 16-byte pieces of a
+// chunk row (CHB * Mfma<F>::BB / 16).  frag(): the lane's operands of a whole chunk from the buffer (row
+// n, k-block kb).  block(): block i of the chunk (row block b) into the lane's sums of tokens 2 kb and
+// 2 kb + 1, A operands read from the row-major input (ab: the lane's input row n at k-block kb of block b;
+// steps 32 bytes apart), (xd / 254, xs) from xb (the block's first step, tokens 2 kb, 2 kb + 1).
+template <int F>
+struct Dma;
 
-// One 256-value block (8 steps, one 32-value group each) of the lane's weight row into its sums of
-// tokens 2 kb and 2 kb + 1, A operands read from the row-major input (arow: the lane's input row n at
-// k-block kb; block b's steps 32 bytes apart).  The block's scales d, dmin apply once per block:
-//   y += d * sum_g (sc_g (254 S1 + S2)) (xd_g / 254)  -  dmin * sum_g m_g xs_g
-// with sc_g (254 S1 + S2) an exact int32 (|.| <= 63 * 254 * 32 * 127 * 15 * 1.004 < 2^31) rounded once to
-// fp32, where mvm_block forms d sc_g and dmin m_g per group.
-__device__ __forceinline__ void mvd_block(const Mfma<NMQ_Q4_K>::Raw& cur, int b, const u8* arow, const float2* xsc,
-                                          int kb, float (&acc)[2]) {
+template <>
+struct Dma<NMQ_Q4_K> {
+    static constexpr int CHB = 2, PR = 18;
     using M = Mfma<NMQ_Q4_K>;
-    const u8* ab = arow + 256 * b;
-    const float2* xb = xsc + 64 * b + 2 * kb;
-    // 6-bit scales and mins of groups 0..3 (bytes of lo) and 4..7 (bytes of hi): get_scale_min_k4
-    const u32 sc_lo = cur.h.y & 0x3f3f3f3fu, m_lo = cur.h.z & 0x3f3f3f3fu;
-    const u32 sc_hi = (cur.h.w & 0x0f0f0f0fu) | ((cur.h.y >> 2) & 0x30303030u);
-    const u32 m_hi = ((cur.h.w >> 4) & 0x0f0f0f0fu) | ((cur.h.z >> 2) & 0x30303030u);
-    float sd0 = 0.f, sd1 = 0.f, sm0 = 0.f, sm1 = 0.f;
-    u64 xv[2];
-    float4 xf[2];
-    xv[0] = *(const u64*)ab;
-    xf[0] = *(const float4*)xb;
+    struct Raw {
+        M::Raw r[2];
+    };
+    // Mfma<Q4_K>::load from the chunk buffer
+    __device__ static void frag(Raw& o, const u8* row, int kb) {
 #pragma unroll
-    for (int s = 0; s < M::STEPS; ++s) {
-        if (s + 1 < M::STEPS) {
-            xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
-            xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+        for (int bb = 0; bb < 2; ++bb) {
+            const u8* b = row + M::BB * bb;
+            o.r[bb].h = *(const u32x4*)b;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.r[bb].q[i] = *(const u32x2*)(b + 16 + 32 * i + 8 * kb);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        const u64 wv = M::frag(cur, s);
-        const u64 x = xv[s & 1];
-        const float4 f = xf[s & 1];
-        i32x4 c = {0, 0, 0, 0};
-        c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
-        const u32 scw = s < 4 ? sc_lo : sc_hi, mw = s < 4 ? m_lo : m_hi;
-        const int sc = (int)((scw >> (8 * (s & 3))) & 0xffu), sc254 = 254 * sc;
-        const float mf = (float)((mw >> (8 * (s & 3))) & 0xffu);
-        // sc (254 S1 + S2) as 24-bit products (|S1|, |S2| <= 32 * 127 * 15, sc254 <= 16002)
-        sd0 = fmaf((float)(__mul24(c[0], sc254) + __mul24(c[1], sc)), f.x, sd0);
-        sd1 = fmaf((float)(__mul24(c[2], sc254) + __mul24(c[3], sc)), f.z, sd1);
-        sm0 = fmaf(mf, f.y, sm0);
-        sm1 = fmaf(mf, f.w, sm1);
     }
-    const float d = h2f(cur.h.x), dm = h2f(cur.h.x >> 16);
-    acc[0] = fmaf(d, sd0, fmaf(-dm, sm0, acc[0]));
-    acc[1] = fmaf(d, sd1, fmaf(-dm, sm1, acc[1]));
-}
+    // The block's scales d, dmin apply once per block:
+    //   y += d * sum_g (sc_g (254 S1 + S2)) (xd_g / 254)  -  dmin * sum_g m_g xs_g
+    // with sc_g (254 S1 + S2) an exact int32 (|.| <= 63 * 254 * 32 * 127 * 15 * 1.004 < 2^31) rounded once
+    // to fp32, where mvm_block forms d sc_g and dmin m_g per group.
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int, float (&acc)[2]) {
+        const M::Raw& cur = o.r[i];
+        // 6-bit scales and mins of groups 0..3 (bytes of lo) and 4..7 (bytes of hi): get_scale_min_k4
+        const u32 sc_lo = cur.h.y & 0x3f3f3f3fu, m_lo = cur.h.z & 0x3f3f3f3fu;
+        const u32 sc_hi = (cur.h.w & 0x0f0f0f0fu) | ((cur.h.y >> 2) & 0x30303030u);
+        const u32 m_hi = ((cur.h.w >> 4) & 0x0f0f0f0fu) | ((cur.h.z >> 2) & 0x30303030u);
+        float sd0 = 0.f, sd1 = 0.f, sm0 = 0.f, sm1 = 0.f;
+        u64 xv[2];
+        float4 xf[2];
+        xv[0] = *(const u64*)ab;
+        xf[0] = *(const float4*)xb;
+#pragma unroll
+        for (int s = 0; s < M::STEPS; ++s) {
+            if (s + 1 < M::STEPS) {
+                xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+                xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const u64 wv = M::frag(cur, s);
+            const u64 x = xv[s & 1];
+            const float4 f = xf[s & 1];
+            i32x4 c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+            const u32 scw = s < 4 ? sc_lo : sc_hi, mw = s < 4 ? m_lo : m_hi;
+            const int sc = (int)((scw >> (8 * (s & 3))) & 0xffu), sc254 = 254 * sc;
+            const float mf = (float)((mw >> (8 * (s & 3))) & 0xffu);
+            // sc (254 S1 + S2) as 24-bit products (|S1|, |S2| <= 32 * 127 * 15, sc254 <= 16002)
+            sd0 = fmaf((float)(__mul24(c[0], sc254) + __mul24(c[1], sc)), f.x, sd0);
+            sd1 = fmaf((float)(__mul24(c[2], sc254) + __mul24(c[3], sc)), f.z, sd1);
+            sm0 = fmaf(mf, f.y, sm0);
+            sm1 = fmaf(mf, f.w, sm1);
+        }
+        const float d = h2f(cur.h.x), dm = h2f(cur.h.x >> 16);
+        acc[0] = fmaf(d, sd0, fmaf(-dm, sm0, acc[0]));
+        acc[1] = fmaf(d, sd1, fmaf(-dm, sm1, acc[1]));
+    }
+};
+
+// Q4_0 and Q8_0: GGUF blocks of 32 values (one step each, d an fp16 at the block's start, then the codes)
+// of BB / 8 bytes, an odd number of 16-bit words: block pairs are 4-byte aligned in the chunk buffer, the
+// codes of the pair's first block start 2 bytes past a dword.  The lane's 8 code bytes of a block start
+// at lo = 8 (kb & 1) (Q4_0: k-block kb of a step is nibble half kb >> 1 of codes lo .. lo + 7, minus 8)
+// or lo = 8 kb (Q8_0: codes lo .. lo + 7).  Per pair the lane reads dwords only: a0..a2 over the first
+// block's bytes 2 + lo .. 9 + lo (shifted into place with v_alignbyte), b0, b1 with the second block's
+// (4-byte aligned), and the two dwords that hold the d's (first block: low half of the pair's dword 0;
+// second block: high half of the dword at byte GB - 2).
+// Per step:  y += d * (xd / 254) * (254 S1 + S2)  (254 S1 + S2 exact in int32, rounded once to fp32).
+template <int F>
+struct DmaSmall {
+    static constexpr int GB = F == NMQ_Q4_0 ? 18 : 34;  // bytes per GGUF block
+    static constexpr int CHB = F == NMQ_Q4_0 ? 2 : 1, PR = CHB * 8 * GB / 16;
+    static constexpr int NP = CHB * 4;                  // block pairs per chunk
+    struct Raw {
+        u32x2 q[2 * NP];
+        u32 d[NP];  // fp16 d of the pair's first block (low half) and second block (high half)
+    };
+    __device__ static void frag(Raw& o, const u8* row, int kb) {
+        const int lo = F == NMQ_Q4_0 ? 8 * (kb & 1) : 8 * kb;  // the lane's code bytes of a block
+#pragma unroll
+        for (int pr = 0; pr < NP; ++pr) {
+            const u8* bp = row + 2 * GB * pr;
+            const u32* a = (const u32*)(bp + lo);
+            const u32 a0 = a[0], a1 = a[1], a2 = a[2];
+            const u32 b0 = a[(GB + 2) / 4], b1 = a[(GB + 2) / 4 + 1];
+            const u32 d0 = ((const u32*)bp)[0], d1 = ((const u32*)bp)[GB / 4];
+            o.q[2 * pr] = u32x2{__builtin_amdgcn_alignbyte(a1, a0, 2), __builtin_amdgcn_alignbyte(a2, a1, 2)};
+            o.q[2 * pr + 1] = u32x2{b0, b1};
+            o.d[pr] = (d0 & 0xffffu) | (d1 & 0xffff0000u);
+        }
+    }
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, float (&acc)[2]) {
+        const u32 sh = F == NMQ_Q4_0 ? 4u * (u32)(kb >> 1) : 0u;
+        u64 xv[2];
+        float4 xf[2];
+        xv[0] = *(const u64*)ab;
+        xf[0] = *(const float4*)xb;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            if (s + 1 < 8) {
+                xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+                xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const u32x2 v = o.q[8 * i + s];
+            u64 wv;
+            if constexpr (F == NMQ_Q4_0)
+                wv = (u64)sub8x4((v.x >> sh) & 0x0f0f0f0fu) | ((u64)sub8x4((v.y >> sh) & 0x0f0f0f0fu) << 32);
+            else
+                wv = (u64)v.x | ((u64)v.y << 32);
+            const u64 x = xv[s & 1];
+            const float4 f = xf[s & 1];
+            i32x4 c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+            const u32 dw = o.d[4 * i + (s >> 1)];
+            const float d = h2f((s & 1) ? dw >> 16 : dw);
+            // |S1|, |S2| <= 32 * 127 * 128: 254 S1 as a 24-bit product
+            acc[0] = fmaf(d * f.x, (float)(__mul24(c[0], 254) + c[1]), acc[0]);
+            acc[1] = fmaf(d * f.z, (float)(__mul24(c[2], 254) + c[3]), acc[1]);
+        }
+    }
+};
+template <>
+struct Dma<NMQ_Q4_0> : DmaSmall<NMQ_Q4_0> {};
+template <>
+struct Dma<NMQ_Q8_0> : DmaSmall<NMQ_Q8_0> {};
 
 // LDS: input rows 16 x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
 __host__ __device__ constexpr size_t mvd_lds(int n_in, int W) {
     return (size_t)16 * (n_in + 16) + (size_t)2 * n_in + (size_t)W * MVD_BUF;
 }
 
-template <int NCH>
+template <int F, int NCH>
 __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
-    using M = Mfma<NMQ_Q4_K>;
+    using D = Dma<F>;
     asm volatile("" ::"s"(p.w), "s"(p.xq), "s"(p.xq2), "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in),
                  "s"(p.nc), "s"(p.ks), "s"(p.tpw), "s"(p.row_bytes), "s"(p.nblk));
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
@@ -554,7 +640,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
     const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
     const int n = lane & 15, kb = lane >> 4;
-    const int b0 = slice * 2 * NCH;
+    const int b0 = slice * D::CHB * NCH;
     float2* xsc = (float2*)(lds + 16 * RS);
     u8* buf = lds + 16 * RS + 2 * p.n_in + wave * MVD_BUF;
 
@@ -580,9 +666,9 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
     // request order, so input requested after another wave's weights would wait for them (the barrier
     // waits for issue only: the reads are not counted by the compiler's waits)
-    const ChunkOffsets co = mvd_offsets(p, row0, lane);
+    const ChunkOffsets co = mvd_offsets<D::PR>(p, row0, lane);
     lds_barrier();
-    mvd_chunk(buf, p, co, row0, b0, lane);
+    mvd_chunk<F>(buf, p, co, row0, b0, lane);
     asm volatile("s_waitcnt vmcnt(5)" : "+v"(xv[0]), "+v"(xv[1]) : : "memory");
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
@@ -602,15 +688,17 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         vm_wait<0>();  // chunk c in the buffer
-        typename M::Raw r0, r1;
-        mvd_frag(r0, buf, 0, n, kb);
-        mvd_frag(r1, buf, 1, n, kb);
+        typename D::Raw r;
+        D::frag(r, buf + n * MVD_ROW, kb);
         if (c + 1 < NCH) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the operands read before the buffer is refilled
-            mvd_chunk(buf, p, co, row0, b0 + 2 * (c + 1), lane);
+            mvd_chunk<F>(buf, p, co, row0, b0 + D::CHB * (c + 1), lane);
         }
-        mvd_block(r0, b0 + 2 * c, arow, xsc, kb, acc);
-        mvd_block(r1, b0 + 2 * c + 1, arow, xsc, kb, acc);
+#pragma unroll
+        for (int i = 0; i < D::CHB; ++i) {
+            const int b = b0 + D::CHB * c + i;
+            D::block(r, i, arow + 256 * b, xsc + 64 * b + 2 * kb, kb, acc);
+        }
     }
 
     // add the KS slices of each tile (as mvm_kernel)
@@ -643,11 +731,16 @@ struct MvdShape {
     size_t lds;
 };
 
-// Q4_K, MVD_MIN (5) .. 8 tokens, rows of 512 .. 4096 values (a multiple of 512): tiles of 16 rows, about
-// one workgroup of 4 .. 16 waves per CU, K slices of 2 or 4 blocks (1 or 2 chunks).
-inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max) {
+// MVD_MIN (Q4_K: 5, Q4_0 and Q8_0: 2) .. 8 tokens, rows of up to 4096 values (a multiple of 256 CHB): tiles
+// of 16 rows, about one workgroup of 4 .. 16 waves per CU, K slices of 1 or 2 chunks of CHB blocks.
+// The weights must start at a 16-byte boundary (global_load_lds_dwordx4).
+template <int F>
+inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, const void* w) {
+    constexpr int CHB = Dma<F>::CHB;
     MvdShape s{};
-    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, 5) || nc > 8 || n_in % 512 || n_in > 4096) return s;
+    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : 2) || nc > 8 || n_in % (256 * CHB) ||
+        n_in > 4096 || (uintptr_t)w % 16)
+        return s;
     const int nblk = n_in / 256;
     const int tiles = (n_out + 15) / 16;
     int tpw = tune(TUNE_MVD_TPW, 0);
@@ -655,10 +748,18 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max) {
     int ks = tune(TUNE_MVD_KS, 0);
     if (ks <= 0) {
         ks = 1;
-        while (ks * 2 * tpw <= 16 && nblk % (ks * 4) == 0) ks *= 2;  // slices of at least 2 blocks
+        while (ks * 2 * tpw <= 16 && nblk % (ks * 2 * CHB) == 0) ks *= 2;  // slices of at least one chunk
     }
-    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || nblk % ks || (nblk / ks) % 2) return s;
-    s.nch = nblk / ks / 2;
+    if (tune(TUNE_MVD_TPW, 0) <= 0 && tune(TUNE_MVD_KS, 0) <= 0) {
+        // slices of more than 2 chunks: fewer tiles per workgroup, more slices (Q8_0 14336x4096 at 8
+        // tokens: 4 x 4 with 4-chunk slices 27.6 us, 2 x 8 with 2-chunk slices 17.4 us)
+        while (nblk / ks > 2 * CHB && tpw > 1 && nblk % (ks * 2) == 0) {
+            tpw = (tpw + 1) / 2;
+            ks *= 2;
+        }
+    }
+    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || nblk % ks || (nblk / ks) % CHB) return s;
+    s.nch = nblk / ks / CHB;
     if (s.nch != 1 && s.nch != 2) return s;
     s.ks = ks;
     s.tpw = tpw;
@@ -668,14 +769,16 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max) {
     return s;
 }
 
+template <int F>
 inline void (*pick_mvd(const MvdShape& s))(MvmParams) {
-    return s.nch == 1 ? mvd_kernel<1> : mvd_kernel<2>;
+    return s.nch == 1 ? mvd_kernel<F, 1> : mvd_kernel<F, 2>;
 }
 
+template <int F>
 inline int launch_mvd(const MvdShape& s, MvmParams p, hipStream_t stream) {
     p.ks = s.ks;
     p.tpw = s.tpw;
-    hipLaunchKernelGGL(pick_mvd(s), dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
+    hipLaunchKernelGGL(pick_mvd<F>(s), dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
     return (int)hipGetLastError();
 }
 

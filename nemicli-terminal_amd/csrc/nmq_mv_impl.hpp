@@ -2264,6 +2264,22 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             return launch_mv<F>(q, nc - 8, n_mats, stream);
         }
     }
+    // The dense-read matrix-core kernel: Q4_0 and Q8_0 from 2 tokens, Q4_K from 5 (MVD_MIN; at 4 tokens it
+    // beats the few-token loop below, 14336x4096 10.8 against 12.7 us, but 2..4 tokens keep outputs equal
+    // to one-token launches bit for bit)
+    if constexpr (F == NMQ_Q4_K || F == NMQ_Q4_0 || F == NMQ_Q8_0) {
+        if (nc >= 2 && p.ids == nullptr) {
+            const MvdShape sd = plan_mvd<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big, p.w);
+            if (sd.ok) {
+                MvmParams q{};
+                q.w = p.w; q.xq = p.xq; q.xq2 = p.xq2; q.xd = p.xd; q.xs = p.xs; q.y = p.y;
+                q.n_out = p.n_out; q.n_in = p.n_in; q.nc = nc;
+                q.row_bytes = p.row_bytes;
+                q.nblk = p.n_in / 256;
+                return launch_mvd<F>(sd, q, stream);
+            }
+        }
+    }
     if constexpr (F == NMQ_Q4_K) {
         // 2..NMQ_MVT_MAX (default 4) tokens of one matrix: the one-token kernel's loop for all of them
         // (one unit per lane: rows of up to 4096 values; the NC input slices take about 65 + 34 NC VGPRs
@@ -2306,19 +2322,6 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
                                      : (n3 ? mvlt_kernel<4, 3> : mvlt_kernel<4, 4>);
                 hipLaunchKernelGGL(k, dim3((unsigned)((p.n_out + W - 1) / W)), dim3(p.nt), lds, stream, p);
                 return (int)hipGetLastError();
-            }
-        }
-    }
-    if constexpr (F == NMQ_Q4_K) {
-        if (nc >= 2 && p.ids == nullptr) {
-            const MvdShape sd = plan_mvd(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
-            if (sd.ok) {
-                MvmParams q{};
-                q.w = p.w; q.xq = p.xq; q.xq2 = p.xq2; q.xd = p.xd; q.xs = p.xs; q.y = p.y;
-                q.n_out = p.n_out; q.n_in = p.n_in; q.nc = nc;
-                q.row_bytes = p.row_bytes;
-                q.nblk = p.n_in / 256;
-                return launch_mvd(sd, q, stream);
             }
         }
     }

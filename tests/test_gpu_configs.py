@@ -1,7 +1,7 @@
 """GPU parity at the workloads' own shapes and data, through the C ABI and the default launch plan:
 
   - Q8_0 4096x4096, one token, W ~N(0,0.02) (seed 11), x ~N(0,1) (seed 12);
-  - Q4_K 14336x4096 / 4096x4096 (seeds 31, 32) at 1, 2, 4 and 8 tokens (x seed 33) -- the speculative
+  - Q4_K 14336x4096 / 4096x4096 (seeds 31, 32) at 1, 2, 3, 4 and 8 tokens (x seed 33) -- the speculative
     verify shapes, 2..4 tokens also bit for bit equal to one-token launches;
   - Q4_0 14336x4096 at one token;
   - TQ2_0 (codes with P(0) = 0.4, P(+-1) = 0.3, fp16 d = |N(0,0.02)|, seed 51) and IQ2_XXS (encoded from
@@ -117,7 +117,7 @@ def test_q4k_speculative_verify(nmq, oracle, q4k_spec, rows):
     X = gauss(33, (8, 4096))
     w = torch.from_numpy(raw).cuda()
     ones = [mv_abi(nmq, "Q4_K", w, X[c:c + 1], rows, 4096)[0] for c in range(8)]
-    for n in (1, 2, 4, 8):
+    for n in (1, 2, 3, 4, 8):
         say("Q4_K speculative", rows, "x 4096, tokens", n)
         y = mv_abi(nmq, "Q4_K", w, X[:n], rows, 4096)
         check(oracle, "Q4_K", raw, rows, 4096, X[:n], y)

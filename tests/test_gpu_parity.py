@@ -271,19 +271,22 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, tune, fmt, split):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q4_0", "Q8_0"])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 4096), (200, 4096), (1000, 2048), (333, 1024),
                                    (130, 512)])
 @pytest.mark.parametrize("split", [None, (1, 4), (2, 8), (4, 2)])
-def test_mv_tokens_dense_mfma(nmq, oracle, tune, shape, split):
-    """Q4_K 2..8 tokens on the dense-read matrix-core kernel (weights and input moved into LDS by
-    global_load_lds; the default for 5..8 tokens): the planner's split and forced (tiles per workgroup,
-    K slices) splits, slices of 2 and 4 blocks, partial last tiles and tiles past the matrix."""
+def test_mv_tokens_dense_mfma(nmq, oracle, tune, fmt, shape, split):
+    """2..8 tokens on the dense-read matrix-core kernel (weights and input moved into LDS by
+    global_load_lds; the default for Q4_K at 5..8 tokens, Q4_0 and Q8_0 at 2..8): the planner's split
+    and forced (tiles per workgroup, K slices) splits, slices of 1 and 2 chunks (Q4_K, Q4_0: chunks of 2
+    blocks of 256 values; Q8_0: 1 block), partial last tiles and tiles past the matrix."""
     from ggufengine_amd.gguf_types import TYPE_ID
     n_out, n_in = shape
     nblk = n_in // 256
+    chb = 1 if fmt == "Q8_0" else 2
     if split is not None:
         tpw, ks = split
-        if nblk % ks or (nblk // ks) not in (2, 4) or tpw * ks < 4:
+        if nblk % ks or (nblk // ks) % chb or (nblk // ks) // chb not in (1, 2) or tpw * ks < 4:
             pytest.skip("split outside the kernel's slices")
         tune(MVD_TPW=tpw)
         tune(MVD_KS=ks)
@@ -291,19 +294,41 @@ def test_mv_tokens_dense_mfma(nmq, oracle, tune, shape, split):
         pytest.skip("planner keeps small matrices elsewhere")
     tune(MVD_MIN=2)
     tune(MVT_MAX=1)
-    raw = random_blocks("Q4_K", n_out * n_in // 256, seed=71 + n_out % 97)
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=71 + n_out % 97)
     raw_d = dev(raw)
     for nc in (2, 5, 8) if n_out > 5000 else (2, 3, 4, 5, 6, 7, 8):
         x = np.random.default_rng(72 + nc).standard_normal((nc, n_in)).astype(np.float32)
         x[:, 3] = -25.0
         e = quant_dev(dev(x))
         y = torch.full((nc, n_out), float("nan"), device="cuda")
-        say("mv tokens dense mfma", shape, split, nc)
-        nmq.check(nmq.lib().nmq_mv(TYPE_ID["Q4_K"], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+        say("mv tokens dense mfma", fmt, shape, split, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
                                    e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
                                    nmq.stream_ptr()))
         torch.cuda.synchronize()
-        _check_mv(oracle, "Q4_K", raw, n_out, n_in, x, y)
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0"])
+def test_mv_tokens_weights_off_16_bytes(nmq, oracle, fmt):
+    """Q4_0 / Q8_0 weights 2 bytes past a 16-byte boundary (allowed for these formats): the dense-read
+    kernel needs 16-byte aligned rows, so 2..8 tokens take the other kernels, with the same results."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out, n_in = 1000, 2048
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=75)
+    buf = torch.zeros(raw.nbytes + 64, dtype=torch.uint8, device="cuda")
+    off = (16 - buf.data_ptr() % 16) % 16 + 2
+    buf[off:off + raw.nbytes] = dev(raw)
+    for nc in (2, 5, 8):
+        x = np.random.default_rng(76 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        e = quant_dev(dev(x))
+        y = torch.full((nc, n_out), float("nan"), device="cuda")
+        say("mv tokens weights off 16 bytes", fmt, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], buf.data_ptr() + off, e.xq.data_ptr(), e.xq2.data_ptr(),
+                                   e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                   nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
 @pytest.mark.parametrize("fmt", FMTS)

@@ -80,7 +80,10 @@ def hazards(asm: str, name: str):
     return found
 
 
-SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip", "nmq_mv_q6_k.hip")
+SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip", "nmq_mv_q6_k.hip", "nmq_mv_q4_0.hip",
+           "nmq_mv_q8_0.hip")
+# the sources with the dense-read matrix-core kernel
+DMA_SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_q4_0.hip", "nmq_mv_q8_0.hip")
 # the K-split long-row kernel with hand-issued reads (mvk_kernel<..., HR = true>): Q4_K, TQ2_0, Q6_K
 KSPLIT_KERNEL = re.compile(r"^(_ZN3nmq10mvk_kernel\w*Lb1EEEvNS_8MvParamsE):", re.M)
 
@@ -162,22 +165,24 @@ def m0_outside_hand_code(asm: str, name: str):
     return bad
 
 
-def test_dense_read_kernels_touch_no_outstanding_register(asm):
+@pytest.mark.parametrize("src", DMA_SOURCES)
+def test_dense_read_kernels_touch_no_outstanding_register(asm, src):
     """mvd_kernel reads (xd, xs) by hand (global_load_dwordx4) with its chunk reads (global_load_lds, no
     destination register) in flight: no instruction may touch those registers before the wait."""
-    names = DMA_KERNEL.findall(asm["nmq_mv_q4_k.hip"])
+    names = DMA_KERNEL.findall(asm[src])
     assert names
-    bad = [h for n in names for h in hazards(asm["nmq_mv_q4_k.hip"], n)]
+    bad = [h for n in names for h in hazards(asm[src], n)]
     assert not bad, bad[:5]
 
 
-def test_dense_read_kernels_keep_m0_to_themselves(asm):
-    names = DMA_KERNEL.findall(asm["nmq_mv_q4_k.hip"])
-    assert len(names) == 2, names
-    bad = [(n, t) for n in names for t in m0_outside_hand_code(asm["nmq_mv_q4_k.hip"], n)]
+@pytest.mark.parametrize("src", DMA_SOURCES)
+def test_dense_read_kernels_keep_m0_to_themselves(asm, src):
+    names = DMA_KERNEL.findall(asm[src])
+    assert len(names) == 2, names   # 1 or 2 chunks per slice
+    bad = [(n, t) for n in names for t in m0_outside_hand_code(asm[src], n)]
     assert not bad, bad[:5]
     # and every hand block that writes M0 issues its LDS load right after
-    text = asm["nmq_mv_q4_k.hip"]
+    text = asm[src]
     for n in names:
         body = text[text.index(n + ":"):]
         body = body[:body.index("s_endpgm")]

@@ -727,7 +727,7 @@ int nmq_mv(int fmt, const void* w, const int8_t* xq, const int8_t* xq2, const fl
     if (e) return e;
     if (ncols < 1) return NMQ_ERR_ARG;
     for (int c0 = 0; c0 < ncols; c0 += 2 * NMQ_MAX_COLS) {
-        // up to 16 tokens per call of the launcher (one launch on the matrix cores, else two of 8)
+        // up to 16 tokens per call of the launcher (one launch on the matrix cores, or two of 8)
         const int nc = ncols - c0 < 2 * NMQ_MAX_COLS ? ncols - c0 : 2 * NMQ_MAX_COLS;
         MvParams p{};
         p.w = (const u8*)w;

@@ -419,7 +419,7 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
     }
 }
 
-// ---- Q4_K (5..8 tokens), Q4_0 and Q8_0 (2..8 tokens): dense reads straight into LDS ---------------
+// ---- Q4_K (5..8 tokens), the other formats (2..8 tokens): dense reads straight into LDS -------------
 // mvm_kernel reads, per instruction, 8 bytes of each of 16 rows per lane group: 16 short pieces per read.
 // A CU issuing those for 16 waves stalls for longer than HBM takes to deliver the bytes (per-wave time
 // stamps: 10 us until the last wave has issued its reads, against 6 us with dense reads of the same
@@ -429,15 +429,16 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
 //   - the input rows (xq, xq2 of each token) row-major, 16 + n_in bytes apart, so that the 16 rows' A
 //     operands of a step (8 bytes at row n, 32 step + 8 k-block) fall on distinct banks;
 //   - the weights, per wave in chunks of CHB 256-value blocks x 16 rows (Q4_K, Q4_0: 2 blocks of 144
-//     bytes; Q8_0: 1 block of 272 bytes, 8 GGUF blocks of 34): slot u = 64 j + lane of instruction j
-//     holds piece min(u % 19, PR - 1) of row u / 19 (PR = 18 or 17 pieces of 16 bytes per row, the
-//     slots past them padding copies of the last piece, so rows are 304 bytes apart and the 16 rows'
-//     operands fall on distinct banks).
+//     bytes; Q8_0: 1 block of 272 bytes, 8 GGUF blocks of 34; Q6_K: 1 block of 210; TQ2_0, IQ2_XXS: 2
+//     blocks of 66): a chunk row is the 16-byte window from the 16-byte boundary at or below the chunk's
+//     first byte (m bytes before it: 0 where CHB blocks fill whole pieces), PR pieces of 16 bytes; slot
+//     u = 64 j + lane of instruction j holds piece min(u % SLOTS, PR - 1) of row u / SLOTS (the slots
+//     past PR padding copies of the last piece; SLOTS = 19, 15 or 11 puts the 16 rows' operands on
+//     distinct banks).  Rows whose bytes sit off a 4-byte boundary in the window are read as dwords
+//     and shifted into place with v_alignbyte.
 // (xd / 254, xs) per step and token are read densely into registers and stored as mvm_kernel stores them.
 // A wave holds one chunk buffer: chunk c + 1 is requested as soon as chunk c's operands are in registers,
 // and streams in while chunk c is computed.
-constexpr int MVD_ROW = 304;            // LDS bytes per row of a chunk buffer
-constexpr int MVD_BUF = 16 * MVD_ROW;   // bytes per wave
 typedef __attribute__((address_space(3))) void lds_void;
 
 // global_load_lds_dwordx4 issued by hand, its address a wave-uniform base (SGPR pair) plus an unsigned
@@ -461,50 +462,60 @@ __device__ __forceinline__ void vm_wait() {
 // Per-lane offsets of the chunk reads (the same for every chunk), from the chunk's first byte in row
 // rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % 19, PR - 1) of row
 // min(row0 + u / 19, n_out - 1) >= rb0, so every offset is non-negative, also for tiles past the matrix.
+template <int NI>
 struct ChunkOffsets {
-    u32 o[5];
+    u32 o[NI];
 };
-template <int PR>
-__device__ __forceinline__ ChunkOffsets mvd_offsets(const MvmParams& p, int row0, int lane) {
-    ChunkOffsets c;
+template <int PR, int SLOTS, int NI>
+__device__ __forceinline__ ChunkOffsets<NI> mvd_offsets(const MvmParams& p, int row0, int lane) {
+    ChunkOffsets<NI> c;
     const int rb0 = min(row0, p.n_out - 1);
 #pragma unroll
-    for (int j = 0; j < 5; ++j) {
+    for (int j = 0; j < NI; ++j) {
         const int u = 64 * j + lane;
-        const int r = min(row0 + u / 19, p.n_out - 1) - rb0, k = min(u % 19, PR - 1);
+        const int r = min(row0 + u / SLOTS, p.n_out - 1) - rb0, k = min(u % SLOTS, PR - 1);
         c.o[j] = (u32)(r * (int)p.row_bytes + 16 * k);
     }
     return c;
 }
 
-// chunk of CHB blocks from blk on, rows row0 .. row0 + 15, into buf (5 instructions; the last one with 48
-// lanes)
-template <int F>
-__device__ __forceinline__ void mvd_chunk(u8* buf, const MvmParams& p, const ChunkOffsets& co, int row0, int blk,
+// chunk of CHB blocks from blk on, rows row0 .. row0 + 15, into buf (NI instructions; the last one with
+// 16 SLOTS - 64 (NI - 1) = 48 lanes): the windows start at the 16-byte boundary at or below the chunk
+template <int F, int NI>
+__device__ __forceinline__ void mvd_chunk(u8* buf, const MvmParams& p, const ChunkOffsets<NI>& co, int row0, int blk,
                                           int lane) {
-    const u8* base = p.w + (int64_t)min(row0, p.n_out - 1) * p.row_bytes + (int64_t)blk * Mfma<F>::BB;
+    const u8* base = p.w + (int64_t)min(row0, p.n_out - 1) * p.row_bytes + (((int64_t)blk * Mfma<F>::BB) & ~15ll);
 #pragma unroll
-    for (int j = 0; j < 5; ++j)
-        if (j < 4 || lane < 48) dma16s(base, co.o[j], buf + 1024 * j);
+    for (int j = 0; j < NI; ++j)
+        if (j < NI - 1 || lane < 48) dma16s(base, co.o[j], buf + 1024 * j);
+}
+
+__device__ __forceinline__ u32 lds32(const u8* p) { return *(const u32*)p; }
+// 8 bytes at p + sh (p 4-byte aligned, sh in 0..3) from three dwords
+__device__ __forceinline__ u32x2 lds8_shifted(const u8* p, u32 sh) {
+    const u32 w0 = lds32(p), w1 = lds32(p + 4), w2 = lds32(p + 8);
+    return u32x2{__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh)};
 }
 
 // Per-format pieces of the dense-read kernel.  CHB: 256-value blocks per chunk, PR: 16-byte pieces of a
-// chunk row (CHB * Mfma<F>::BB / 16).  frag(): the lane's operands of a whole chunk from the buffer (row
-// n, k-block kb).  block(): block i of the chunk (row block b) into the lane's sums of tokens 2 kb and
-// 2 kb + 1, A operands read from the row-major input (ab: the lane's input row n at k-block kb of block b;
-// steps 32 bytes apart), (xd / 254, xs) from xb (the block's first step, tokens 2 kb, 2 kb + 1).
+// chunk row, SLOTS: its LDS stride in pieces.  frag(): the lane's operands of a whole chunk from the
+// buffer (row: the lane's row n, m: the chunk's offset in the window, kb: the lane's k-block).
+// block(): block i of the chunk (row block b) into the lane's sums of tokens 2 kb and 2 kb + 1, A operands
+// read from the row-major input (ab: the lane's input row n at k-block kb of block b; steps 32 bytes
+// apart), (xd / 254, xs) from xb (the block's first step, tokens 2 kb, 2 kb + 1); tab: the IQ2_XXS grid
+// and sign tables.
 template <int F>
 struct Dma;
 
 template <>
 struct Dma<NMQ_Q4_K> {
-    static constexpr int CHB = 2, PR = 18;
+    static constexpr int CHB = 2, PR = 18, SLOTS = 19;
     using M = Mfma<NMQ_Q4_K>;
     struct Raw {
         M::Raw r[2];
     };
     // Mfma<Q4_K>::load from the chunk buffer
-    __device__ static void frag(Raw& o, const u8* row, int kb) {
+    __device__ static void frag(Raw& o, const u8* row, int, int kb) {
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb) {
             const u8* b = row + M::BB * bb;
@@ -517,7 +528,8 @@ struct Dma<NMQ_Q4_K> {
     //   y += d * sum_g (sc_g (254 S1 + S2)) (xd_g / 254)  -  dmin * sum_g m_g xs_g
     // with sc_g (254 S1 + S2) an exact int32 (|.| <= 63 * 254 * 32 * 127 * 15 * 1.004 < 2^31) rounded once
     // to fp32, where mvm_block forms d sc_g and dmin m_g per group.
-    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int, float (&acc)[2]) {
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int, const u64*,
+                                float (&acc)[2]) {
         const M::Raw& cur = o.r[i];
         // 6-bit scales and mins of groups 0..3 (bytes of lo) and 4..7 (bytes of hi): get_scale_min_k4
         const u32 sc_lo = cur.h.y & 0x3f3f3f3fu, m_lo = cur.h.z & 0x3f3f3f3fu;
@@ -567,13 +579,13 @@ struct Dma<NMQ_Q4_K> {
 template <int F>
 struct DmaSmall {
     static constexpr int GB = F == NMQ_Q4_0 ? 18 : 34;  // bytes per GGUF block
-    static constexpr int CHB = F == NMQ_Q4_0 ? 2 : 1, PR = CHB * 8 * GB / 16;
+    static constexpr int CHB = F == NMQ_Q4_0 ? 2 : 1, PR = CHB * 8 * GB / 16, SLOTS = 19;
     static constexpr int NP = CHB * 4;                  // block pairs per chunk
     struct Raw {
         u32x2 q[2 * NP];
         u32 d[NP];  // fp16 d of the pair's first block (low half) and second block (high half)
     };
-    __device__ static void frag(Raw& o, const u8* row, int kb) {
+    __device__ static void frag(Raw& o, const u8* row, int, int kb) {
         const int lo = F == NMQ_Q4_0 ? 8 * (kb & 1) : 8 * kb;  // the lane's code bytes of a block
 #pragma unroll
         for (int pr = 0; pr < NP; ++pr) {
@@ -587,7 +599,8 @@ struct DmaSmall {
             o.d[pr] = (d0 & 0xffffu) | (d1 & 0xffff0000u);
         }
     }
-    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, float (&acc)[2]) {
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, const u64*,
+                                float (&acc)[2]) {
         const u32 sh = F == NMQ_Q4_0 ? 4u * (u32)(kb >> 1) : 0u;
         u64 xv[2];
         float4 xf[2];
@@ -623,17 +636,171 @@ struct Dma<NMQ_Q4_0> : DmaSmall<NMQ_Q4_0> {};
 template <>
 struct Dma<NMQ_Q8_0> : DmaSmall<NMQ_Q8_0> {};
 
+// Q6_K: chunks of one 210-byte block; the window offset m = 2 b mod 16 is even, so the block's fields
+// sit 0 or 2 bytes off a dword (sh = m & 3): every 8 bytes are read as three dwords and shifted.  Per
+// step two MFMAs, the input masked to one 16-value scale group each (as mvm_kernel).
+template <>
+struct Dma<NMQ_Q6_K> {
+    static constexpr int CHB = 1, PR = 14, SLOTS = 15;
+    using M = Mfma<NMQ_Q6_K>;
+    using Raw = M::Raw;
+    __device__ static void frag(Raw& r, const u8* row, int m, int kb) {
+        const u8* b = row + (m & 12);
+        const u32 sh = (u32)(m & 3);
+#pragma unroll
+        for (int n = 0; n < 2; ++n) {
+            r.ql[2 * n] = lds8_shifted(b + 64 * n + 8 * kb, sh);
+            r.ql[2 * n + 1] = lds8_shifted(b + 64 * n + 32 + 8 * kb, sh);
+            r.qh[n] = lds8_shifted(b + 128 + 32 * n + 8 * kb, sh);
+        }
+        const u32x2 s0 = lds8_shifted(b + 192, sh), s1 = lds8_shifted(b + 200, sh);
+        r.sc = u32x4{s0.x, s0.y, s1.x, s1.y};
+        r.d = lds32(b + 208) >> (8 * sh);
+    }
+    __device__ static void block(const Raw& cur, int, const u8* ab, const float2* xb, int kb, const u64*,
+                                float (&acc)[2]) {
+        u64 xv[2];
+        float4 xf[2];
+        xv[0] = *(const u64*)ab;
+        xf[0] = *(const float4*)xb;
+#pragma unroll
+        for (int s = 0; s < M::STEPS; ++s) {
+            if (s + 1 < M::STEPS) {
+                xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+                xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const u64 wv = M::frag(cur, s);
+            const u64 x = xv[s & 1];
+            const float4 f = xf[s & 1];
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                const u64 xm = (kb >> 1) == half ? x : 0ull;
+                i32x4 c = {0, 0, 0, 0};
+                c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)xm, (long)wv, c, 0, 0, 0);
+                const float w = M::fac(cur, 2 * s + half).x;
+                acc[0] = fmaf(w * f.x, (float)__mul24(c[0], 254) + (float)c[1], acc[0]);
+                acc[1] = fmaf(w * f.z, (float)__mul24(c[2], 254) + (float)c[3], acc[1]);
+            }
+        }
+    }
+};
+
+// TQ2_0 and IQ2_XXS: chunks of two 66-byte blocks; the window offset m = 132 (b / 2) mod 16 is a
+// multiple of 4, so the chunk's first block is dword-aligned and its second sits 2 bytes off (read as
+// dwords and shifted by 2).  PR = 9 pieces (m + 132 <= 144 bytes).
+template <>
+struct Dma<NMQ_TQ2_0> {
+    static constexpr int CHB = 2, PR = 9, SLOTS = 11;
+    using M = Mfma<NMQ_TQ2_0>;
+    struct Raw {
+        M::Raw r[2];
+    };
+    __device__ static void frag(Raw& o, const u8* row, int m, int kb) {
+        const u8* b = row + m;  // block 0: codes at 0, d at 64; block 1: codes at 66, d at 130
+        o.r[0].q[0] = u32x2{lds32(b + 8 * kb), lds32(b + 8 * kb + 4)};
+        o.r[0].q[1] = u32x2{lds32(b + 32 + 8 * kb), lds32(b + 36 + 8 * kb)};
+        o.r[0].d = lds32(b + 64);
+        o.r[1].q[0] = lds8_shifted(b + 64 + 8 * kb, 2);
+        o.r[1].q[1] = lds8_shifted(b + 96 + 8 * kb, 2);
+        o.r[1].d = lds32(b + 128) >> 16;
+    }
+    // one fp16 d per block: the steps' exact sums (|254 S1 + S2| <= 254 * 32 * 127 + 32 * 127 < 2^24)
+    // scaled by xd / 254 and added, then d once
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int, const u64*,
+                                float (&acc)[2]) {
+        const M::Raw& cur = o.r[i];
+        float sd0 = 0.f, sd1 = 0.f;
+        u64 xv[2];
+        float4 xf[2];
+        xv[0] = *(const u64*)ab;
+        xf[0] = *(const float4*)xb;
+#pragma unroll
+        for (int s = 0; s < M::STEPS; ++s) {
+            if (s + 1 < M::STEPS) {
+                xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+                xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const u64 wv = M::frag(cur, s);
+            const u64 x = xv[s & 1];
+            const float4 f = xf[s & 1];
+            i32x4 c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+            sd0 = fmaf((float)(__mul24(c[0], 254) + c[1]), f.x, sd0);
+            sd1 = fmaf((float)(__mul24(c[2], 254) + c[3]), f.z, sd1);
+        }
+        const float d = h2f(cur.d);
+        acc[0] = fmaf(d, sd0, acc[0]);
+        acc[1] = fmaf(d, sd1, acc[1]);
+    }
+};
+
+template <>
+struct Dma<NMQ_IQ2_XXS> {
+    static constexpr int CHB = 2, PR = 9, SLOTS = 11;
+    using M = Mfma<NMQ_IQ2_XXS>;
+    struct Raw {
+        M::Raw r[2];
+    };
+    // block 0: d at 0, sub-block s's {aux0, aux1} at 2 + 8 s (2 bytes off a dword); block 1: d at 66
+    // (high half of the dword at 64), its pairs at 68 + 8 s (aligned).  Every lane reads all of them.
+    __device__ static void frag(Raw& o, const u8* row, int m, int) {
+        const u8* b = row + m;
+        u32 w[17];
+#pragma unroll
+        for (int j = 0; j < 17; ++j) w[j] = lds32(b + 4 * j);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+            o.r[0].a[s] = u32x2{__builtin_amdgcn_alignbyte(w[2 * s + 1], w[2 * s], 2),
+                                __builtin_amdgcn_alignbyte(w[2 * s + 2], w[2 * s + 1], 2)};
+            o.r[1].a[s] = u32x2{lds32(b + 68 + 8 * s), lds32(b + 72 + 8 * s)};
+        }
+        o.r[0].d = w[0];
+        o.r[1].d = w[16] >> 16;
+    }
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, const u64* tab,
+                                float (&acc)[2]) {
+        const M::Raw& cur = o.r[i];
+        u64 xv[2];
+        float4 xf[2];
+        xv[0] = *(const u64*)ab;
+        xf[0] = *(const float4*)xb;
+#pragma unroll
+        for (int s = 0; s < M::STEPS; ++s) {
+            if (s + 1 < M::STEPS) {
+                xv[(s + 1) & 1] = *(const u64*)(ab + 32 * (s + 1));
+                xf[(s + 1) & 1] = *(const float4*)(xb + 8 * (s + 1));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const u64 wv = M::frag_iq(cur, s, kb, tab);
+            const u64 x = xv[s & 1];
+            const float4 f = xf[s & 1];
+            i32x4 c = {0, 0, 0, 0};
+            c = __builtin_amdgcn_mfma_i32_16x16x32_i8((long)x, (long)wv, c, 0, 0, 0);
+            const float w = M::fac(cur, s).x;
+            acc[0] = fmaf(w * f.x, (float)(__mul24(c[0], 254) + c[1]), acc[0]);
+            acc[1] = fmaf(w * f.z, (float)(__mul24(c[2], 254) + c[3]), acc[1]);
+        }
+    }
+};
+
 // LDS: input rows 16 x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
+template <int F>
 __host__ __device__ constexpr size_t mvd_lds(int n_in, int W) {
-    return (size_t)16 * (n_in + 16) + (size_t)2 * n_in + (size_t)W * MVD_BUF;
+    return (size_t)16 * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * Dma<F>::SLOTS;
 }
 
 template <int F, int NCH>
 __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     using D = Dma<F>;
+    constexpr int ROW = 16 * D::SLOTS;              // LDS bytes per row of a chunk buffer
+    constexpr int NI = (16 * D::SLOTS + 63) / 64;   // chunk read instructions
+    static_assert(16 * D::SLOTS - 64 * (NI - 1) == 48, "the last chunk read has 48 lanes");
     asm volatile("" ::"s"(p.w), "s"(p.xq), "s"(p.xq2), "s"(p.xd), "s"(p.xs), "s"(p.y), "s"(p.n_out), "s"(p.n_in),
                  "s"(p.nc), "s"(p.ks), "s"(p.tpw), "s"(p.row_bytes), "s"(p.nblk));
     extern __shared__ __attribute__((aligned(16))) u8 lds[];
+    __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = p.ks * p.tpw, nt = 64 * W;
     const int S = p.n_in / 32, RS = p.n_in + 16;
@@ -642,7 +809,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     const int n = lane & 15, kb = lane >> 4;
     const int b0 = slice * D::CHB * NCH;
     float2* xsc = (float2*)(lds + 16 * RS);
-    u8* buf = lds + 16 * RS + 2 * p.n_in + wave * MVD_BUF;
+    u8* buf = lds + 16 * RS + 2 * p.n_in + wave * 16 * ROW;
 
     // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2 (absent tokens re-read xq's first
     // bytes), 1 KB per instruction, instruction i = row i / MB, kilobyte i % MB, over the waves
@@ -663,13 +830,18 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
         const bool ok = i < 4 * S && t < p.nc;
         xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * S + 4 * m : p.xd);
     }
+    u32x2 gv = tab_load_hand<F>();  // IQ2_XXS: this thread's grid entry (W >= 4: 256 threads)
     // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
     // request order, so input requested after another wave's weights would wait for them (the barrier
     // waits for issue only: the reads are not counted by the compiler's waits)
-    const ChunkOffsets co = mvd_offsets<D::PR>(p, row0, lane);
+    const ChunkOffsets<NI> co = mvd_offsets<D::PR, D::SLOTS, NI>(p, row0, lane);
     lds_barrier();
-    mvd_chunk<F>(buf, p, co, row0, b0, lane);
-    asm volatile("s_waitcnt vmcnt(5)" : "+v"(xv[0]), "+v"(xv[1]) : : "memory");
+    mvd_chunk<F, NI>(buf, p, co, row0, b0, lane);
+    if constexpr (F == NMQ_IQ2_XXS)
+        asm volatile("s_waitcnt vmcnt(%3)" : "+v"(xv[0]), "+v"(xv[1]), "+v"(gv) : "n"(NI) : "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(%2)" : "+v"(xv[0]), "+v"(xv[1]) : "n"(NI) : "memory");
+    tab_store_hand<F>(tab, gv, nt);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
@@ -689,15 +861,15 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     for (int c = 0; c < NCH; ++c) {
         vm_wait<0>();  // chunk c in the buffer
         typename D::Raw r;
-        D::frag(r, buf + n * MVD_ROW, kb);
+        D::frag(r, buf + n * ROW, (int)(((int64_t)(b0 + D::CHB * c) * Mfma<F>::BB) & 15), kb);
         if (c + 1 < NCH) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the operands read before the buffer is refilled
-            mvd_chunk<F>(buf, p, co, row0, b0 + D::CHB * (c + 1), lane);
+            mvd_chunk<F, NI>(buf, p, co, row0, b0 + D::CHB * (c + 1), lane);
         }
 #pragma unroll
         for (int i = 0; i < D::CHB; ++i) {
             const int b = b0 + D::CHB * c + i;
-            D::block(r, i, arow + 256 * b, xsc + 64 * b + 2 * kb, kb, acc);
+            D::block(r, i, arow + 256 * b, xsc + 64 * b + 2 * kb, kb, tab, acc);
         }
     }
 
@@ -731,15 +903,15 @@ struct MvdShape {
     size_t lds;
 };
 
-// MVD_MIN (Q4_K: 5, Q4_0 and Q8_0: 2) .. 8 tokens, rows of up to 4096 values (a multiple of 256 CHB): tiles
-// of 16 rows, about one workgroup of 4 .. 16 waves per CU, K slices of 1 or 2 chunks of CHB blocks.
-// The weights must start at a 16-byte boundary (global_load_lds_dwordx4).
+// MVD_MIN (Q4_K: 5, Q6_K: 3, the others: 2) .. 8 tokens, rows of up to 4096 values (a multiple of 256 CHB, and of
+// 16 bytes): tiles of 16 rows, about one workgroup of 4 .. 16 waves per CU, K slices of 1 or 2 chunks of
+// CHB blocks.  The weights must start at a 16-byte boundary (global_load_lds_dwordx4).
 template <int F>
 inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, const void* w) {
     constexpr int CHB = Dma<F>::CHB;
     MvdShape s{};
-    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : 2) || nc > 8 || n_in % (256 * CHB) ||
-        n_in > 4096 || (uintptr_t)w % 16)
+    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : (F == NMQ_Q6_K ? 3 : 2)) || nc > 8 || n_in % (256 * CHB) ||
+        n_in > 4096 || (uintptr_t)w % 16 || (int64_t)n_in / 256 * Mfma<F>::BB % 16)
         return s;
     const int nblk = n_in / 256;
     const int tiles = (n_out + 15) / 16;
@@ -764,7 +936,7 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, cons
     s.ks = ks;
     s.tpw = tpw;
     s.grid_x = (tiles + tpw - 1) / tpw;
-    s.lds = mvd_lds(n_in, ks * tpw);
+    s.lds = mvd_lds<F>(n_in, ks * tpw);
     s.ok = s.lds + 4096 <= (size_t)lds_max;
     return s;
 }

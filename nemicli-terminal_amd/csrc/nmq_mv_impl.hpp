@@ -2251,8 +2251,12 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     // 2..16 tokens of one matrix: the matrix cores (see nmq_mfma.hpp); more than 8 tokens that cannot
     // go there in one launch run as two launches of at most 8
     if (nc > 8) {
+        // where the dense-read kernel takes 8 tokens, two launches of it beat one matrix-core launch of
+        // both groups (14336x4096 at 16 tokens: Q4_0 52.1 -> 22.9 us, Q8_0 60.6 -> 33.2, Q4_K 24.9 -> 20.5,
+        // TQ2_0 19.5 -> 16.1, IQ2_XXS 27.4 -> 24.7)
         const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
-        if (!(sm.ok && p.ids == nullptr)) {
+        const bool dense8 = p.ids == nullptr && plan_mvd<F>(p.n_out, p.n_in, 8, di.cus, di.lds_max_big, p.w).ok;
+        if (!(sm.ok && p.ids == nullptr) || dense8) {
             int e = launch_mv<F>(p, 8, n_mats, stream);
             if (e) return e;
             MvParams q = p;
@@ -2264,10 +2268,10 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             return launch_mv<F>(q, nc - 8, n_mats, stream);
         }
     }
-    // The dense-read matrix-core kernel: Q4_0 and Q8_0 from 2 tokens, Q4_K from 5 (MVD_MIN; at 4 tokens it
-    // beats the few-token loop below, 14336x4096 10.8 against 12.7 us, but 2..4 tokens keep outputs equal
-    // to one-token launches bit for bit)
-    if constexpr (F == NMQ_Q4_K || F == NMQ_Q4_0 || F == NMQ_Q8_0) {
+    // The dense-read matrix-core kernel: from 2 tokens, Q6_K from 3 (at 2 the dot4 kernel is faster:
+    // 4096x4096 6.8 against 7.2 us), Q4_K from 5 (MVD_MIN; at 4 tokens it beats the few-token loop below,
+    // 14336x4096 10.8 against 12.7 us, but 2..4 tokens keep outputs equal to one-token launches bit for bit)
+    {
         if (nc >= 2 && p.ids == nullptr) {
             const MvdShape sd = plan_mvd<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big, p.w);
             if (sd.ok) {

@@ -271,19 +271,21 @@ def test_mv_tokens_matrix_core_splits(nmq, oracle, tune, fmt, split):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
-@pytest.mark.parametrize("fmt", ["Q4_K", "Q4_0", "Q8_0"])
+@pytest.mark.parametrize("fmt", ["Q4_K", "Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"])
 @pytest.mark.parametrize("shape", [(14336, 4096), (4096, 4096), (200, 4096), (1000, 2048), (333, 1024),
                                    (130, 512)])
 @pytest.mark.parametrize("split", [None, (1, 4), (2, 8), (4, 2)])
 def test_mv_tokens_dense_mfma(nmq, oracle, tune, fmt, shape, split):
     """2..8 tokens on the dense-read matrix-core kernel (weights and input moved into LDS by
-    global_load_lds; the default for Q4_K at 5..8 tokens, Q4_0 and Q8_0 at 2..8): the planner's split
-    and forced (tiles per workgroup, K slices) splits, slices of 1 and 2 chunks (Q4_K, Q4_0: chunks of 2
-    blocks of 256 values; Q8_0: 1 block), partial last tiles and tiles past the matrix."""
+    global_load_lds; the default for Q4_K at 5..8 tokens, the other formats at 2..8): the planner's split
+    and forced (tiles per workgroup, K slices) splits, slices of 1 and 2 chunks (Q4_K, Q4_0, TQ2_0,
+    IQ2_XXS: chunks of 2 blocks of 256 values; Q8_0, Q6_K: 1 block), chunk windows starting off a 16-byte
+    boundary (Q6_K, TQ2_0, IQ2_XXS), partial last tiles and tiles past the matrix.  Rows whose bytes are not
+    a multiple of 16 (Q6_K, TQ2_0, IQ2_XXS below 2048 values) take the other kernels."""
     from ggufengine_amd.gguf_types import TYPE_ID
     n_out, n_in = shape
     nblk = n_in // 256
-    chb = 1 if fmt == "Q8_0" else 2
+    chb = 1 if fmt in ("Q8_0", "Q6_K") else 2
     if split is not None:
         tpw, ks = split
         if nblk % ks or (nblk // ks) % chb or (nblk // ks) // chb not in (1, 2) or tpw * ks < 4:
@@ -309,9 +311,9 @@ def test_mv_tokens_dense_mfma(nmq, oracle, tune, fmt, shape, split):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
-@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0"])
+@pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"])
 def test_mv_tokens_weights_off_16_bytes(nmq, oracle, fmt):
-    """Q4_0 / Q8_0 weights 2 bytes past a 16-byte boundary (allowed for these formats): the dense-read
+    """Weights 2 bytes past a 16-byte boundary (allowed for every format but Q4_K): the dense-read
     kernel needs 16-byte aligned rows, so 2..8 tokens take the other kernels, with the same results."""
     from ggufengine_amd.gguf_types import TYPE_ID
     n_out, n_in = 1000, 2048

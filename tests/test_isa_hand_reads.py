@@ -82,8 +82,8 @@ def hazards(asm: str, name: str):
 
 SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_tq2_0.hip", "nmq_mv_iq2_xxs.hip", "nmq_mv_q6_k.hip", "nmq_mv_q4_0.hip",
            "nmq_mv_q8_0.hip")
-# the sources with the dense-read matrix-core kernel
-DMA_SOURCES = ("nmq_mv_q4_k.hip", "nmq_mv_q4_0.hip", "nmq_mv_q8_0.hip")
+# the sources with the dense-read matrix-core kernel (all of them)
+DMA_SOURCES = SOURCES
 # the K-split long-row kernel with hand-issued reads (mvk_kernel<..., HR = true>): Q4_K, TQ2_0, Q6_K
 KSPLIT_KERNEL = re.compile(r"^(_ZN3nmq10mvk_kernel\w*Lb1EEEvNS_8MvParamsE):", re.M)
 

@@ -37,7 +37,7 @@ enum Tune : int {
     TUNE_MMH_G,       // fp16 matrix-core kernel: groups of 16 tokens per workgroup
     TUNE_MVK,         // 0 disables the K-split long-row kernel (one token, rows of 129..256 units)
     TUNE_MVK_WPC,     // K-split long-row kernel: resident waves per CU
-    TUNE_MVD,         // 0 disables the dense-read matrix-core kernel (Q4_K, 5..8 tokens)
+    TUNE_MVD,         // 0 disables the dense-read matrix-core kernel (2..8 tokens)
     TUNE_MVD_MIN,     // fewest tokens that it takes
     TUNE_MVD_TPW,     // its row tiles per workgroup
     TUNE_MVD_KS,      // its slices of the row

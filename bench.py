@@ -297,11 +297,29 @@ def run_configs(which, steps, warmup):
                 us, err = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup)
                 extra = {}
                 if n > 1:
-                    us4, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"MVM": 0})
-                    usm, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup, {"MVM": 2})
+                    us4, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup,
+                                      {"MVM": 0, "MVD": 0})
+                    usm, _ = _mv_case(L, stream, "Q4_0", ws, raw, rows, 4096, X[:n], steps, warmup,
+                                      {"MVM": 2, "MVD": 0})
                     extra = {"us_dot4_kernel": round(us4, 3), "us_matrix_core_kernel": round(usm, 3)}
                 _record("q4_0", f"Q4_0 {rows}x4096 n={n}", "Q4_0", us, alg_bytes("Q4_0", rows, 4096, n), err, **extra)
             del ws
+
+    if which in ("fewtoken", "all"):
+        # 2..16 tokens of the other formats (speculative verification, small batches) on the dense-read
+        # matrix-core kernel: 14336x4096 and 4096x4096, W ~N(0,0.02) (seed 81), x ~N(0,1) (seed 82); beside
+        # each, the launch plan without that kernel (the other matrix-core kernel or dot4)
+        for rows in (14336, 4096):
+            for fmt in ("Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"):
+                raw = make_weights(fmt, rows, 4096, 81)
+                ws = _copies(torch.from_numpy(raw).cuda())
+                X = _x(82, (16, 4096))
+                for n in (2, 4, 8, 16):
+                    us, err = _mv_case(L, stream, fmt, ws, raw, rows, 4096, X[:n], steps, warmup)
+                    uso, _ = _mv_case(L, stream, fmt, ws, raw, rows, 4096, X[:n], steps, warmup, {"MVD": 0})
+                    _record("fewtoken", f"{fmt} {rows}x4096 n={n}", fmt, us, alg_bytes(fmt, rows, 4096, n), err,
+                            us_without_dense_kernel=round(uso, 3))
+                del ws
 
     if which in ("lowbit", "all"):
         # TQ2_0: codes i.i.d. P(0)=0.4, P(+-1)=0.3, d = fp16(|N(0,0.02)|) (seed 51); IQ2_XXS from N(0,0.02)
@@ -621,7 +639,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-layer", action="store_true", help="skip the per-layer timing")
     ap.add_argument("--config", default="headline",
-                    choices=("headline", "q8_0", "speculative", "q4_0", "lowbit", "prefill", "moe", "offload", "ceiling",
+                    choices=("headline", "q8_0", "speculative", "q4_0", "fewtoken", "lowbit", "prefill", "moe", "offload", "ceiling",
                              "all"),
                     help="headline (default): the metric line; the others print one record per case of "
                          "the other workloads (Q8_0 batch 1, speculative verify n=1..8, Q4_0, TQ2_0/IQ2_XXS, "

@@ -811,11 +811,12 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     float2* xsc = (float2*)(lds + 16 * RS);
     u8* buf = lds + 16 * RS + 2 * p.n_in + wave * 16 * ROW;
 
-    // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2 (absent tokens re-read xq's first
-    // bytes), 1 KB per instruction, instruction i = row i / MB, kilobyte i % MB, over the waves
-    for (int r = wave; r < 16; r += W) {
+    // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2, 1 KB per instruction, over the waves.
+    // The rows of absent tokens are not read: their LDS bytes only enter MFMA result rows of those tokens,
+    // which are never stored (the integer products of whatever the LDS holds), and their (xd, xs) are 0.
+    for (int r = wave; r < 2 * p.nc; r += W) {
         const int t = r >> 1;
-        const int8_t* row = t < p.nc ? ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in : p.xq;
+        const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in;
         for (int m = 0; 1024 * m < p.n_in; ++m)
             if (1024 * m + 16 * lane < p.n_in) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
     }
@@ -903,14 +904,14 @@ struct MvdShape {
     size_t lds;
 };
 
-// MVD_MIN (Q4_K: 5, Q6_K: 3, the others: 2) .. 8 tokens, rows of up to 4096 values (a multiple of 256 CHB, and of
+// MVD_MIN (Q4_K: 5, the others: 2) .. 8 tokens, rows of up to 4096 values (a multiple of 256 CHB, and of
 // 16 bytes): tiles of 16 rows, about one workgroup of 4 .. 16 waves per CU, K slices of 1 or 2 chunks of
 // CHB blocks.  The weights must start at a 16-byte boundary (global_load_lds_dwordx4).
 template <int F>
 inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, const void* w) {
     constexpr int CHB = Dma<F>::CHB;
     MvdShape s{};
-    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : (F == NMQ_Q6_K ? 3 : 2)) || nc > 8 || n_in % (256 * CHB) ||
+    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : 2) || nc > 8 || n_in % (256 * CHB) ||
         n_in > 4096 || (uintptr_t)w % 16 || (int64_t)n_in / 256 * Mfma<F>::BB % 16)
         return s;
     const int nblk = n_in / 256;

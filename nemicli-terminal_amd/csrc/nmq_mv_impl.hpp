@@ -2268,9 +2268,9 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             return launch_mv<F>(q, nc - 8, n_mats, stream);
         }
     }
-    // The dense-read matrix-core kernel: from 2 tokens, Q6_K from 3 (at 2 the dot4 kernel is faster:
-    // 4096x4096 6.8 against 7.2 us), Q4_K from 5 (MVD_MIN; at 4 tokens it beats the few-token loop below,
-    // 14336x4096 10.8 against 12.7 us, but 2..4 tokens keep outputs equal to one-token launches bit for bit)
+    // The dense-read matrix-core kernel: from 2 tokens, Q4_K from 5 (MVD_MIN; at 4 tokens it beats the
+    // few-token loop below, 14336x4096 10.6 against 12.9 us, but 2..4 tokens keep outputs equal to
+    // one-token launches bit for bit)
     {
         if (nc >= 2 && p.ids == nullptr) {
             const MvdShape sd = plan_mvd<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big, p.w);

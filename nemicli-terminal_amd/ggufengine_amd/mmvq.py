@@ -12,8 +12,9 @@ gfx950 device, and calls raise.
 
 Differences from the reference (documented, same results within the parity tolerance):
   - up to 16 tokens per launch on the int8 matrix cores, SPALTEN = 8 on the dot4 kernels (the
-    reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for Q4_K and 4
-    for Q6_K, measured on MI355X (the reference: 16);
+    reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for rows of up to
+    4096 values and, for longer rows, MMVQ_BIS_LANG: 1 for Q4_K and 4 for Q6_K, measured on MI355X (the
+    reference: 16 for both); `mv_bis(fmt, n_in)` picks between them;
   - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs on the fp16 matrix
     cores with exact integer weights and a two-stage fp16 input (about 22 bits against the
     reference's fp16 weights and input), 64 tokens per launch;
@@ -39,11 +40,21 @@ SPALTEN = _native.MAX_COLS    # tokens (input rows) per launch, weights read onc
 # weight rows per team of lanes by token count (the kernels are compiled for these)
 ZEILEN_JE_WARP = {"Q4_K": lambda nc: 1 if nc == 1 else 2, "Q6_K": lambda nc: 1 if nc == 1 else 2}
 # Most tokens per call for the int8 mat-vec kernels; from one more token on, callers take `mm` (the fp16
-# matrix cores).  Measured on MI355X (14336x4096, 4096x4096 Q4_K and 4096x14336 Q6_K): the reference's
-# 16 / 16 (mmvq.py:32) become 8 / 4 here (Q6_K 4096x14336 through mv / mm: 2-4 tokens 22-26 / 35-36 us,
-# 5 tokens 51 / 36 us).
-MMVQ_BIS = {"Q4_K": 8, "Q6_K": 4}
+# matrix cores); the reference's 16 / 16 (mmvq.py:32).  Measured on MI355X, each call with its input
+# launch (mv / mm, us):
+#   rows of up to 4096 values (the dense-read matrix-core kernel up to 8 tokens): Q4_K 14336x4096 at 8
+#   tokens 13.3 / 25.0, at 9 19.7 / 25.0, at 12 26.0 / 25.1; Q6_K 14336x4096 at 8 22.5 / 32.8, at 9
+#   31.8 / 32.8, at 12 41.0 / 33.0; 4096x4096 at 9 11.0 / 11.0 (Q4_K), 13.8 / 13.3 (Q6_K);
+#   longer rows: Q4_K 4096x14336 at 2 tokens 27.9 / 25.0, at 4 39.0 / 25.5; Q6_K 4096x14336 at 2-4
+#   tokens 20.3-26.6 / 35.8-36.3 (the few-token long-row kernel), at 5 51.2 / 36.6.
+MMVQ_BIS = {"Q4_K": 8, "Q6_K": 8}
+MMVQ_BIS_LANG = {"Q4_K": 1, "Q6_K": 4}
 MMQ_BIS = {"Q4_K": 112, "Q6_K": 112}
+
+
+def mv_bis(fmt: str, n_in: int) -> int:
+    """Most tokens per call that go to `mv` for rows of n_in values (more go to `mm`)."""
+    return MMVQ_BIS[fmt] if n_in <= 4096 else MMVQ_BIS_LANG[fmt]
 
 
 def verfuegbar(device, fmt: str, n_in: int) -> bool:

@@ -7,7 +7,8 @@ table: an ordered list of (most input rows, kernel) pairs from what the device o
 and row length; a call takes the first route whose bound covers its row count M and otherwise unpacks
 W to the compute dtype and multiplies.  The bounds are the reference's (`_rechnen`, common.py:400-431):
 
-  Q4_K, Q6_K (mmvq formats)          M <= mmvq.MMVQ_BIS   the int8 mat-vec kernels (mmvq.mv)
+  Q4_K, Q6_K (mmvq formats)          M <= mmvq.mv_bis     the int8 mat-vec kernels (mmvq.mv; MMVQ_BIS,
+                                                          or MMVQ_BIS_LANG for rows beyond 4096 values)
                                      M <= mmvq.MMQ_BIS    the fp16 matrix-core kernel (mmvq.mm)
   Q4_0, Q8_0, TQ2_0, IQ2_XXS         M == 1               the gathered kernel with expert id 0 (cudakern.mv)
                                      M <= mm_bis          the several-token kernels (cudakern.mm)
@@ -46,7 +47,7 @@ def unpack(fmt_type: int, raw: torch.Tensor, n_rows: int, n_in: int) -> torch.Te
 def routes(name: str, device, n_in: int, mm_limit: int) -> List[Route]:
     """The kernels a layer of format `name` and row length n_in can use on `device`, by input rows."""
     if name in mmvq.FORMATE and mmvq.verfuegbar(device, name, n_in):
-        return [(mmvq.MMVQ_BIS[name], "mmvq.mv"), (mmvq.MMQ_BIS[name], "mmvq.mm")]
+        return [(mmvq.mv_bis(name, n_in), "mmvq.mv"), (mmvq.MMQ_BIS[name], "mmvq.mm")]
     if cudakern.verfuegbar(device, name, n_in):
         return [(1, "cudakern.mv"), (mm_limit, "cudakern.mm")]
     return []

@@ -34,7 +34,8 @@ def dev(a):
 
 # (format, tokens M, branch of PackedLinear._rechnen expected)
 DISPATCH = [("Q4_K", 1, "mmvq.mv"), ("Q4_K", 8, "mmvq.mv"), ("Q4_K", 9, "mmvq.mm"), ("Q4_K", 40, "mmvq.mm"),
-            ("Q4_K", 120, "unpack"), ("Q6_K", 4, "mmvq.mv"), ("Q6_K", 5, "mmvq.mm"), ("Q6_K", 17, "mmvq.mm"),
+            ("Q4_K", 120, "unpack"), ("Q6_K", 4, "mmvq.mv"), ("Q6_K", 8, "mmvq.mv"), ("Q6_K", 9, "mmvq.mm"),
+            ("Q6_K", 17, "mmvq.mm"),
             ("TQ2_0", 1, "cudakern.mv"), ("TQ2_0", 5, "cudakern.mm"), ("TQ2_0", 17, "unpack"),
             ("IQ2_XXS", 1, "cudakern.mv"), ("IQ2_XXS", 16, "cudakern.mm"), ("Q8_0", 1, "cudakern.mv"),
             ("Q8_0", 8, "cudakern.mm"), ("Q8_0", 24, "unpack"), ("Q4_0", 1, "cudakern.mv"),

@@ -129,3 +129,14 @@ def test_hostmem_without_gpu():
     with pytest.raises(ValueError):
         hostmem.abbilden(t, "cpu")
     assert hostmem.ram_reicht(0) in (True, False)
+
+
+def test_mat_vec_bound_by_row_length():
+    """Where PackedLinear switches from the int8 mat-vec kernels to the fp16 matrix cores: 8 tokens for
+    rows of up to 4096 values (the dense-read kernel), for longer rows 1 (Q4_K) and 4 (Q6_K, the
+    few-token long-row kernel)."""
+    from ggufengine_amd import mmvq
+    assert mmvq.mv_bis("Q4_K", 4096) == 8 and mmvq.mv_bis("Q6_K", 4096) == 8
+    assert mmvq.mv_bis("Q4_K", 1024) == 8 and mmvq.mv_bis("Q6_K", 2048) == 8
+    assert mmvq.mv_bis("Q4_K", 14336) == 1 and mmvq.mv_bis("Q6_K", 14336) == 4
+    assert mmvq.mv_bis("Q4_K", 4352) == 1 and mmvq.mv_bis("Q6_K", 4352) == 4

@@ -785,10 +785,10 @@ struct Dma<NMQ_IQ2_XXS> {
     }
 };
 
-// LDS: input rows 16 x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
+// LDS: input rows 2 nc x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
 template <int F>
-__host__ __device__ constexpr size_t mvd_lds(int n_in, int W) {
-    return (size_t)16 * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * Dma<F>::SLOTS;
+__host__ __device__ constexpr size_t mvd_lds(int n_in, int W, int nc) {
+    return (size_t)2 * nc * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * Dma<F>::SLOTS;
 }
 
 template <int F, int NCH>
@@ -808,13 +808,14 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
     const int n = lane & 15, kb = lane >> 4;
     const int b0 = slice * D::CHB * NCH;
-    float2* xsc = (float2*)(lds + 16 * RS);
-    u8* buf = lds + 16 * RS + 2 * p.n_in + wave * 16 * ROW;
+    const int NR = 2 * p.nc;  // input rows in LDS
+    float2* xsc = (float2*)(lds + NR * RS);
+    u8* buf = lds + NR * RS + 2 * p.n_in + wave * 16 * ROW;
 
     // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2, 1 KB per instruction, over the waves.
-    // The rows of absent tokens are not read: their LDS bytes only enter MFMA result rows of those tokens,
-    // which are never stored (the integer products of whatever the LDS holds), and their (xd, xs) are 0.
-    for (int r = wave; r < 2 * p.nc; r += W) {
+    // Only the present tokens' rows are held: the lanes of absent tokens' A rows read the last row, whose
+    // products enter only MFMA result rows of those tokens, which are never stored (their (xd, xs) are 0).
+    for (int r = wave; r < NR; r += W) {
         const int t = r >> 1;
         const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in;
         for (int m = 0; 1024 * m < p.n_in; ++m)
@@ -856,7 +857,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     }
     lds_barrier();
 
-    const u8* arow = lds + n * RS + 8 * kb;
+    const u8* arow = lds + min(n, NR - 1) * RS + 8 * kb;
     float acc[2] = {0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
@@ -916,12 +917,18 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, cons
         return s;
     const int nblk = n_in / 256;
     const int tiles = (n_out + 15) / 16;
+    // workgroups per CU aimed at: two of half the waves for up to 4 tokens on more rows than CUs x 16
+    // (the staged input is smaller; 14336x4096 at 2 / 4 tokens: Q6_K 19.3 / 19.5 -> 18.2 / 18.5 us, Q8_0
+    // 16.5 / 16.6 -> 15.7 / 16.3, Q4_0 11.4 / 11.6 -> 11.3 / 11.4; TQ2_0 and IQ2_XXS 0.2-0.4 us slower,
+    // so they keep one; at 8 tokens every format is slower with two)
+    const int wgpc_def = nc <= 4 && tiles > cus && F != NMQ_TQ2_0 && F != NMQ_IQ2_XXS ? 2 : 1;
+    const int wgpc = std::max(1, std::min(tune(TUNE_MVD_WGPC, wgpc_def), 4));
     int tpw = tune(TUNE_MVD_TPW, 0);
-    if (tpw <= 0) tpw = std::min((tiles + cus - 1) / cus, 8);
+    if (tpw <= 0) tpw = std::min((tiles + cus * wgpc - 1) / (cus * wgpc), 8);
     int ks = tune(TUNE_MVD_KS, 0);
     if (ks <= 0) {
         ks = 1;
-        while (ks * 2 * tpw <= 16 && nblk % (ks * 2 * CHB) == 0) ks *= 2;  // slices of at least one chunk
+        while (ks * 2 * tpw <= 16 / wgpc && nblk % (ks * 2 * CHB) == 0) ks *= 2;  // slices of at least one chunk
     }
     if (tune(TUNE_MVD_TPW, 0) <= 0 && tune(TUNE_MVD_KS, 0) <= 0) {
         // slices of more than 2 chunks: fewer tiles per workgroup, more slices (Q8_0 14336x4096 at 8
@@ -937,7 +944,7 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, cons
     s.ks = ks;
     s.tpw = tpw;
     s.grid_x = (tiles + tpw - 1) / tpw;
-    s.lds = mvd_lds<F>(n_in, ks * tpw);
+    s.lds = mvd_lds<F>(n_in, ks * tpw, nc);
     s.ok = s.lds + 4096 <= (size_t)lds_max;
     return s;
 }

@@ -311,6 +311,27 @@ def test_mv_tokens_dense_mfma(nmq, oracle, tune, fmt, shape, split):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt):
+    """9..16 tokens where the dense-read kernel takes 8: two launches (8 and the rest, the rest on its own
+    kernel: one-token, few-token or dense), against the oracle."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out, n_in = 1000, 4096
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=77)
+    raw_d = dev(raw)
+    for nc in (9, 10, 12, 13, 16):
+        x = np.random.default_rng(78 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        x[nc - 1, 11] = 40.0
+        e = quant_dev(dev(x))
+        y = torch.full((nc, n_out), float("nan"), device="cuda")
+        say("mv 9..16 tokens dense pairs", fmt, nc)
+        nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                   e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                   nmq.stream_ptr()))
+        torch.cuda.synchronize()
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
+
+
 @pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"])
 def test_mv_tokens_weights_off_16_bytes(nmq, oracle, fmt):
     """Weights 2 bytes past a 16-byte boundary (allowed for every format but Q4_K): the dense-read

@@ -426,16 +426,16 @@ __global__ __launch_bounds__(1024) void mvm_kernel(MvmParams p) {
 // bytes).  mvd_kernel keeps mvm_kernel's work split and arithmetic, but every read is dense (16 bytes per
 // lane, consecutive lanes on consecutive bytes), and weights and input move with global_load_lds_dwordx4
 // (lane l's 16 bytes land at the LDS address of the instruction + 16 l, no registers in between):
-//   - the input rows (xq, xq2 of each token) row-major, 16 + n_in bytes apart, so that the 16 rows' A
-//     operands of a step (8 bytes at row n, 32 step + 8 k-block) fall on distinct banks;
+//   - the input rows (xq, xq2 of each present token: 2 nc rows) row-major, 16 + n_in bytes apart, so that
+//     the A operands of a step (8 bytes at row n, 32 step + 8 k-block) fall on distinct banks;
 //   - the weights, per wave in chunks of CHB 256-value blocks x 16 rows (Q4_K, Q4_0: 2 blocks of 144
 //     bytes; Q8_0: 1 block of 272 bytes, 8 GGUF blocks of 34; Q6_K: 1 block of 210; TQ2_0, IQ2_XXS: 2
 //     blocks of 66): a chunk row is the 16-byte window from the 16-byte boundary at or below the chunk's
 //     first byte (m bytes before it: 0 where CHB blocks fill whole pieces), PR pieces of 16 bytes; slot
 //     u = 64 j + lane of instruction j holds piece min(u % SLOTS, PR - 1) of row u / SLOTS (the slots
 //     past PR padding copies of the last piece; SLOTS = 19, 15 or 11 puts the 16 rows' operands on
-//     distinct banks).  Rows whose bytes sit off a 4-byte boundary in the window are read as dwords
-//     and shifted into place with v_alignbyte.
+//     distinct banks).  Fields (codes, scales) that sit off a 4-byte boundary in the window are read as
+//     dwords and shifted into place with v_alignbyte.
 // (xd / 254, xs) per step and token are read densely into registers and stored as mvm_kernel stores them.
 // A wave holds one chunk buffer: chunk c + 1 is requested as soon as chunk c's operands are in registers,
 // and streams in while chunk c is computed.
@@ -459,9 +459,9 @@ __device__ __forceinline__ void vm_wait() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Per-lane offsets of the chunk reads (the same for every chunk), from the chunk's first byte in row
-// rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % 19, PR - 1) of row
-// min(row0 + u / 19, n_out - 1) >= rb0, so every offset is non-negative, also for tiles past the matrix.
+// Per-lane offsets of the chunk reads (the same for every chunk), from the window's first byte in row
+// rb0 = min(row0, n_out - 1): slot u = 64 j + lane holds piece min(u % SLOTS, PR - 1) of row
+// min(row0 + u / SLOTS, n_out - 1) >= rb0, so every offset is non-negative, also for tiles past the matrix.
 template <int NI>
 struct ChunkOffsets {
     u32 o[NI];

@@ -42,6 +42,8 @@ struct MvmParams {
     int tpw;      // tiles per workgroup
     int64_t row_bytes;
     int nblk;     // 256-value blocks per row
+    int x_stride;  // mvd_kernel: values from one token's input to the next (the whole row of a K range)
+    int acc_y;     // mvd_kernel: add the sums to y instead of writing them
 };
 
 // Per-format pieces of the MFMA path.  Steps are 32 values; GS = values per scale group (Q6_K: 16,
@@ -817,7 +819,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     // products enter only MFMA result rows of those tokens, which are never stored (their (xd, xs) are 0).
     for (int r = wave; r < NR; r += W) {
         const int t = r >> 1;
-        const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.n_in;
+        const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.x_stride;
         for (int m = 0; 1024 * m < p.n_in; ++m)
             if (1024 * m + 16 * lane < p.n_in) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
     }
@@ -830,7 +832,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     for (int k = 0; k < 2; ++k) {
         const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
         const bool ok = i < 4 * S && t < p.nc;
-        xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * S + 4 * m : p.xd);
+        xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * (p.x_stride / 32) + 4 * m : p.xd);
     }
     u32x2 gv = tab_load_hand<F>();  // IQ2_XXS: this thread's grid entry (W >= 4: 256 threads)
     // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
@@ -891,8 +893,10 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
         }
         const int t = 2 * kb;
         if (r < p.n_out) {
-            if (t < p.nc) gpw<float>(p.y)[(int64_t)t * p.n_out + r] = s0;
-            if (t + 1 < p.nc) gpw<float>(p.y)[(int64_t)(t + 1) * p.n_out + r] = s1;
+            auto* y0 = gpw<float>(p.y) + (int64_t)t * p.n_out + r;
+            auto* y1 = y0 + p.n_out;
+            if (t < p.nc) *y0 = p.acc_y ? *y0 + s0 : s0;
+            if (t + 1 < p.nc) *y1 = p.acc_y ? *y1 + s1 : s1;
         }
     }
 }
@@ -909,10 +913,11 @@ struct MvdShape {
 // 16 bytes): tiles of 16 rows, about one workgroup of 4 .. 16 waves per CU, K slices of 1 or 2 chunks of
 // CHB blocks.  The weights must start at a 16-byte boundary (global_load_lds_dwordx4).
 template <int F>
-inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, const void* w) {
+inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, const void* w, int min_nc = 0) {
     constexpr int CHB = Dma<F>::CHB;
     MvdShape s{};
-    if (!tune(TUNE_MVD, 1) || nc < tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : 2) || nc > 8 || n_in % (256 * CHB) ||
+    if (min_nc <= 0) min_nc = tune(TUNE_MVD_MIN, F == NMQ_Q4_K ? 5 : 2);
+    if (!tune(TUNE_MVD, 1) || nc < min_nc || nc > 8 || n_in % (256 * CHB) ||
         n_in > 4096 || (uintptr_t)w % 16 || (int64_t)n_in / 256 * Mfma<F>::BB % 16)
         return s;
     const int nblk = n_in / 256;
@@ -958,6 +963,7 @@ template <int F>
 inline int launch_mvd(const MvdShape& s, MvmParams p, hipStream_t stream) {
     p.ks = s.ks;
     p.tpw = s.tpw;
+    if (p.x_stride == 0) p.x_stride = p.n_in;
     hipLaunchKernelGGL(pick_mvd<F>(s), dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
     return (int)hipGetLastError();
 }

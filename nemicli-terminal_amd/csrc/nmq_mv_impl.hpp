@@ -2329,6 +2329,39 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
             }
         }
     }
+    // Rows beyond the dense kernel's 4096 values, 2..8 tokens of one matrix (Q6_K: from 5, after the
+    // few-token long-row kernel above): K ranges of 4096 values (the last one shorter), one dense launch
+    // each, in range order on the stream, each adding its sums to y (the first writes it), so the
+    // result does not depend on timing.  The rows and the ranges must start on 16-byte boundaries.
+    if (nc >= 2 && nc <= 8 && p.ids == nullptr && p.xv == nullptr && p.n_seg == 0 && p.n_in > 4096 &&
+        p.n_in <= 8 * 4096 && p.row_bytes % 16 == 0 && tune(TUNE_MVD_LONG, 1) != 0) {
+        constexpr int R = 4096;
+        const int nr = (p.n_in + R - 1) / R;
+        MvdShape sh[8];
+        bool ok = true;
+        for (int j = 0; j < nr && ok; ++j) {
+            const int k0 = j * R, len = p.n_in - k0 < R ? p.n_in - k0 : R;
+            const int64_t off = (int64_t)(k0 / 256) * Mfma<F>::BB;
+            sh[j] = plan_mvd<F>(p.n_out, len, nc, di.cus, di.lds_max_big, p.w + off, 2);
+            ok = sh[j].ok && off % 16 == 0;
+        }
+        if (ok) {
+            for (int j = 0; j < nr; ++j) {
+                const int k0 = j * R, len = p.n_in - k0 < R ? p.n_in - k0 : R;
+                MvmParams q{};
+                q.w = p.w + (int64_t)(k0 / 256) * Mfma<F>::BB;
+                q.xq = p.xq + k0; q.xq2 = p.xq2 + k0; q.xd = p.xd + k0 / 32; q.xs = p.xs + k0 / 32; q.y = p.y;
+                q.n_out = p.n_out; q.n_in = len; q.nc = nc;
+                q.row_bytes = p.row_bytes;
+                q.nblk = len / 256;
+                q.x_stride = p.n_in;
+                q.acc_y = j > 0;
+                const int e = launch_mvd<F>(sh[j], q, stream);
+                if (e) return e;
+            }
+            return 0;
+        }
+    }
     if (nc >= 2 && p.ids == nullptr) {
         const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
         if (sm.ok) {

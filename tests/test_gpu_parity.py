@@ -332,6 +332,36 @@ def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt):
         _check_mv(oracle, fmt, raw, n_out, n_in, x, y)
 
 
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("shape", [(4096, 14336), (300, 8192), (130, 6144)])
+def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape):
+    """2..8 tokens on rows beyond 4096 values: dense-read launches over K ranges of 4096 values (the last
+    shorter), each adding its sums to y in range order; against the oracle, and two calls bit for bit
+    equal (the order of the additions is fixed).  Q6_K 2..4 tokens take the few-token long-row kernel
+    by default, so its ranges are forced on with that kernel off."""
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out, n_in = shape
+    if fmt == "Q6_K":
+        tune(MVLT_MAX=1)
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=79 + n_in % 89)
+    raw_d = dev(raw)
+    for nc in ((2, 5, 8) if n_out > 1000 else (2, 3, 4, 5, 6, 7, 8)):
+        x = np.random.default_rng(80 + nc).standard_normal((nc, n_in)).astype(np.float32)
+        x[:, 5000 % n_in] = -30.0
+        e = quant_dev(dev(x))
+        ys = []
+        for rep in range(2):
+            y = torch.full((nc, n_out), float("nan"), device="cuda")
+            say("mv tokens long rows", fmt, shape, nc, rep)
+            nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
+                                       e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
+                                       nmq.stream_ptr()))
+            torch.cuda.synchronize()
+            ys.append(y)
+        assert torch.equal(ys[0], ys[1])
+        _check_mv(oracle, fmt, raw, n_out, n_in, x, ys[0])
+
+
 @pytest.mark.parametrize("fmt", ["Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"])
 def test_mv_tokens_weights_off_16_bytes(nmq, oracle, fmt):
     """Weights 2 bytes past a 16-byte boundary (allowed for every format but Q4_K): the dense-read

@@ -133,10 +133,10 @@ def test_hostmem_without_gpu():
 
 def test_mat_vec_bound_by_row_length():
     """Where PackedLinear switches from the int8 mat-vec kernels to the fp16 matrix cores: 8 tokens for
-    rows of up to 4096 values (the dense-read kernel), for longer rows 1 (Q4_K) and 4 (Q6_K, the
-    few-token long-row kernel)."""
+    rows of up to 4096 values (the dense-read kernel), for longer rows 5 (Q4_K) and 8 (Q6_K; the dense
+    kernel over K ranges, Q6_K 2..4 tokens on the few-token long-row kernel)."""
     from ggufengine_amd import mmvq
     assert mmvq.mv_bis("Q4_K", 4096) == 8 and mmvq.mv_bis("Q6_K", 4096) == 8
     assert mmvq.mv_bis("Q4_K", 1024) == 8 and mmvq.mv_bis("Q6_K", 2048) == 8
-    assert mmvq.mv_bis("Q4_K", 14336) == 1 and mmvq.mv_bis("Q6_K", 14336) == 4
-    assert mmvq.mv_bis("Q4_K", 4352) == 1 and mmvq.mv_bis("Q6_K", 4352) == 4
+    assert mmvq.mv_bis("Q4_K", 14336) == 5 and mmvq.mv_bis("Q6_K", 14336) == 8
+    assert mmvq.mv_bis("Q4_K", 4352) == 5 and mmvq.mv_bis("Q6_K", 4352) == 8

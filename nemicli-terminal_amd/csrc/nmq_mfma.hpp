@@ -44,6 +44,7 @@ struct MvmParams {
     int nblk;     // 256-value blocks per row
     int x_stride;  // mvd_kernel: values from one token's input to the next (the whole row of a K range)
     int acc_y;     // mvd_kernel: add the sums to y instead of writing them
+    int nr, rb;    // mvd_kernel<..., KL>: K ranges of rb blocks, staged one after another
 };
 
 // Per-format pieces of the MFMA path.  Steps are 32 values; GS = values per scale group (Q6_K: 16,
@@ -793,7 +794,10 @@ __host__ __device__ constexpr size_t mvd_lds(int n_in, int W, int nc) {
     return (size_t)2 * nc * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * Dma<F>::SLOTS;
 }
 
-template <int F, int NCH>
+// KL: rows beyond the LDS's input capacity, as p.nr K ranges of p.rb blocks in one launch: each range's
+// input is staged after every wave is done with the previous one's, the wave's slice of each range runs
+// through its chunk buffer, and the sums of all ranges add up in the wave's registers.
+template <int F, int NCH, bool KL = false>
 __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     using D = Dma<F>;
     constexpr int ROW = 16 * D::SLOTS;              // LDS bytes per row of a chunk buffer
@@ -805,23 +809,32 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     __shared__ u64 tab[F == NMQ_IQ2_XXS ? 384 : 1];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int W = p.ks * p.tpw, nt = 64 * W;
-    const int S = p.n_in / 32, RS = p.n_in + 16;
+    const int KV = KL ? p.rb * 256 : p.n_in;  // values per K range (the whole row without ranges)
+    const int S = KV / 32, RS = KV + 16;
     const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
     const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
     const int n = lane & 15, kb = lane >> 4;
     const int b0 = slice * D::CHB * NCH;
     const int NR = 2 * p.nc;  // input rows in LDS
     float2* xsc = (float2*)(lds + NR * RS);
-    u8* buf = lds + NR * RS + 2 * p.n_in + wave * 16 * ROW;
+    u8* buf = lds + NR * RS + 2 * KV + wave * 16 * ROW;
+    u32x2 gv = tab_load_hand<F>();  // IQ2_XXS: this thread's grid entry (W >= 4: 256 threads)
+    const ChunkOffsets<NI> co = mvd_offsets<D::PR, D::SLOTS, NI>(p, row0, lane);
+    const u8* arow = lds + min(n, NR - 1) * RS + 8 * kb;
+    float acc[2] = {0.f, 0.f};
+    const int nr = KL ? p.nr : 1;
+    for (int j = 0; j < nr; ++j) {
+    const int k0 = j * KV, jb = j * (KV / 256);  // the range's first value and block
+    if (KL && j > 0) lds_barrier();  // every wave done with the previous range's input
 
     // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2, 1 KB per instruction, over the waves.
     // Only the present tokens' rows are held: the lanes of absent tokens' A rows read the last row, whose
     // products enter only MFMA result rows of those tokens, which are never stored (their (xd, xs) are 0).
     for (int r = wave; r < NR; r += W) {
         const int t = r >> 1;
-        const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.x_stride;
-        for (int m = 0; 1024 * m < p.n_in; ++m)
-            if (1024 * m + 16 * lane < p.n_in) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
+        const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.x_stride + k0;
+        for (int m = 0; 1024 * m < KV; ++m)
+            if (1024 * m + 16 * lane < KV) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
     }
     // (xd, xs): piece i < 4 S = 4 consecutive steps (of S / 4 groups of 4) of token i & 7 of xd
     // (i / 8 < S / 4) or xs, read by hand.  Every thread issues both reads (threads past the pieces and
@@ -832,20 +845,18 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     for (int k = 0; k < 2; ++k) {
         const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
         const bool ok = i < 4 * S && t < p.nc;
-        xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * (p.x_stride / 32) + 4 * m : p.xd);
+        xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * (p.x_stride / 32) + k0 / 32 + 4 * m : p.xd);
     }
-    u32x2 gv = tab_load_hand<F>();  // IQ2_XXS: this thread's grid entry (W >= 4: 256 threads)
     // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
     // request order, so input requested after another wave's weights would wait for them (the barrier
     // waits for issue only: the reads are not counted by the compiler's waits)
-    const ChunkOffsets<NI> co = mvd_offsets<D::PR, D::SLOTS, NI>(p, row0, lane);
     lds_barrier();
-    mvd_chunk<F, NI>(buf, p, co, row0, b0, lane);
+    mvd_chunk<F, NI>(buf, p, co, row0, jb + b0, lane);
     if constexpr (F == NMQ_IQ2_XXS)
         asm volatile("s_waitcnt vmcnt(%3)" : "+v"(xv[0]), "+v"(xv[1]), "+v"(gv) : "n"(NI) : "memory");
     else
         asm volatile("s_waitcnt vmcnt(%2)" : "+v"(xv[0]), "+v"(xv[1]) : "n"(NI) : "memory");
-    tab_store_hand<F>(tab, gv, nt);
+    if (j == 0) tab_store_hand<F>(tab, gv, nt);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
         const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
@@ -859,23 +870,22 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     }
     lds_barrier();
 
-    const u8* arow = lds + min(n, NR - 1) * RS + 8 * kb;
-    float acc[2] = {0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
         vm_wait<0>();  // chunk c in the buffer
         typename D::Raw r;
-        D::frag(r, buf + n * ROW, (int)(((int64_t)(b0 + D::CHB * c) * Mfma<F>::BB) & 15), kb);
+        D::frag(r, buf + n * ROW, (int)(((int64_t)(jb + b0 + D::CHB * c) * Mfma<F>::BB) & 15), kb);
         if (c + 1 < NCH) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the operands read before the buffer is refilled
-            mvd_chunk<F, NI>(buf, p, co, row0, b0 + D::CHB * (c + 1), lane);
+            mvd_chunk<F, NI>(buf, p, co, row0, jb + b0 + D::CHB * (c + 1), lane);
         }
 #pragma unroll
         for (int i = 0; i < D::CHB; ++i) {
-            const int b = b0 + D::CHB * c + i;
+            const int b = b0 + D::CHB * c + i;  // block of the range
             D::block(r, i, arow + 256 * b, xsc + 64 * b + 2 * kb, kb, tab, acc);
         }
     }
+    }  // K ranges
 
     // add the KS slices of each tile (as mvm_kernel)
     float* red = (float*)lds;
@@ -906,6 +916,7 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
 struct MvdShape {
     bool ok;
     int ks, tpw, grid_x, nch;
+    int nr, rb;  // K ranges (the launch over long rows)
     size_t lds;
 };
 
@@ -952,6 +963,56 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, cons
     s.lds = mvd_lds<F>(n_in, ks * tpw, nc);
     s.ok = s.lds + 4096 <= (size_t)lds_max;
     return s;
+}
+
+// Rows of 4097 .. 32768 values, 2..8 tokens, in one launch: nr equal K ranges of rb blocks (below), one
+// tile per workgroup when the rows allow, the most slices (up to 16 waves) whose slice of a range is 1
+// or 2 chunks.
+template <int F>
+inline MvdShape plan_mvd_long(int n_out, int n_in, int nc, int cus, int lds_max, const void* w, int64_t row_bytes) {
+    constexpr int CHB = Dma<F>::CHB;
+    MvdShape s{};
+    if (!tune(TUNE_MVD, 1) || nc < 2 || nc > 8 || n_in % 256 || n_in <= 4096 || n_in > 8 * 4096 ||
+        (uintptr_t)w % 16 || row_bytes % 16)
+        return s;
+    // ranges: the most blocks up to 16 that divide the row, fill whole chunks and start on 16-byte
+    // boundaries (14336 values: 4 ranges of 14 blocks for Q4_K, Q4_0, Q8_0; 7 of 8 for the 210- and
+    // 66-byte blocks); at least 8 blocks
+    const int nblk = n_in / 256;
+    int rb = 0;
+    for (int c = std::min(16, nblk); c >= 8 && rb == 0; --c)
+        if (nblk % c == 0 && c % CHB == 0 && (int64_t)c * Mfma<F>::BB % 16 == 0) rb = c;
+    if (rb == 0) return s;
+    const int nr = nblk / rb;
+    const int tiles = (n_out + 15) / 16;
+    int tpw = tune(TUNE_MVD_TPW, 0);
+    if (tpw <= 0) tpw = std::min((tiles + cus - 1) / cus, 8);
+    int ks = tune(TUNE_MVD_KS, 0);
+    if (ks <= 0)
+        for (int k = 16 / tpw; k >= 1 && ks <= 0; --k)
+            if (rb % (k * CHB) == 0 && rb / (k * CHB) <= 2) ks = k;
+    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || rb % (ks * CHB) || rb / (ks * CHB) > 2) return s;
+    s.nch = rb / (ks * CHB);
+    s.ks = ks;
+    s.tpw = tpw;
+    s.grid_x = (tiles + tpw - 1) / tpw;
+    s.nr = nr;
+    s.rb = rb;
+    s.lds = mvd_lds<F>(rb * 256, ks * tpw, nc);
+    s.ok = s.lds + 4096 <= (size_t)lds_max;
+    return s;
+}
+
+template <int F>
+inline int launch_mvd_long(const MvdShape& s, MvmParams p, hipStream_t stream) {
+    p.ks = s.ks;
+    p.tpw = s.tpw;
+    p.nr = s.nr;
+    p.rb = s.rb;
+    p.x_stride = p.n_in;
+    void (*k)(MvmParams) = s.nch == 1 ? mvd_kernel<F, 1, true> : mvd_kernel<F, 2, true>;
+    hipLaunchKernelGGL(k, dim3((unsigned)s.grid_x), dim3(64 * s.ks * s.tpw), s.lds, stream, p);
+    return (int)hipGetLastError();
 }
 
 template <int F>

@@ -2334,6 +2334,18 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
     // each, in range order on the stream, each adding its sums to y (the first writes it), so the
     // result does not depend on timing.  The rows and the ranges must start on 16-byte boundaries.
     if (nc >= 2 && nc <= 8 && p.ids == nullptr && p.xv == nullptr && p.n_seg == 0 && p.n_in > 4096 &&
+        tune(TUNE_MVD_LONG, 1) == 1) {
+        const MvdShape sl = plan_mvd_long<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big, p.w, p.row_bytes);
+        if (sl.ok) {
+            MvmParams q{};
+            q.w = p.w; q.xq = p.xq; q.xq2 = p.xq2; q.xd = p.xd; q.xs = p.xs; q.y = p.y;
+            q.n_out = p.n_out; q.n_in = p.n_in; q.nc = nc;
+            q.row_bytes = p.row_bytes;
+            q.nblk = p.n_in / 256;
+            return launch_mvd_long<F>(sl, q, stream);
+        }
+    }
+    if (nc >= 2 && nc <= 8 && p.ids == nullptr && p.xv == nullptr && p.n_seg == 0 && p.n_in > 4096 &&
         p.n_in <= 8 * 4096 && p.row_bytes % 16 == 0 && tune(TUNE_MVD_LONG, 1) != 0) {
         constexpr int R = 4096;
         const int nr = (p.n_in + R - 1) / R;

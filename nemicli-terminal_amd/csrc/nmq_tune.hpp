@@ -49,7 +49,7 @@ enum Tune : int {
     TUNE_MVP_RPW,     // rows per wave and group of the dense gate|up kernel with the activation (4, 8)
     TUNE_MVP_WGS,     // its workgroups (default: the fewest groups of 32 rows per workgroup, spread evenly)
     TUNE_MVD_WGPC,    // workgroups per CU the dense-read kernel's plan aims at (1 .. 4)
-    TUNE_MVD_LONG,    // 0: no dense-read launches over K ranges for rows beyond 4096 values
+    TUNE_MVD_LONG,    // rows beyond 4096 values: 1 one dense launch over K ranges, 2 one launch per range, 0 neither
     TUNE_COUNT
 };
 

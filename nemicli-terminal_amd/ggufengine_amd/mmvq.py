@@ -13,8 +13,8 @@ gfx950 device, and calls raise.
 Differences from the reference (documented, same results within the parity tolerance):
   - up to 16 tokens per launch on the int8 matrix cores, SPALTEN = 8 on the dot4 kernels (the
     reference compiles 1..9 per launch); MMVQ_BIS (where callers switch to `mm`) is 8 for rows of up to
-    4096 values and, for longer rows, MMVQ_BIS_LANG: 5 for Q4_K and 8 for Q6_K, measured on MI355X (the
-    reference: 16 for both); `mv_bis(fmt, n_in)` picks between them;
+    4096 values or a multiple of 2048 up to 32768 and, for other rows, MMVQ_BIS_LANG: 1 for Q4_K and 4 for
+    Q6_K, measured on MI355X (the reference: 16 for both); `mv_bis(fmt, n_in)` picks between them;
   - `mm` (the reference's fp16 tensor-core MMQ tiles for 17..112 tokens) runs on the fp16 matrix
     cores with exact integer weights and a two-stage fp16 input (about 22 bits against the
     reference's fp16 weights and input), 64 tokens per launch;
@@ -45,17 +45,21 @@ ZEILEN_JE_WARP = {"Q4_K": lambda nc: 1 if nc == 1 else 2, "Q6_K": lambda nc: 1 i
 #   rows of up to 4096 values (the dense-read matrix-core kernel up to 8 tokens): Q4_K 14336x4096 at 8
 #   tokens 13.3 / 25.0, at 9 19.7 / 25.0, at 12 26.0 / 25.1; Q6_K 14336x4096 at 8 22.5 / 32.8, at 9
 #   31.8 / 32.8, at 12 41.0 / 33.0; 4096x4096 at 9 11.0 / 11.0 (Q4_K), 13.8 / 13.3 (Q6_K);
-#   longer rows (the dense kernel over K ranges of 4096 values): Q4_K 4096x14336 at 2 / 4 / 5 / 8
-#   tokens 23.9 / 24.5 / 25.1 / 26.0 against 25.0 / 25.4 / 25.5 / 25.6; Q6_K 4096x14336 at 2-4 tokens
-#   20.5-26.5 / 35.3-35.7 (the few-token long-row kernel), at 5 / 8 31.6 / 32.9 against 35.5 / 35.8.
+#   longer rows of a multiple of 2048 values (the dense kernel over K ranges in one launch): Q4_K
+#   4096x14336 at 2 / 4 / 8 tokens 14.9 / 15.6 / 17.4 against 25.2 / 25.6 / 25.9; Q6_K 4096x14336 at
+#   2-4 tokens 20.6-26.7 / 35.6-35.8 (the few-token long-row kernel), at 5 / 8 25.0 / 26.0 against
+#   35.9 / 36.1;
+#   other long rows (MMVQ_BIS_LANG): Q4_K 4096x14336 on the other kernels at 2 tokens 27.9 / 25.0, at 4
+#   39.0 / 25.5; Q6_K at 5 tokens 51.2 / 36.6.
 MMVQ_BIS = {"Q4_K": 8, "Q6_K": 8}
-MMVQ_BIS_LANG = {"Q4_K": 5, "Q6_K": 8}
+MMVQ_BIS_LANG = {"Q4_K": 1, "Q6_K": 4}
 MMQ_BIS = {"Q4_K": 112, "Q6_K": 112}
 
 
 def mv_bis(fmt: str, n_in: int) -> int:
     """Most tokens per call that go to `mv` for rows of n_in values (more go to `mm`)."""
-    return MMVQ_BIS[fmt] if n_in <= 4096 else MMVQ_BIS_LANG[fmt]
+    dense = n_in <= 4096 or (n_in % 2048 == 0 and n_in <= 32768)
+    return MMVQ_BIS[fmt] if dense else MMVQ_BIS_LANG[fmt]
 
 
 def verfuegbar(device, fmt: str, n_in: int) -> bool:

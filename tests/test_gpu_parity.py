@@ -334,13 +334,16 @@ def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("shape", [(4096, 14336), (300, 8192), (130, 6144)])
-def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape):
-    """2..8 tokens on rows beyond 4096 values: dense-read launches over K ranges of 4096 values (the last
-    shorter), each adding its sums to y in range order; against the oracle, and two calls bit for bit
-    equal (the order of the additions is fixed).  Q6_K 2..4 tokens take the few-token long-row kernel
-    by default, so its ranges are forced on with that kernel off."""
+@pytest.mark.parametrize("mode", [1, 2])
+def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape, mode):
+    """2..8 tokens on rows beyond 4096 values on the dense-read kernel over equal K ranges: one launch
+    staging the ranges one after another (mode 1, the default), or one launch per range of 4096 values
+    (the last shorter), each adding its sums to y in range order (mode 2); against the oracle, and two
+    calls bit for bit equal.  Q6_K 2..4 tokens take the few-token long-row kernel by default, so the
+    ranges are forced on with that kernel off."""
     from ggufengine_amd.gguf_types import TYPE_ID
     n_out, n_in = shape
+    tune(MVD_LONG=mode)
     if fmt == "Q6_K":
         tune(MVLT_MAX=1)
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=79 + n_in % 89)
@@ -352,7 +355,7 @@ def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape):
         ys = []
         for rep in range(2):
             y = torch.full((nc, n_out), float("nan"), device="cuda")
-            say("mv tokens long rows", fmt, shape, nc, rep)
+            say("mv tokens long rows", fmt, shape, mode, nc, rep)
             nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
                                        e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
                                        nmq.stream_ptr()))

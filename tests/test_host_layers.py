@@ -133,10 +133,13 @@ def test_hostmem_without_gpu():
 
 def test_mat_vec_bound_by_row_length():
     """Where PackedLinear switches from the int8 mat-vec kernels to the fp16 matrix cores: 8 tokens for
-    rows of up to 4096 values (the dense-read kernel), for longer rows 5 (Q4_K) and 8 (Q6_K; the dense
-    kernel over K ranges, Q6_K 2..4 tokens on the few-token long-row kernel)."""
+    rows the dense-read kernel takes (up to 4096 values, or a multiple of 2048 up to 32768 over K
+    ranges), for other rows 1 (Q4_K) and 4 (Q6_K, the few-token long-row kernel)."""
     from ggufengine_amd import mmvq
     assert mmvq.mv_bis("Q4_K", 4096) == 8 and mmvq.mv_bis("Q6_K", 4096) == 8
     assert mmvq.mv_bis("Q4_K", 1024) == 8 and mmvq.mv_bis("Q6_K", 2048) == 8
-    assert mmvq.mv_bis("Q4_K", 14336) == 5 and mmvq.mv_bis("Q6_K", 14336) == 8
-    assert mmvq.mv_bis("Q4_K", 4352) == 5 and mmvq.mv_bis("Q6_K", 4352) == 8
+    assert mmvq.mv_bis("Q4_K", 14336) == 8 and mmvq.mv_bis("Q6_K", 14336) == 8
+    assert mmvq.mv_bis("Q4_K", 28672) == 8 and mmvq.mv_bis("Q6_K", 6144) == 8
+    assert mmvq.mv_bis("Q4_K", 11008) == 1 and mmvq.mv_bis("Q6_K", 11008) == 4
+    assert mmvq.mv_bis("Q4_K", 4352) == 1 and mmvq.mv_bis("Q6_K", 4352) == 4
+    assert mmvq.mv_bis("Q4_K", 36864) == 1 and mmvq.mv_bis("Q6_K", 36864) == 4

@@ -2255,7 +2255,10 @@ int launch_mv(MvParams p, int nc, int n_mats, hipStream_t stream) {
         // both groups (14336x4096 at 16 tokens: Q4_0 52.1 -> 22.9 us, Q8_0 60.6 -> 33.2, Q4_K 24.9 -> 20.5,
         // TQ2_0 19.5 -> 16.1, IQ2_XXS 27.4 -> 24.7)
         const MvmShape sm = plan_mvm<F>(p.n_out, p.n_in, nc, di.cus, di.lds_max_big);
-        const bool dense8 = p.ids == nullptr && plan_mvd<F>(p.n_out, p.n_in, 8, di.cus, di.lds_max_big, p.w).ok;
+        const bool dense8 = p.ids == nullptr && (plan_mvd<F>(p.n_out, p.n_in, 8, di.cus, di.lds_max_big, p.w).ok ||
+                                                 (tune(TUNE_MVD_LONG, 1) == 1 &&
+                                                  plan_mvd_long<F>(p.n_out, p.n_in, 8, di.cus, di.lds_max_big, p.w,
+                                                                   p.row_bytes).ok));
         if (!(sm.ok && p.ids == nullptr) || dense8) {
             int e = launch_mv<F>(p, 8, n_mats, stream);
             if (e) return e;

@@ -312,11 +312,13 @@ def test_mv_tokens_dense_mfma(nmq, oracle, tune, fmt, shape, split):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt):
-    """9..16 tokens where the dense-read kernel takes 8: two launches (8 and the rest, the rest on its own
-    kernel: one-token, few-token or dense), against the oracle."""
+@pytest.mark.parametrize("shape", [(1000, 4096), (300, 14336)])
+def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt, shape):
+    """9..16 tokens where the dense-read kernel takes 8 (rows of 4096 values, and 14336 over K ranges):
+    two launches (8 and the rest, the rest on its own kernel: one-token, few-token or dense), against the
+    oracle."""
     from ggufengine_amd.gguf_types import TYPE_ID
-    n_out, n_in = 1000, 4096
+    n_out, n_in = shape
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=77)
     raw_d = dev(raw)
     for nc in (9, 10, 12, 13, 16):
@@ -324,7 +326,7 @@ def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt):
         x[nc - 1, 11] = 40.0
         e = quant_dev(dev(x))
         y = torch.full((nc, n_out), float("nan"), device="cuda")
-        say("mv 9..16 tokens dense pairs", fmt, nc)
+        say("mv 9..16 tokens dense pairs", fmt, shape, nc)
         nmq.check(nmq.lib().nmq_mv(TYPE_ID[fmt], raw_d.data_ptr(), e.xq.data_ptr(), e.xq2.data_ptr(),
                                    e.xd.data_ptr(), e.xs.data_ptr(), y.data_ptr(), n_out, n_in, nc,
                                    nmq.stream_ptr()))

@@ -274,15 +274,19 @@ def run_configs(which, steps, warmup):
                         **extra)
             del ws
         # the layer's down projection under the same verification: Q6_K 4096x14336 (seed 27), n in 1..4
+        # (the few-token long-row kernel) and 8 (the dense-read kernel over K ranges)
         raw = make_weights("Q6_K", 4096, 14336, 27)
         ws = _copies(torch.from_numpy(raw).cuda())
-        X = _x(29, (4, 14336))
-        for n in (1, 2, 3, 4):
+        X = _x(29, (8, 14336))
+        for n in (1, 2, 3, 4, 8):
             us, err = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup)
             extra = {}
-            if n > 1:
+            if 1 < n <= 4:
                 usg, _ = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup, {"MVLT_MAX": 1})
                 extra = {"us_without_few_token_kernel": round(usg, 3)}
+            elif n > 4:
+                usg, _ = _mv_case(L, stream, "Q6_K", ws, raw, 4096, 14336, X[:n], steps, warmup, {"MVD_LONG": 0})
+                extra = {"us_without_dense_kernel": round(usg, 3)}
             _record("speculative", f"Q6_K 4096x14336 n={n}", "Q6_K", us, alg_bytes("Q6_K", 4096, 14336, n), err, **extra)
         del ws
 
@@ -308,16 +312,19 @@ def run_configs(which, steps, warmup):
     if which in ("fewtoken", "all"):
         # 2..16 tokens of the other formats (speculative verification, small batches) on the dense-read
         # matrix-core kernel: 14336x4096 and 4096x4096, W ~N(0,0.02) (seed 81), x ~N(0,1) (seed 82); beside
-        # each, the launch plan without that kernel (the other matrix-core kernel or dot4)
-        for rows in (14336, 4096):
-            for fmt in ("Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS"):
-                raw = make_weights(fmt, rows, 4096, 81)
+        # each, the launch plan without that kernel (the other matrix-core kernel or dot4); then every
+        # format on rows of 14336 values (4096x14336, the down projection's shape: K ranges)
+        for rows, n_in, fmts in ((14336, 4096, ("Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS")),
+                                 (4096, 4096, ("Q4_0", "Q8_0", "Q6_K", "TQ2_0", "IQ2_XXS")),
+                                 (4096, 14336, ("Q4_K", "Q6_K", "Q4_0", "Q8_0", "TQ2_0", "IQ2_XXS"))):
+            for fmt in fmts:
+                raw = make_weights(fmt, rows, n_in, 81)
                 ws = _copies(torch.from_numpy(raw).cuda())
-                X = _x(82, (16, 4096))
+                X = _x(82, (16, n_in))
                 for n in (2, 4, 8, 16):
-                    us, err = _mv_case(L, stream, fmt, ws, raw, rows, 4096, X[:n], steps, warmup)
-                    uso, _ = _mv_case(L, stream, fmt, ws, raw, rows, 4096, X[:n], steps, warmup, {"MVD": 0})
-                    _record("fewtoken", f"{fmt} {rows}x4096 n={n}", fmt, us, alg_bytes(fmt, rows, 4096, n), err,
+                    us, err = _mv_case(L, stream, fmt, ws, raw, rows, n_in, X[:n], steps, warmup)
+                    uso, _ = _mv_case(L, stream, fmt, ws, raw, rows, n_in, X[:n], steps, warmup, {"MVD": 0})
+                    _record("fewtoken", f"{fmt} {rows}x{n_in} n={n}", fmt, us, alg_bytes(fmt, rows, n_in, n), err,
                             us_without_dense_kernel=round(uso, 3))
                 del ws
 

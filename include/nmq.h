@@ -118,7 +118,9 @@ int nmq_akt_q8(const float* g, const float* u, int gelu, float* a, int8_t* xq, i
 /*
  * y[c][r] = W[r,:] . x_c for c < ncols tokens (any ncols >= 1; launches of up to 2 * NMQ_MAX_COLS
  * tokens on the matrix cores, NMQ_MAX_COLS on the dot4 kernels; 9..16 tokens as two launches of up to 8
- * where the dense-read matrix-core kernel takes the shape).  2..4 tokens of Q4_K with rows of up
+ * where the dense-read matrix-core kernel takes the shape; rows beyond 4096 values that do not split
+ * into equal aligned K ranges: one launch per range, each adding to y in range order).  2..4 tokens of
+ * Q4_K with rows of up
  * to 4096 values, or of Q6_K with rows of 8K..16K values: every token's output equals the ncols = 1 call
  * on that token bit for bit.
  * w: n_out rows of n_in values in GGUF block format, rows back to back.  Token c's two-stage input

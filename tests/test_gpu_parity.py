@@ -335,7 +335,7 @@ def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt, shape):
 
 
 @pytest.mark.parametrize("fmt", FMTS)
-@pytest.mark.parametrize("shape", [(4096, 14336), (300, 8192), (130, 6144)])
+@pytest.mark.parametrize("shape", [(4096, 14336), (300, 8192), (130, 6144), (64, 28672)])
 @pytest.mark.parametrize("mode", [1, 2])
 def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape, mode):
     """2..8 tokens on rows beyond 4096 values on the dense-read kernel over equal K ranges: one launch

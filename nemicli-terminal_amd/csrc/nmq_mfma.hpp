@@ -788,10 +788,86 @@ struct Dma<NMQ_IQ2_XXS> {
     }
 };
 
-// LDS: input rows 2 nc x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
+// The long-row form (K ranges of 8 blocks) of TQ2_0 and IQ2_XXS: chunks of one 66-byte block; the window offset m = 2 b mod 16 is even, so the
+// block's fields sit 0 or 2 bytes off a dword (sh = m & 3) and are read as dwords and shifted.  PR = 5
+// pieces (m + 66 <= 80 bytes; the last block of a row has m = 14 and ends on the row's end).
 template <int F>
+struct Dma1;
+template <>
+struct Dma1<NMQ_TQ2_0> {
+    static constexpr int CHB = 1, PR = 5, SLOTS = 7;
+    using M = Mfma<NMQ_TQ2_0>;
+    struct Raw {
+        M::Raw r[1];
+    };
+    // codes at 0, d at 64
+    __device__ static void frag(Raw& o, const u8* row, int m, int kb) {
+        const u8* b = row + (m & 12);
+        const u32 sh = (u32)(m & 3);
+        o.r[0].q[0] = lds8_shifted(b + 8 * kb, sh);
+        o.r[0].q[1] = lds8_shifted(b + 32 + 8 * kb, sh);
+        o.r[0].d = lds32(b + 64) >> (8 * sh);
+    }
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, const u64* tab,
+                                float (&acc)[2]) {
+        Dma<NMQ_TQ2_0>::Raw r2;
+        r2.r[0] = o.r[i];
+        Dma<NMQ_TQ2_0>::block(r2, 0, ab, xb, kb, tab, acc);
+    }
+};
+
+template <>
+struct Dma1<NMQ_IQ2_XXS> {
+    static constexpr int CHB = 1, PR = 5, SLOTS = 7;
+    using M = Mfma<NMQ_IQ2_XXS>;
+    struct Raw {
+        M::Raw r[1];
+    };
+    // d at 0, sub-block s's {aux0, aux1} at 2 + 8 s: from the dword at or below the block's start (shift
+    // sh = 0 or 2) the pairs begin 2 + sh bytes in.  Every lane reads all of them.
+    __device__ static void frag(Raw& o, const u8* row, int m, int) {
+        const u8* b = row + (m & 12);
+        const u32 sh = (u32)(m & 3);
+        u32 w[18];
+#pragma unroll
+        for (int j = 0; j < 18; ++j) w[j] = lds32(b + 4 * j);
+        const int k = sh >> 1;          // first dword of the pairs
+        const u32 shp = 2u - sh;        // their byte shift within it
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+            o.r[0].a[s] = u32x2{__builtin_amdgcn_alignbyte(w[2 * s + k + 1], w[2 * s + k], shp),
+                                __builtin_amdgcn_alignbyte(w[2 * s + k + 2], w[2 * s + k + 1], shp)};
+        o.r[0].d = w[0] >> (8 * sh);
+    }
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, const u64* tab,
+                                float (&acc)[2]) {
+        Dma<NMQ_IQ2_XXS>::Raw r2;
+        r2.r[0] = o.r[i];
+        Dma<NMQ_IQ2_XXS>::block(r2, 0, ab, xb, kb, tab, acc);
+    }
+};
+
+// The chunk layout a kernel form uses: the long-row form of the 66-byte formats takes one block per chunk
+// (8-block ranges give twice the waves per workgroup; 4096x14336 at 8 tokens TQ2_0 15.3 -> 12.2 us,
+// IQ2_XXS 22.2 -> 17.3), the rows of up to 4096 values keep two (14336x4096 at 8 tokens: one block
+// 10.5 / 14.5 us against two 8.6 / 12.6).
+template <int F, bool KL>
+struct DmaSel {
+    using T = Dma<F>;
+};
+template <>
+struct DmaSel<NMQ_TQ2_0, true> {
+    using T = Dma1<NMQ_TQ2_0>;
+};
+template <>
+struct DmaSel<NMQ_IQ2_XXS, true> {
+    using T = Dma1<NMQ_IQ2_XXS>;
+};
+
+// LDS: input rows 2 nc x (n_in + 16), then (xd / 254, xs) [step][token] (64 S bytes), then W chunk buffers.
+template <int F, bool KL = false>
 __host__ __device__ constexpr size_t mvd_lds(int n_in, int W, int nc) {
-    return (size_t)2 * nc * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * Dma<F>::SLOTS;
+    return (size_t)2 * nc * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * DmaSel<F, KL>::T::SLOTS;
 }
 
 // KL: rows beyond the LDS's input capacity, as p.nr K ranges of p.rb blocks in one launch: each range's
@@ -799,7 +875,7 @@ __host__ __device__ constexpr size_t mvd_lds(int n_in, int W, int nc) {
 // through its chunk buffer, and the sums of all ranges add up in the wave's registers.
 template <int F, int NCH, bool KL = false>
 __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
-    using D = Dma<F>;
+    using D = typename DmaSel<F, KL>::T;
     constexpr int ROW = 16 * D::SLOTS;              // LDS bytes per row of a chunk buffer
     constexpr int NI = (16 * D::SLOTS + 63) / 64;   // chunk read instructions
     static_assert(16 * D::SLOTS - 64 * (NI - 1) == 48, "the last chunk read has 48 lanes");
@@ -970,7 +1046,7 @@ inline MvdShape plan_mvd(int n_out, int n_in, int nc, int cus, int lds_max, cons
 // or 2 chunks.
 template <int F>
 inline MvdShape plan_mvd_long(int n_out, int n_in, int nc, int cus, int lds_max, const void* w, int64_t row_bytes) {
-    constexpr int CHB = Dma<F>::CHB;
+    constexpr int CHB = DmaSel<F, true>::T::CHB;
     MvdShape s{};
     if (!tune(TUNE_MVD, 1) || nc < 2 || nc > 8 || n_in % 256 || n_in <= 4096 || n_in > 8 * 4096 ||
         (uintptr_t)w % 16 || row_bytes % 16)
@@ -998,7 +1074,7 @@ inline MvdShape plan_mvd_long(int n_out, int n_in, int nc, int cus, int lds_max,
     s.grid_x = (tiles + tpw - 1) / tpw;
     s.nr = nr;
     s.rb = rb;
-    s.lds = mvd_lds<F>(rb * 256, ks * tpw, nc);
+    s.lds = mvd_lds<F, true>(rb * 256, ks * tpw, nc);
     s.ok = s.lds + 4096 <= (size_t)lds_max;
     return s;
 }

@@ -579,10 +579,10 @@ struct Dma<NMQ_Q4_K> {
 // (4-byte aligned), and the two dwords that hold the d's (first block: low half of the pair's dword 0;
 // second block: high half of the dword at byte GB - 2).
 // Per step:  y += d * (xd / 254) * (254 S1 + S2)  (254 S1 + S2 exact in int32, rounded once to fp32).
-template <int F>
+template <int F, int CHB_ = F == NMQ_Q4_0 ? 2 : 1>
 struct DmaSmall {
     static constexpr int GB = F == NMQ_Q4_0 ? 18 : 34;  // bytes per GGUF block
-    static constexpr int CHB = F == NMQ_Q4_0 ? 2 : 1, PR = CHB * 8 * GB / 16, SLOTS = 19;
+    static constexpr int CHB = CHB_, PR = CHB * 8 * GB / 16, SLOTS = PR <= 9 ? 11 : 19;
     static constexpr int NP = CHB * 4;                  // block pairs per chunk
     struct Raw {
         u32x2 q[2 * NP];
@@ -793,6 +793,31 @@ struct Dma<NMQ_IQ2_XXS> {
 // pieces (m + 66 <= 80 bytes; the last block of a row has m = 14 and ends on the row's end).
 template <int F>
 struct Dma1;
+
+// The long-row form of Q4_K and Q4_0: chunks of one 144-byte block (9 pieces), so that ranges of 14 or
+// 16 blocks keep 14 or 16 waves per workgroup.
+template <>
+struct Dma1<NMQ_Q4_K> {
+    static constexpr int CHB = 1, PR = 9, SLOTS = 11;
+    using M = Mfma<NMQ_Q4_K>;
+    struct Raw {
+        M::Raw r[1];
+    };
+    __device__ static void frag(Raw& o, const u8* row, int, int kb) {
+        o.r[0].h = *(const u32x4*)row;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.r[0].q[i] = *(const u32x2*)(row + 16 + 32 * i + 8 * kb);
+    }
+    __device__ static void block(const Raw& o, int i, const u8* ab, const float2* xb, int kb, const u64* tab,
+                                float (&acc)[2]) {
+        Dma<NMQ_Q4_K>::Raw r2;
+        r2.r[0] = o.r[i];
+        Dma<NMQ_Q4_K>::block(r2, 0, ab, xb, kb, tab, acc);
+    }
+};
+template <>
+struct Dma1<NMQ_Q4_0> : DmaSmall<NMQ_Q4_0, 1> {};
+
 template <>
 struct Dma1<NMQ_TQ2_0> {
     static constexpr int CHB = 1, PR = 5, SLOTS = 7;
@@ -858,6 +883,14 @@ struct DmaSel {
 template <>
 struct DmaSel<NMQ_TQ2_0, true> {
     using T = Dma1<NMQ_TQ2_0>;
+};
+template <>
+struct DmaSel<NMQ_Q4_K, true> {
+    using T = Dma1<NMQ_Q4_K>;
+};
+template <>
+struct DmaSel<NMQ_Q4_0, true> {
+    using T = Dma1<NMQ_Q4_0>;
 };
 template <>
 struct DmaSel<NMQ_IQ2_XXS, true> {

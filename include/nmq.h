@@ -50,7 +50,7 @@ const char* nmq_strerror(int code);
  * the launch planner without or with the "NMQ_" prefix (MV1, MV1_MODE, MV1_HR, MV1_WPC, MV1_W,
  * MV1_RW, MV1_NBUF, MV1_MAXNIT, MVL, MVL_WPC, MVL_W, MVC_WGPC, MVC_RW, MVC_ROWS, MVT_MAX, MVT_WPC,
  * MVLT_MAX, MVM, MVM_TPW, MVM_KS, MMH_T, MMH_G, MVK, MVK_WPC, MVK_HR, MVK_NBUF, MVD, MVD_MIN, MVD_TPW,
- * MVD_KS, MVD_WGPC, MVD_LONG, MV1_T, MOE_GU_RW, MOE_GU_WGS, MVP_RPW, MVP_WGS); value
+ * MVD_KS, MVD_WGPC, MVD_LONG, MVD_UNEQ, MV1_T, MOE_GU_RW, MOE_GU_WGS, MVP_RPW, MVP_WGS); value
  * NMQ_TUNE_DEFAULT restores the measured default.
  * Process-wide, read by every later launch; the environment is never consulted.  NMQ_ERR_ARG for an
  * unknown name.  nmq_get_tuning writes the override or NMQ_TUNE_DEFAULT.

@@ -903,9 +903,10 @@ __host__ __device__ constexpr size_t mvd_lds(int n_in, int W, int nc) {
     return (size_t)2 * nc * (n_in + 16) + (size_t)2 * n_in + (size_t)W * 256 * DmaSel<F, KL>::T::SLOTS;
 }
 
-// KL: rows beyond the LDS's input capacity, as p.nr K ranges of p.rb blocks in one launch: each range's
-// input is staged after every wave is done with the previous one's, the wave's slice of each range runs
-// through its chunk buffer, and the sums of all ranges add up in the wave's registers.
+// KL: rows beyond the LDS's input capacity, as p.nr K ranges of p.rb blocks in one launch (the last one
+// the rest of the row, possibly shorter; a wave's slice of every range is 1 or 2 chunks, NCH the most):
+// each range's input is staged after every wave is done with the previous one's, the wave's slice of
+// each range runs through its chunk buffer, and the sums of all ranges add up in the wave's registers.
 template <int F, int NCH, bool KL = false>
 __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     using D = typename DmaSel<F, KL>::T;
@@ -923,7 +924,6 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     const int tile_in_wg = wave / p.ks, slice = wave % p.ks;
     const int row0 = (blockIdx.x * p.tpw + tile_in_wg) * 16;
     const int n = lane & 15, kb = lane >> 4;
-    const int b0 = slice * D::CHB * NCH;
     const int NR = 2 * p.nc;  // input rows in LDS
     float2* xsc = (float2*)(lds + NR * RS);
     u8* buf = lds + NR * RS + 2 * KV + wave * 16 * ROW;
@@ -934,6 +934,10 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     const int nr = KL ? p.nr : 1;
     for (int j = 0; j < nr; ++j) {
     const int k0 = j * KV, jb = j * (KV / 256);  // the range's first value and block
+    const int rbj = KL && j == nr - 1 ? p.nblk - jb : KV / 256;  // blocks of this range
+    const int KVj = rbj * 256, Sj = KVj / 32;
+    const int nchj = KL ? rbj / (p.ks * D::CHB) : NCH;  // chunks of the wave's slice
+    const int b0 = slice * D::CHB * nchj;
     if (KL && j > 0) lds_barrier();  // every wave done with the previous range's input
 
     // input rows: row r = xq (r even) or xq2 (r odd) of token r / 2, 1 KB per instruction, over the waves.
@@ -942,8 +946,8 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     for (int r = wave; r < NR; r += W) {
         const int t = r >> 1;
         const int8_t* row = ((r & 1) ? p.xq2 : p.xq) + (int64_t)t * p.x_stride + k0;
-        for (int m = 0; 1024 * m < KV; ++m)
-            if (1024 * m + 16 * lane < KV) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
+        for (int m = 0; 1024 * m < KVj; ++m)
+            if (1024 * m + 16 * lane < KVj) dma16s(row, (u32)(1024 * m + 16 * lane), lds + r * RS + 1024 * m);
     }
     // (xd, xs): piece i < 4 S = 4 consecutive steps (of S / 4 groups of 4) of token i & 7 of xd
     // (i / 8 < S / 4) or xs, read by hand.  Every thread issues both reads (threads past the pieces and
@@ -952,8 +956,8 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     u32x4 xv[2];
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
-        const bool ok = i < 4 * S && t < p.nc;
+        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= Sj / 4, m = g - a * (Sj / 4);
+        const bool ok = i < 4 * Sj && t < p.nc;
         xv[k] = gload16(ok ? (a ? p.xs : p.xd) + (int64_t)t * (p.x_stride / 32) + k0 / 32 + 4 * m : p.xd);
     }
     // the first chunk's reads only once every wave has issued its input reads: the CU returns reads in
@@ -968,8 +972,8 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
     if (j == 0) tab_store_hand<F>(tab, gv, nt);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
-        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= S / 4, m = g - a * (S / 4);
-        if (i < 4 * S) {
+        const int i = (int)threadIdx.x + k * nt, t = i & 7, g = i >> 3, a = g >= Sj / 4, m = g - a * (Sj / 4);
+        if (i < 4 * Sj) {
             const float v[4] = {__uint_as_float(xv[k].x), __uint_as_float(xv[k].y), __uint_as_float(xv[k].z),
                                 __uint_as_float(xv[k].w)};
 #pragma unroll
@@ -981,10 +985,11 @@ __global__ __launch_bounds__(1024) void mvd_kernel(MvmParams p) {
 
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
+        if (KL && c >= nchj) break;
         vm_wait<0>();  // chunk c in the buffer
         typename D::Raw r;
         D::frag(r, buf + n * ROW, (int)(((int64_t)(jb + b0 + D::CHB * c) * Mfma<F>::BB) & 15), kb);
-        if (c + 1 < NCH) {
+        if (c + 1 < nchj) {
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the operands read before the buffer is refilled
             mvd_chunk<F, NI>(buf, p, co, row0, jb + b0 + D::CHB * (c + 1), lane);
         }
@@ -1091,16 +1096,28 @@ inline MvdShape plan_mvd_long(int n_out, int n_in, int nc, int cus, int lds_max,
     int rb = 0;
     for (int c = std::min(16, nblk); c >= 8 && rb == 0; --c)
         if (nblk % c == 0 && c % CHB == 0 && (int64_t)c * Mfma<F>::BB % 16 == 0) rb = c;
+    // equal ranges below 12 blocks: ranges of 16 and a shorter last one instead, where the same slices
+    // fit both (14336 values: 16, 16, 16, 8 blocks for the 210- and 66-byte blocks instead of 7 x 8)
+    int last = rb;
+    if (rb < 12 && nblk > 16 && 16 * Mfma<F>::BB % 16 == 0 && tune(TUNE_MVD_UNEQ, 1) != 0) {
+        const int l = nblk % 16 == 0 ? 16 : nblk % 16;
+        if (l % CHB == 0) {
+            rb = 16;
+            last = l;
+        }
+    }
     if (rb == 0) return s;
-    const int nr = nblk / rb;
+    const int nr = (nblk + rb - 1) / rb;
     const int tiles = (n_out + 15) / 16;
     int tpw = tune(TUNE_MVD_TPW, 0);
     if (tpw <= 0) tpw = std::min((tiles + cus - 1) / cus, 8);
     int ks = tune(TUNE_MVD_KS, 0);
     if (ks <= 0)
         for (int k = 16 / tpw; k >= 1 && ks <= 0; --k)
-            if (rb % (k * CHB) == 0 && rb / (k * CHB) <= 2) ks = k;
-    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || rb % (ks * CHB) || rb / (ks * CHB) > 2) return s;
+            if (rb % (k * CHB) == 0 && rb / (k * CHB) <= 2 && last % (k * CHB) == 0) ks = k;
+    if (ks < 1 || tpw < 1 || ks * tpw > 16 || ks * tpw < 4 || rb % (ks * CHB) || rb / (ks * CHB) > 2 ||
+        last % (ks * CHB) || last / (ks * CHB) < 1)
+        return s;
     s.nch = rb / (ks * CHB);
     s.ks = ks;
     s.tpw = tpw;

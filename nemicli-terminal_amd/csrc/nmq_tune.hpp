@@ -50,6 +50,7 @@ enum Tune : int {
     TUNE_MVP_WGS,     // its workgroups (default: the fewest groups of 32 rows per workgroup, spread evenly)
     TUNE_MVD_WGPC,    // workgroups per CU the dense-read kernel's plan aims at (1 .. 4)
     TUNE_MVD_LONG,    // rows beyond 4096 values: 1 one dense launch over K ranges, 2 one launch per range, 0 neither
+    TUNE_MVD_UNEQ,    // 0: long rows only in equal K ranges (not 16-block ranges and a shorter last one)
     TUNE_COUNT
 };
 
@@ -59,7 +60,7 @@ inline const char* const kTuneNames[TUNE_COUNT] = {
     "MVL",      "MVL_WPC",    "MVL_W",   "MVC_WGPC", "MVC_RW",  "MVC_ROWS", "MVT_MAX", "MVT_WPC",
     "MVLT_MAX", "MVM",        "MVM_TPW", "MVM_KS",   "MMH_T",   "MMH_G",    "MVK",     "MVK_WPC",
     "MVD",      "MVD_MIN",    "MVD_TPW", "MVD_KS",   "MV1_T",    "MVK_HR",   "MVK_NBUF",
-    "MOE_GU_RW", "MOE_GU_WGS", "MVP_RPW", "MVP_WGS", "MVD_WGPC", "MVD_LONG"};
+    "MOE_GU_RW", "MOE_GU_WGS", "MVP_RPW", "MVP_WGS", "MVD_WGPC", "MVD_LONG", "MVD_UNEQ"};
 
 constexpr int TUNE_UNSET = INT_MIN;
 

@@ -336,16 +336,19 @@ def test_mv_9_to_16_tokens_dense_pairs(nmq, oracle, fmt, shape):
 
 @pytest.mark.parametrize("fmt", FMTS)
 @pytest.mark.parametrize("shape", [(4096, 14336), (300, 8192), (130, 6144), (64, 28672)])
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 def test_mv_tokens_long_rows_k_ranges(nmq, oracle, tune, fmt, shape, mode):
-    """2..8 tokens on rows beyond 4096 values on the dense-read kernel over equal K ranges: one launch
-    staging the ranges one after another (mode 1, the default), or one launch per range of 4096 values
-    (the last shorter), each adding its sums to y in range order (mode 2); against the oracle, and two
-    calls bit for bit equal.  Q6_K 2..4 tokens take the few-token long-row kernel by default, so the
+    """2..8 tokens on rows beyond 4096 values on the dense-read kernel over K ranges: one launch staging
+    the ranges one after another (mode 1, the default: equal ranges, or ranges of 16 blocks and a shorter
+    last one; mode 3: equal ranges only), or one launch per range of 4096 values (the last shorter),
+    each adding its sums to y in range order (mode 2); against the oracle, and two calls bit for bit
+    equal.  Q6_K 2..4 tokens take the few-token long-row kernel by default, so the
     ranges are forced on with that kernel off."""
     from ggufengine_amd.gguf_types import TYPE_ID
     n_out, n_in = shape
-    tune(MVD_LONG=mode)
+    tune(MVD_LONG=min(mode, 2))
+    if mode == 3:
+        tune(MVD_UNEQ=0)   # equal ranges only
     if fmt == "Q6_K":
         tune(MVLT_MAX=1)
     raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=79 + n_in % 89)

@@ -42,6 +42,33 @@ DISPATCH = [("Q4_K", 1, "mmvq.mv"), ("Q4_K", 8, "mmvq.mv"), ("Q4_K", 9, "mmvq.mm
             ("Q4_0", 3, "cudakern.mm"), ("Q4_0", 20, "unpack")]
 
 
+# long rows: (format, row length, tokens M, branch)
+DISPATCH_LONG = [("Q6_K", 14336, 6, "mmvq.mv"), ("Q6_K", 14336, 9, "mmvq.mm"), ("Q4_K", 14336, 8, "mmvq.mv"),
+                 ("Q4_K", 11008, 2, "mmvq.mm"), ("Q6_K", 11008, 4, "mmvq.mv"), ("Q6_K", 11008, 5, "mmvq.mm")]
+
+
+@pytest.mark.parametrize("fmt,n_in,M,branch", DISPATCH_LONG)
+def test_packed_linear_dispatch_long_rows(nmq, oracle, monkeypatch, fmt, n_in, M, branch):
+    """PackedLinear on rows beyond 4096 values: the mat-vec kernels up to mmvq.mv_bis tokens (8 where the
+    dense kernel splits the row into K ranges, otherwise 1 for Q4_K and 4 for Q6_K), the fp16 matrix
+    cores above; results against the oracle."""
+    from ggufengine_amd import mmvq, packed
+    from ggufengine_amd.gguf_types import TYPE_ID
+    n_out = 96
+    raw = random_blocks(fmt, n_out * n_in // BV[fmt], seed=93 + M)
+    x = np.random.default_rng(94 + M).standard_normal((M, n_in)).astype(np.float32)
+    taken = []
+    for name in ("mv", "mm"):
+        orig = getattr(mmvq, name)
+        monkeypatch.setattr(mmvq, name, lambda *a, _o=orig, _n=f"mmvq.{name}", **k: (taken.append(_n), _o(*a, **k))[1])
+    say("packed linear long rows", fmt, n_in, M, branch)
+    lin = packed.PackedLinear(dev(raw), TYPE_ID[fmt], n_out, n_in, dtype=torch.float32)
+    y = lin(dev(x)).cpu().numpy()
+    assert taken and set(taken) == {branch}, taken
+    err = oracle.rel_err_rows(y, oracle.mv_deq(fmt, raw, n_out, n_in, x))
+    assert err.max() <= 1e-3, (fmt, n_in, M, branch, float(err.max()))
+
+
 @pytest.mark.parametrize("fmt,M,branch", DISPATCH)
 def test_packed_linear_dispatch(nmq, oracle, monkeypatch, fmt, M, branch):
     from ggufengine_amd import cudakern, mmvq, packed
